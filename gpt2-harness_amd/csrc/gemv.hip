@@ -1,0 +1,290 @@
+// Decode GEMV on the vector ALUs (gfx950), for the reference's quantized
+// Linears at decode time (model.py:254,319,352,355 with T = 1, M = batch):
+//     y[m, n] = scale[n] * sum_k q[n, k] * x[m, k] + bias[n]
+//
+// The op is bound by the weight stream: N*K bytes of int8 (N*K/2 of int4)
+// per call against 2-4*M*K bytes of activations. Design:
+//   * a workgroup stages its MT activation rows in LDS once, as fp32 and in
+//     "planes" (float4 p of every 16-byte weight chunk stored contiguously
+//     over chunks), so lane l's reads of chunk l are consecutive 16-byte LDS
+//     words: no bank conflicts;
+//   * each wavefront owns R weight rows; lane l streams 16-byte chunks
+//     l, l+64, ... of each row (global_load_dwordx4, fully coalesced: a
+//     wavefront instruction covers 1 KB of one row);
+//   * the chunk is dequantized in registers (sign-extended bytes or biased
+//     nibbles -> fp32) once and reused for all MT activation rows;
+//   * per-row partial sums are reduced across the wavefront with xor
+//     shuffles; the per-channel scale and the bias are applied once per
+//     output; the group-wise format scales each 32-column chunk's partial sum
+//     by its group's fp16 scale.
+// No MFMA: at M <= 4 the int8->fp32 convert plus M FMAs per weight byte stay
+// within the VALU budget of the HBM stream.
+#include "tiq_internal.hpp"
+
+namespace tiq {
+namespace {
+
+constexpr int kWavesPerBlock = 8;
+
+template <int FMT>
+struct Fmt {
+    static constexpr int KC = (FMT == kW8) ? 16 : 32;  // columns per 16-byte chunk
+};
+
+template <typename TX>
+__device__ __forceinline__ float4 load_x4(const TX* p);
+
+template <>
+__device__ __forceinline__ float4 load_x4<float>(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+
+template <>
+__device__ __forceinline__ float4 load_x4<uint16_t>(const uint16_t* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
+
+template <typename TY>
+__device__ __forceinline__ void store_y(TY* p, float v);
+
+template <>
+__device__ __forceinline__ void store_y<float>(float* p, float v) {
+    *p = v;
+}
+
+template <>
+__device__ __forceinline__ void store_y<uint16_t>(uint16_t* p, float v) {
+    *p = f32_to_bf16_bits(v);
+}
+
+// sum over the 16 columns of an int8 chunk
+__device__ __forceinline__ float dot_w8(const uint4& w, const float4* xv) {
+    float s = 0.f;
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 xx = xv[j];
+        s = fmaf(sbyte_f32<0>(d[j]), xx.x, s);
+        s = fmaf(sbyte_f32<1>(d[j]), xx.y, s);
+        s = fmaf(sbyte_f32<2>(d[j]), xx.z, s);
+        s = fmaf(sbyte_f32<3>(d[j]), xx.w, s);
+    }
+    return s;
+}
+
+// sum over the 32 columns of a nibble chunk (low nibble = even column)
+__device__ __forceinline__ float dot_w4(const uint4& w, const float4* xv) {
+    float s = 0.f;
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 a = xv[2 * j], b = xv[2 * j + 1];
+        s = fmaf(nibble_f32<0>(d[j]), a.x, s);
+        s = fmaf(nibble_f32<1>(d[j]), a.y, s);
+        s = fmaf(nibble_f32<2>(d[j]), a.z, s);
+        s = fmaf(nibble_f32<3>(d[j]), a.w, s);
+        s = fmaf(nibble_f32<4>(d[j]), b.x, s);
+        s = fmaf(nibble_f32<5>(d[j]), b.y, s);
+        s = fmaf(nibble_f32<6>(d[j]), b.z, s);
+        s = fmaf(nibble_f32<7>(d[j]), b.w, s);
+    }
+    return s;
+}
+
+template <int MT, int R, int FMT, typename TX, typename TY>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
+    const TX* __restrict__ x, int64_t ldx, int M, const uint8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, const uint16_t* __restrict__ scale16, int group,
+    const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int N, int K) {
+    constexpr int KC = Fmt<FMT>::KC;
+    constexpr int P = KC / 4;  // float4 planes per chunk
+    extern __shared__ float4 xs[];
+    const int K4 = K >> 2;
+    const int NC = K / KC;
+    const int m0 = blockIdx.y * MT;
+
+    // stage MT activation rows as fp32 planes: xs[m][p][c]
+    for (int t = threadIdx.x; t < MT * K4; t += blockDim.x) {
+        const int m = t / K4, k4 = t - m * K4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m0 + m < M) v = load_x4<TX>(x + (int64_t)(m0 + m) * ldx + 4 * k4);
+        const int c = k4 / P, p = k4 - c * P;
+        xs[m * K4 + p * NC + c] = v;
+    }
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * kWavesPerBlock + wave) * R;
+    if (n0 >= N) return;  // wave-uniform, after the only barrier
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+
+    const uint8_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = w + (int64_t)((n0 + r < N) ? n0 + r : n0) * ldw;
+
+    // U chunks per row in flight per lane before the first use
+    constexpr int U = 4;
+    for (int c0 = lane; c0 < NC; c0 += 64 * U) {
+        uint4 wv[U][R];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                wv[u][r] = (c < NC) ? *reinterpret_cast<const uint4*>(wrow[r] + 16 * (int64_t)c) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + 64 * u;
+            if (c >= NC) break;
+            float gs[R];
+            if (FMT == kW4G) {
+                const int g = (c * KC) / group;
+                const int ng = (K + group - 1) / group;
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    gs[r] = f16_bits_to_f32(scale16[(int64_t)((n0 + r < N) ? n0 + r : n0) * ng + g]);
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float4 xv[P];
+#pragma unroll
+                for (int p = 0; p < P; ++p) xv[p] = xs[m * K4 + p * NC + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float part = (FMT == kW8) ? dot_w8(wv[u][r], xv) : dot_w4(wv[u][r], xv);
+                    if (FMT == kW4G) acc[r][m] = fmaf(gs[r], part, acc[r][m]);
+                    else acc[r][m] += part;
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = wave_sum(acc[r][m]);
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = n0 + r;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (lane == r * MT + m && n < N && m0 + m < M) {
+                float v = acc[r][m];
+                if (FMT != kW4G) v *= scale[n];
+                if (bias) v += bias[n];
+                store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
+            }
+        }
+    }
+}
+
+// Fallback for any shape or alignment: one wavefront per output (m, n),
+// scalar loads.
+template <int FMT, typename TX, typename TY>
+__global__ __launch_bounds__(256) void gemv_generic(const TX* __restrict__ x, int64_t ldx, int M,
+                                                    const uint8_t* __restrict__ w, int64_t ldw,
+                                                    const float* __restrict__ scale,
+                                                    const uint16_t* __restrict__ scale16, int group,
+                                                    const float* __restrict__ bias, TY* __restrict__ y,
+                                                    int64_t ldy, int N, int64_t K) {
+    const int lane = threadIdx.x & 63;
+    const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (o >= (int64_t)M * N) return;
+    const int m = (int)(o / N), n = (int)(o % N);
+    const uint8_t* wr = w + (int64_t)n * ldw;
+    const int64_t ng = (K + group - 1) / group;
+    float s = 0.f;
+    for (int64_t k = lane; k < K; k += 64) {
+        float xv;
+        if constexpr (sizeof(TX) == 4) xv = x[(int64_t)m * ldx + k];
+        else xv = bf16_bits_to_f32(x[(int64_t)m * ldx + k]);
+        float wv;
+        if (FMT == kW8) {
+            wv = (float)(int8_t)wr[k];
+        } else {
+            const uint8_t b = wr[k >> 1];
+            wv = (float)((int)((k & 1) ? (b >> 4) : (b & 0xf)) - 8);
+            if (FMT == kW4G) wv *= f16_bits_to_f32(scale16[(int64_t)n * ng + k / group]);
+        }
+        s = fmaf(wv, xv, s);
+    }
+    s = wave_sum(s);
+    if (lane == 0) {
+        if (FMT != kW4G) s *= scale[n];
+        if (bias) s += bias[n];
+        store_y<TY>(y + (int64_t)m * ldy + n, s);
+    }
+}
+
+constexpr size_t kMaxLds = 64 * 1024;
+
+template <int MT, int R, int FMT, typename TX, typename TY>
+int run_gemv(const LinearArgs& a) {
+    const int N = (int)a.N, K = (int)a.K, M = (int)a.M;
+    const size_t lds = (size_t)MT * K * sizeof(float);
+    const dim3 grid((unsigned)((N + kWavesPerBlock * R - 1) / (kWavesPerBlock * R)), (unsigned)((M + MT - 1) / MT));
+    hipLaunchKernelGGL((gemv_kernel<MT, R, FMT, TX, TY>), grid, dim3(kWavesPerBlock * 64), lds, a.stream,
+                       static_cast<const TX*>(a.x), a.ldx, M, a.w, a.ldw, a.scale, a.scale16, a.group, a.bias,
+                       static_cast<TY*>(a.y), a.ldy, N, K);
+    return launch_status();
+}
+
+template <int FMT, typename TX, typename TY>
+int run_generic(const LinearArgs& a) {
+    const int64_t outs = a.M * a.N;
+    hipLaunchKernelGGL((gemv_generic<FMT, TX, TY>), dim3((unsigned)((outs + 3) / 4)), dim3(256), 0, a.stream,
+                       static_cast<const TX*>(a.x), a.ldx, (int)a.M, a.w, a.ldw, a.scale, a.scale16, a.group,
+                       a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.N, a.K);
+    return launch_status();
+}
+
+template <int FMT, typename TX, typename TY>
+int dispatch_fmt(const LinearArgs& a) {
+    constexpr int KC = Fmt<FMT>::KC;
+    const size_t xb = (a.x_dtype == TIQ_F32) ? 16 : 8;
+    const bool vec = (a.K % KC == 0) && aligned(a.w, 16) && (a.ldw % 16 == 0) && aligned(a.x, xb) &&
+                     (a.ldx % 4 == 0) && (FMT != kW4G || a.group % KC == 0) && a.K * sizeof(float) <= kMaxLds &&
+                     a.N <= 0x7fffffff;
+    if (!vec) return run_generic<FMT, TX, TY>(a);
+    const size_t row_lds = (size_t)a.K * sizeof(float);
+    int mt = 4;
+    while (mt > 1 && (size_t)mt * row_lds > kMaxLds) mt >>= 1;
+    if (a.M < mt) mt = a.M >= 2 ? 2 : 1;
+    // two rows per wavefront once the grid has enough wavefronts to fill the chip
+    const bool r2 = a.N >= 2048;
+    switch (mt) {
+        case 4: return r2 ? run_gemv<4, 2, FMT, TX, TY>(a) : run_gemv<4, 1, FMT, TX, TY>(a);
+        case 2: return r2 ? run_gemv<2, 2, FMT, TX, TY>(a) : run_gemv<2, 1, FMT, TX, TY>(a);
+        default: return r2 ? run_gemv<1, 2, FMT, TX, TY>(a) : run_gemv<1, 1, FMT, TX, TY>(a);
+    }
+}
+
+template <int FMT>
+int dispatch_types(const LinearArgs& a) {
+    if (a.x_dtype == TIQ_F32) {
+        return a.y_dtype == TIQ_F32 ? dispatch_fmt<FMT, float, float>(a) : dispatch_fmt<FMT, float, uint16_t>(a);
+    }
+    return a.y_dtype == TIQ_F32 ? dispatch_fmt<FMT, uint16_t, float>(a) : dispatch_fmt<FMT, uint16_t, uint16_t>(a);
+}
+
+}  // namespace
+
+int launch_gemv(const LinearArgs& a) {
+    switch (a.fmt) {
+        case kW8: return dispatch_types<kW8>(a);
+        case kW4: return dispatch_types<kW4>(a);
+        case kW4G: return dispatch_types<kW4G>(a);
+    }
+    return TIQ_EINVAL;
+}
+
+}  // namespace tiq

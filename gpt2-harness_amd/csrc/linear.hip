@@ -1,0 +1,118 @@
+// Linear entry points of the C ABI: argument checks and the choice between
+// the decode GEMV (vector ALUs) and the prefill GEMM (matrix cores).
+#include "tiq_internal.hpp"
+
+namespace tiq {
+
+int check_linear(const LinearArgs& a) {
+    if (a.x_dtype != TIQ_F32 && a.x_dtype != TIQ_BF16) return TIQ_EINVAL;
+    if (a.y_dtype != TIQ_F32 && a.y_dtype != TIQ_BF16) return TIQ_EINVAL;
+    if (a.M < 0 || a.N < 0 || a.K < 0) return TIQ_EINVAL;
+    if (a.M == 0 || a.N == 0) return TIQ_OK;
+    if (a.K == 0) return TIQ_EINVAL;
+    if (!a.x || !a.w || !a.y) return TIQ_EINVAL;
+    if (a.fmt == kW4G ? !a.scale16 : !a.scale) return TIQ_EINVAL;
+    if (a.ldx < a.K || a.ldy < a.N) return TIQ_EINVAL;
+    if (a.M > 0x7fffffff || a.N > 0x7fffffff || a.K > 0x7fffffff) return TIQ_EUNSUPPORTED;
+    if (a.fmt == kW4 && (a.K % 2)) return TIQ_EINVAL;
+    if (a.fmt == kW4G && (a.group < 2 || (a.group & 1))) return TIQ_EINVAL;
+    return TIQ_OK;
+}
+
+namespace {
+
+// Rows of M at and above which the MFMA GEMM beats the vector-ALU GEMV.
+constexpr int64_t kGemmMinRows = 16;
+
+LinearArgs make_args(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w, int64_t ldw,
+                     const float* scale, const uint16_t* scale16, int group, const float* bias, int64_t N, void* y,
+                     int y_dtype, int64_t ldy, void* stream, WFormat fmt) {
+    LinearArgs a;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.M = M;
+    a.K = K;
+    a.ldx = ldx;
+    a.w = w;
+    a.ldw = ldw;
+    a.scale = scale;
+    a.scale16 = scale16;
+    a.group = group;
+    a.bias = bias;
+    a.N = N;
+    a.y = y;
+    a.y_dtype = y_dtype;
+    a.ldy = ldy;
+    a.stream = as_stream(stream);
+    a.fmt = fmt;
+    return a;
+}
+
+int run_linear(const LinearArgs& a) {
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || a.M == 0 || a.N == 0) return rc;
+    if (a.M >= kGemmMinRows && gemm_supported(a)) return launch_gemm(a);
+    return launch_gemv(a);
+}
+
+}  // namespace
+}  // namespace tiq
+
+using namespace tiq;
+
+extern "C" int tiq_version(void) { return 100; }
+
+extern "C" const char* tiq_status_string(int status) {
+    switch (status) {
+        case TIQ_OK: return "ok";
+        case TIQ_EINVAL: return "invalid argument";
+        case TIQ_EBITS: return "bits must be in [2, 8]";
+        case TIQ_EALIGN: return "misaligned pointer or leading dimension";
+        case TIQ_EUNSUPPORTED: return "unsupported shape or layout";
+        case TIQ_EWORKSPACE: return "workspace too small";
+        default: break;
+    }
+    if (status <= TIQ_EHIP_BASE) return hipGetErrorString((hipError_t)(TIQ_EHIP_BASE - status));
+    return "unknown status";
+}
+
+extern "C" int tiq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,
+                             const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                             void* stream) {
+    return run_linear(make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0,
+                                bias, N, y, y_dtype, ldy, stream, kW8));
+}
+
+extern "C" int tiq_gemv_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,
+                           const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                           void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0, bias,
+                             N, y, y_dtype, ldy, stream, kW8);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    return launch_gemv(a);
+}
+
+extern "C" int tiq_gemm_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,
+                           const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                           void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0, bias,
+                             N, y, y_dtype, ldy, stream, kW8);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    return launch_gemm(a);
+}
+
+extern "C" int tiq_linear_w4(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                             const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                             void* stream) {
+    return run_linear(make_args(x, x_dtype, M, K, ldx, packed, K / 2, scale, nullptr, 0, bias, N, y, y_dtype, ldy,
+                                stream, kW4));
+}
+
+extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                              const uint16_t* scale_f16, int group, const float* bias, int64_t N, void* y,
+                              int y_dtype, int64_t ldy, void* stream) {
+    return run_linear(make_args(x, x_dtype, M, K, ldx, packed, (K + 1) / 2, nullptr, scale_f16, group, bias, N, y,
+                                y_dtype, ldy, stream, kW4G));
+}

@@ -1,0 +1,104 @@
+// Shared device helpers and host-side launch plumbing for libtiq_hip.so.
+// CDNA4 (gfx950) only: 64-lane wavefronts, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "tiq.h"
+
+namespace tiq {
+
+constexpr int kWave = 64;
+
+inline int status_of(hipError_t e) { return e == hipSuccess ? TIQ_OK : TIQ_EHIP_BASE - (int)e; }
+
+// Status of the most recent launch on this thread.
+inline int launch_status() { return status_of(hipGetLastError()); }
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------ device helpers
+
+// |x| as raw bits. For non-negative floats integer order is float order and
+// every NaN sorts above +inf, so an unsigned max propagates NaN like torch.amax.
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        uint32_t o = __shfl_xor(v, off, kWave);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Max over aligned groups of `width` lanes (width a power of two <= 64).
+template <int Width>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = Width / 2; off >= 1; off >>= 1) {
+        uint32_t o = __shfl_xor(v, off, kWave);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// (amax / qmax).clamp(min=FLT_MIN) with the IEEE correctly rounded division
+// (hipcc keeps fp32 division correctly rounded unless told otherwise; this
+// library is never built with fast-math). NaN passes through the clamp.
+__device__ __forceinline__ float scale_from_amax(float amax, float qmax) {
+    float s = amax / qmax;
+    return (s < 1.17549435e-38f) ? 1.17549435e-38f : s;
+}
+
+// clamp(rint_half_even(w / s), qmin, qmax) as an int.
+__device__ __forceinline__ int code_of(float w, float s, float qmin, float qmax) {
+    float r = __builtin_rintf(w / s);
+    r = r < qmin ? qmin : r;
+    r = r > qmax ? qmax : r;
+    return (int)r;
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> fp16 bits, round to nearest even (hardware conversion).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Sign-extended byte `i` of a dword, as float.
+template <int I>
+__device__ __forceinline__ float sbyte_f32(uint32_t d) {
+    return (float)((int32_t)(d << (24 - 8 * I)) >> 24);
+}
+
+// Nibble `i` (0..7) of a dword minus the +8 bias, as float.
+template <int I>
+__device__ __forceinline__ float nibble_f32(uint32_t d) {
+    return (float)((int32_t)((d >> (4 * I)) & 0xfu) - 8);
+}
+
+}  // namespace tiq

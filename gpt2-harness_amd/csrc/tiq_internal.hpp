@@ -1,0 +1,41 @@
+// Internal launch interfaces shared by the linear entry points.
+#pragma once
+
+#include "tiq_common.hpp"
+
+namespace tiq {
+
+// Weight storage formats of a quantized Linear (rows = N outputs, cols = K inputs).
+enum WFormat : int {
+    kW8 = 0,   // int8 codes, row n at byte n * ldw
+    kW4 = 1,   // reference nibble layout, row n at byte n * K / 2 (K even)
+    kW4G = 2,  // group-wise nibbles, row n at byte n * ((K + 1) / 2), fp16 group scales
+};
+
+struct LinearArgs {
+    const void* x;
+    int x_dtype;
+    int64_t M, K, ldx;
+    const uint8_t* w;
+    int64_t ldw;             // bytes between weight rows
+    const float* scale;      // per-row fp32 (kW8, kW4)
+    const uint16_t* scale16; // per-group fp16 bits (kW4G)
+    int group;
+    const float* bias;
+    int64_t N;
+    void* y;
+    int y_dtype;
+    int64_t ldy;
+    hipStream_t stream;
+    WFormat fmt;
+};
+
+// Validates the common arguments; TIQ_OK when they are consistent.
+int check_linear(const LinearArgs& a);
+
+int launch_gemv(const LinearArgs& a);
+int launch_gemm(const LinearArgs& a);
+// True when the MFMA GEMM has a kernel for these arguments.
+bool gemm_supported(const LinearArgs& a);
+
+}  // namespace tiq

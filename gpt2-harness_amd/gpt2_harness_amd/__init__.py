@@ -1,0 +1,47 @@
+"""gpt2_harness_amd -- MI355X-native quantized inference for GPT-2.
+
+The quantize-and-run API of gpt2-harness (``quantize_tensor``, ``pack_int4``,
+``quantize_model``, ``generate`` ...) backed by hand-written HIP kernels for
+gfx950 in ``libtiq_hip.so`` (C ABI in ``include/tiq.h``). Importing the
+package does not touch the GPU; the first kernel call loads the library and
+raises if it is missing or no ROCm GPU is visible.
+"""
+
+from .config import GPT2_SIZES, GPTConfig, gpt2_config
+from .model import GPT, KVCache
+from .qlinear import QuantLinear
+from .quantization import (
+    TARGET_SUFFIXES,
+    QuantResult,
+    pack_int4,
+    packed_size_bytes,
+    perplexity_with_error_bars,
+    quantize_dequantize,
+    quantize_groupwise_int4,
+    quantize_linear,
+    quantize_model,
+    quantize_tensor,
+    unpack_int4,
+)
+from .sampling import generate
+
+__all__ = [
+    "GPT",
+    "GPT2_SIZES",
+    "GPTConfig",
+    "KVCache",
+    "QuantLinear",
+    "QuantResult",
+    "TARGET_SUFFIXES",
+    "generate",
+    "gpt2_config",
+    "pack_int4",
+    "packed_size_bytes",
+    "perplexity_with_error_bars",
+    "quantize_dequantize",
+    "quantize_groupwise_int4",
+    "quantize_linear",
+    "quantize_model",
+    "quantize_tensor",
+    "unpack_int4",
+]

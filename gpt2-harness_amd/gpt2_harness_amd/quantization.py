@@ -1,0 +1,387 @@
+"""Post-training weight quantization on the MI355X, behind the reference's API.
+
+Same public names, argument meaning and error messages as the reference's
+``src/transformer_internals/quantization.py`` (``:55-65``):
+
+* :func:`quantize_tensor`     (``:78-116``)  -- HIP kernel, bit-identical codes
+  and scales;
+* :func:`quantize_dequantize` (``:119-129``);
+* :func:`pack_int4` / :func:`unpack_int4` (``:132-158``) -- HIP kernels, the
+  reference's byte layout;
+* :func:`quantize_model`      (``:161-216``) -- returns a copy whose target
+  Linears are :class:`~gpt2_harness_amd.qlinear.QuantLinear` modules holding
+  the codes (int8, or nibble-packed for <= 4 bits), so the forward pass reads
+  1 (or 0.5) byte per weight instead of the 4 bytes of the reference's
+  simulated fp32 ``W_hat``; the stats dict has the reference's keys;
+* :func:`packed_size_bytes`   (``:219-259``) -- same payload schema;
+* :func:`perplexity_with_error_bars` (``:262-319``) and :class:`QuantResult`.
+
+Everything runs on the GPU: tensors must live on a ROCm device, and the
+functions raise when the HIP library is missing. Group-wise int4 with fp16
+scales (``group_size=``) is an extension with no counterpart in the reference.
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+import statistics
+import tempfile
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Any, Literal
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .qlinear import FMT_W4, FMT_W4G, FMT_W8, QuantLinear
+
+__all__ = [
+    "TARGET_SUFFIXES",
+    "QuantResult",
+    "pack_int4",
+    "packed_size_bytes",
+    "perplexity_with_error_bars",
+    "quantize_dequantize",
+    "quantize_groupwise_int4",
+    "quantize_linear",
+    "quantize_model",
+    "quantize_tensor",
+    "unpack_int4",
+]
+
+Granularity = Literal["per_tensor", "per_channel"]
+
+#: Module-name suffixes of the Linears that get quantized (``quantization.py:75``).
+TARGET_SUFFIXES = ("attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj")
+
+
+def _check_bits_granularity(bits: int, granularity: str) -> None:
+    if bits < 2 or bits > 8:
+        raise ValueError(f"bits must be in [2, 8], got {bits}")
+    if granularity not in ("per_channel", "per_tensor"):
+        raise ValueError(f"unknown granularity {granularity!r}")
+
+
+def _fp32_on_gpu(w: torch.Tensor, name: str = "w") -> torch.Tensor:
+    _lib.require_gpu(w, name)
+    if w.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 (the reference quantizes w.float()), got {w.dtype}")
+    return w.contiguous()
+
+
+def quantize_tensor(
+    w: torch.Tensor, bits: int, granularity: Granularity = "per_channel"
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric linear quantization of a weight matrix (one HIP kernel pass).
+
+    Args:
+        w: ``(out_features, in_features)`` fp32 weight on the GPU (any shape for
+            ``per_tensor``).
+        bits: Bit width in ``[2, 8]``.
+        granularity: ``per_channel`` (one scale per row) or ``per_tensor``.
+
+    Returns:
+        ``(q, scale)``: int8 codes in ``[-2^(b-1), 2^(b-1)-1]`` shaped like ``w``
+        and an fp32 scale of shape ``(rows, 1)`` or ``()``, bit-identical to the
+        reference's ``quantize_tensor``.
+    """
+    _check_bits_granularity(bits, granularity)
+    w = _fp32_on_gpu(w)
+    L = _lib.lib()
+    st = _lib.stream_of(w)
+    q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
+    if granularity == "per_channel":
+        if w.dim() != 2:
+            raise ValueError(f"per_channel quantization expects a 2-D weight, got shape {tuple(w.shape)}")
+        rows, cols = w.shape
+        scale = torch.empty((rows, 1), dtype=torch.float32, device=w.device)
+        if rows and cols:
+            rc = L.tiq_quantize_per_channel(w.data_ptr(), rows, cols, cols, bits, q.data_ptr(), cols,
+                                            scale.data_ptr(), st)
+            _lib.check(rc, "quantize_tensor(per_channel)")
+        return q, scale
+    scale = torch.empty((), dtype=torch.float32, device=w.device)
+    n = w.numel()
+    if n == 0:
+        raise RuntimeError("amax(): cannot reduce over an empty tensor")
+    ws = torch.empty(int(L.tiq_quantize_per_tensor_workspace(n)), dtype=torch.uint8, device=w.device)
+    rc = L.tiq_quantize_per_tensor(w.data_ptr(), n, bits, q.data_ptr(), scale.data_ptr(), ws.data_ptr(),
+                                   ws.numel(), st)
+    _lib.check(rc, "quantize_tensor(per_tensor)")
+    return q, scale
+
+
+def quantize_dequantize(
+    w: torch.Tensor, bits: int, granularity: Granularity = "per_channel"
+) -> torch.Tensor:
+    """Round-trip through quantization; returns ``q.float() * scale``."""
+    q, scale = quantize_tensor(w, bits, granularity)
+    rows = q.shape[0] if q.dim() == 2 else 1
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    if q.numel():
+        rc = _lib.lib().tiq_dequantize_int8(q.data_ptr(), scale.data_ptr(), int(granularity == "per_channel"),
+                                            rows, q.numel() // rows, out.data_ptr(), _lib.stream_of(q))
+        _lib.check(rc, "dequantize")
+    return out.to(w.dtype)
+
+
+def pack_int4(q: torch.Tensor) -> torch.Tensor:
+    """Pack int4 codes two per byte (low nibble = even index, +8 bias)."""
+    _lib.require_gpu(q, "q")
+    flat = q.reshape(-1)
+    if flat.dtype != torch.int8:
+        flat = flat.to(torch.int8)
+    flat = flat.contiguous()
+    out = torch.empty((flat.numel() + 1) // 2, dtype=torch.uint8, device=q.device)
+    rc = _lib.lib().tiq_pack_int4(flat.data_ptr(), flat.numel(), out.data_ptr(), _lib.stream_of(q))
+    _lib.check(rc, "pack_int4")
+    return out
+
+
+def unpack_int4(packed: torch.Tensor, numel: int) -> torch.Tensor:
+    """Inverse of :func:`pack_int4`."""
+    _lib.require_gpu(packed, "packed")
+    if numel > 2 * packed.numel():
+        raise ValueError(f"numel={numel} exceeds the {2 * packed.numel()} codes held by packed")
+    p = packed.reshape(-1).contiguous()
+    out = torch.empty(numel, dtype=torch.int8, device=packed.device)
+    rc = _lib.lib().tiq_unpack_int4(p.data_ptr(), numel, out.data_ptr(), _lib.stream_of(packed))
+    _lib.check(rc, "unpack_int4")
+    return out
+
+
+def quantize_groupwise_int4(w: torch.Tensor, group_size: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """Group-wise int4 codes with fp16 scales (no counterpart in the reference).
+
+    Groups are ``group_size`` consecutive columns of a row (the last one
+    ragged); ``scale = fp16(amax / 7)`` (0 -> smallest positive fp16, overflow
+    -> 65504); codes ``clamp(rint(w / scale), -8, 7)`` packed per row, low
+    nibble = even column, +8 bias.
+
+    Returns ``(packed uint8 (rows, ceil(cols/2)), scale fp16 (rows, ceil(cols/group)))``.
+    """
+    w = _fp32_on_gpu(w)
+    if w.dim() != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(w.shape)}")
+    if group_size < 2 or group_size % 2:
+        raise ValueError(f"group_size must be even and >= 2, got {group_size}")
+    rows, cols = w.shape
+    packed = torch.empty((rows, (cols + 1) // 2), dtype=torch.uint8, device=w.device)
+    scale = torch.empty((rows, -(-cols // group_size)), dtype=torch.float16, device=w.device)
+    if rows and cols:
+        rc = _lib.lib().tiq_quantize_groupwise_int4(w.data_ptr(), rows, cols, group_size, packed.data_ptr(),
+                                                    scale.data_ptr(), _lib.stream_of(w))
+        _lib.check(rc, "quantize_groupwise_int4")
+    return packed, scale
+
+
+def quantize_linear(
+    linear: nn.Linear, bits: int, granularity: Granularity = "per_channel", group_size: int | None = None
+) -> tuple[QuantLinear, tuple[torch.Tensor, torch.Tensor]]:
+    """Build the :class:`QuantLinear` replacing ``linear``.
+
+    Returns ``(module, (q, scale))`` where ``(q, scale)`` are the reference's
+    ``quantize_tensor`` outputs (kept for :func:`packed_size_bytes`); for the
+    group-wise format they are the packed nibbles and the fp16 scales.
+    """
+    _check_bits_granularity(bits, granularity)
+    w = linear.weight.detach().float()
+    N, K = w.shape
+    bias = None if linear.bias is None else linear.bias.detach()
+    if group_size is not None:
+        if bits != 4:
+            raise ValueError(f"group-wise quantization is int4 only, got bits={bits}")
+        packed, s16 = quantize_groupwise_int4(w, group_size)
+        mod = QuantLinear(packed, s16, bias, K, N, bits, f"group{group_size}", FMT_W4G, group_size)
+        return mod, (packed, s16)
+    q, scale = quantize_tensor(w, bits, granularity)
+    row_scale = scale.reshape(-1).expand(N).contiguous() if granularity == "per_tensor" else scale.reshape(N)
+    if bits <= 4 and K % 2 == 0:
+        mod = QuantLinear(pack_int4(q), row_scale, bias, K, N, bits, granularity, FMT_W4)
+    else:
+        mod = QuantLinear(q, row_scale, bias, K, N, bits, granularity, FMT_W8)
+    return mod, (q, scale)
+
+
+def _set_submodule(root: nn.Module, name: str, new: nn.Module) -> None:
+    parent_name, _, leaf = name.rpartition(".")
+    parent = root.get_submodule(parent_name) if parent_name else root
+    setattr(parent, leaf, new)
+
+
+def quantize_model(
+    model: nn.Module,
+    bits: int,
+    granularity: Granularity = "per_channel",
+    include_embedding: bool = False,
+    group_size: int | None = None,
+) -> tuple[nn.Module, dict[str, Any]]:
+    """Return a copy of the model with its target Linears quantized.
+
+    Args:
+        model: Source model on the GPU. Not modified.
+        bits: Bit width in ``[2, 8]``.
+        granularity: ``per_channel`` or ``per_tensor``.
+        include_embedding: Also quantize ``wte`` (and so the tied ``lm_head``):
+            its ``W_hat`` is written back in fp32 as the reference does.
+        group_size: Extension: group-wise int4 with fp16 scales for the
+            target Linears (``bits`` must be 4).
+
+    Returns:
+        ``(quantized_model, stats)`` with the reference's stats keys.
+    """
+    _check_bits_granularity(bits, granularity)
+    for p in model.parameters():
+        _lib.require_gpu(p, "model parameters")
+        break
+    q_model = copy.deepcopy(model)
+    quantized: list[str] = []
+    n_quant_params = 0
+    codes: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
+
+    targets = []
+    for name, module in q_model.named_modules():
+        is_target = name.endswith(TARGET_SUFFIXES)
+        is_emb = include_embedding and name == "wte"
+        if not (is_target or is_emb) or not isinstance(module, (nn.Linear, nn.Embedding)):
+            continue
+        targets.append((name, module))
+
+    with torch.no_grad():
+        for name, module in targets:
+            w = module.weight.data
+            if isinstance(module, nn.Linear):
+                new, code = quantize_linear(module, bits, granularity, group_size)
+                _set_submodule(q_model, name, new)
+            else:
+                q, scale = quantize_tensor(w.float(), bits, granularity)
+                code = (q, scale)
+                module.weight.data = quantize_dequantize(w.float(), bits, granularity).to(w.dtype)
+            codes[name] = code
+            quantized.append(name)
+            n_quant_params += w.numel()
+
+    total_params = sum(p.numel() for p in {id(p): p for p in model.parameters()}.values())
+    stats = {
+        "bits": bits,
+        "granularity": granularity,
+        "include_embedding": include_embedding,
+        "n_quantized_tensors": len(quantized),
+        "n_quantized_params": n_quant_params,
+        "n_total_params": total_params,
+        "fraction_quantized": n_quant_params / total_params,
+        "packed_bytes": packed_size_bytes(q_model, codes, bits, group_size=group_size),
+        "fp32_bytes": total_params * 4,
+    }
+    stats["compression_ratio"] = stats["fp32_bytes"] / stats["packed_bytes"]
+    if group_size is not None:
+        stats["group_size"] = group_size
+    return q_model, stats
+
+
+def packed_size_bytes(
+    model: nn.Module,
+    codes: dict[str, tuple[torch.Tensor, torch.Tensor]],
+    bits: int,
+    group_size: int | None = None,
+) -> int:
+    """Serialise a packed checkpoint (reference payload schema) and return its size.
+
+    Keys: ``name.q`` (int8 codes, or ``pack_int4`` bytes at 4 bits),
+    ``name.scale`` (fp32; fp16 for the group-wise format), ``name.shape``
+    (int32), plus every other unique parameter in fp32.
+    """
+    payload: dict[str, torch.Tensor] = {}
+    for name, (q, scale) in codes.items():
+        if group_size is not None and q.dtype == torch.uint8:
+            payload[f"{name}.q"] = q.cpu()
+            payload[f"{name}.scale"] = scale.cpu()
+            payload[f"{name}.shape"] = torch.tensor([q.shape[0], 0], dtype=torch.int32)
+            continue
+        payload[f"{name}.q"] = (pack_int4(q) if bits == 4 else q).cpu()
+        payload[f"{name}.scale"] = scale.to(torch.float32).cpu()
+        payload[f"{name}.shape"] = torch.tensor(list(q.shape), dtype=torch.int32)
+
+    quantized_weight_names = {f"{n}.weight" for n in codes}
+    seen: set[int] = set()
+    for name, p in model.named_parameters():
+        if name in quantized_weight_names or id(p) in seen:
+            continue
+        seen.add(id(p))
+        payload[name] = p.detach().to(torch.float32).cpu()
+
+    with tempfile.NamedTemporaryFile(suffix=".pt", delete=False) as fh:
+        tmp = Path(fh.name)
+    try:
+        torch.save(payload, tmp)
+        return tmp.stat().st_size
+    finally:
+        tmp.unlink(missing_ok=True)
+
+
+@torch.no_grad()
+def perplexity_with_error_bars(
+    model: nn.Module,
+    dataset: Any,
+    n_chunks: int = 8,
+    batches_per_chunk: int = 2,
+    batch_size: int = 4,
+    device: str | torch.device = "cuda",
+) -> dict[str, Any]:
+    """Held-out perplexity with a spread over disjoint chunks (``quantization.py:262-319``).
+
+    ``dataset`` is anything with ``sequential_batches(split, batch_size=, limit=)``
+    returning ``(x, y)`` id tensors, as the reference's ``TokenDataset``.
+    """
+    model = model.to(device).eval()
+    batches = dataset.sequential_batches("val", batch_size=batch_size, limit=n_chunks * batches_per_chunk)
+    chunk_losses: list[float] = []
+    for c in range(0, len(batches), batches_per_chunk):
+        group = batches[c : c + batches_per_chunk]
+        if not group:
+            continue
+        total, n = 0.0, 0
+        for x, y in group:
+            logits = model(x.to(device))["logits"].float().cpu()
+            total += F.cross_entropy(logits.reshape(-1, logits.size(-1)), y.reshape(-1), reduction="sum").item()
+            n += y.numel()
+        chunk_losses.append(total / n)
+    mean = statistics.fmean(chunk_losses)
+    std = statistics.stdev(chunk_losses) if len(chunk_losses) > 1 else 0.0
+    ppls = [math.exp(v) for v in chunk_losses]
+    return {
+        "loss_mean": mean,
+        "loss_std": std,
+        "ppl_mean": statistics.fmean(ppls),
+        "ppl_std": statistics.stdev(ppls) if len(ppls) > 1 else 0.0,
+        "ppl_of_mean_loss": math.exp(mean),
+        "n_chunks": len(chunk_losses),
+        "chunk_losses": chunk_losses,
+    }
+
+
+@dataclass
+class QuantResult:
+    """One row of the quantization table (``quantization.py:322-343``)."""
+
+    label: str
+    bits: int
+    granularity: str
+    include_embedding: bool
+    stats: dict[str, Any]
+    quality: dict[str, Any]
+    speed: dict[str, Any]
+
+    def to_dict(self) -> dict[str, Any]:
+        return {
+            "label": self.label,
+            "bits": self.bits,
+            "granularity": self.granularity,
+            "include_embedding": self.include_embedding,
+            **self.stats,
+            "quality": self.quality,
+            "speed": self.speed,
+        }

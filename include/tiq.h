@@ -1,0 +1,150 @@
+/*
+ * tiq.h -- C ABI of libtiq_hip.so, the MI355X (gfx950) quantized-linear
+ * library behind gpt2_harness_amd's quantize-and-run API.
+ *
+ * Conventions shared by every entry point:
+ *   - all pointers are device pointers (hipMalloc / torch CUDA tensors) unless
+ *     a comment says otherwise; matrices are row-major with an explicit
+ *     leading dimension in elements;
+ *   - a weight matrix is (rows = N = out_features, cols = K = in_features),
+ *     the nn.Linear layout of the reference (model.py:201-204,333-334);
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream);
+ *     every call only enqueues work on it and returns;
+ *   - no entry point allocates device or host memory, keeps state between
+ *     calls, or synchronises; calls on different streams are independent;
+ *   - the return value is TIQ_OK (0) or a negative status; tiq_status_string
+ *     names it. TIQ_EHIP_BASE - s means hipError_t s from the launch.
+ *
+ * Reference interfaces each entry point replaces are cited as
+ * file:line under /src/transformer_internals of gpt2-harness.
+ */
+#ifndef TIQ_H
+#define TIQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum tiq_status {
+    TIQ_OK = 0,
+    TIQ_EINVAL = -1,        /* bad size, null pointer, out-of-range argument   */
+    TIQ_EBITS = -2,         /* bits outside [2, 8] (quantization.py:98-99)       */
+    TIQ_EALIGN = -3,        /* pointer or leading dimension misaligned          */
+    TIQ_EUNSUPPORTED = -4,  /* valid request this build has no kernel for       */
+    TIQ_EWORKSPACE = -5,    /* workspace too small                              */
+    TIQ_EHIP_BASE = -1000   /* TIQ_EHIP_BASE - hipError_t                        */
+};
+
+enum tiq_dtype { TIQ_F32 = 0, TIQ_BF16 = 1 };
+
+/* Library version (major*10000 + minor*100 + patch). */
+int tiq_version(void);
+/* Static string naming a status code (never NULL). */
+const char* tiq_status_string(int status);
+
+/* ------------------------------------------------------------ quantize */
+
+/* quantize_tensor(w, bits, "per_channel")  -- quantization.py:78-116.
+ * w (rows, cols) fp32 with leading dim ldw; q (rows, cols) int8 codes with
+ * leading dim ldq; scale (rows) fp32. Codes and scales are bit-identical to the
+ * reference: scale = max(amax_row / qmax, FLT_MIN) with IEEE division,
+ * q = clamp(rint_half_even(w / scale), qmin, qmax). */
+int tiq_quantize_per_channel(const float* w, int64_t rows, int64_t cols, int64_t ldw, int bits,
+                             int8_t* q, int64_t ldq, float* scale, void* stream);
+
+/* Workspace bytes tiq_quantize_per_tensor needs for `numel` elements. */
+size_t tiq_quantize_per_tensor_workspace(int64_t numel);
+
+/* quantize_tensor(w, bits, "per_tensor")  -- quantization.py:78-116, with the
+ * single scale written to scale[0]. w and q are contiguous, numel elements. */
+int tiq_quantize_per_tensor(const float* w, int64_t numel, int bits, int8_t* q, float* scale,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* pack_int4(q)  -- quantization.py:132-149. q: numel int8 codes in [-8, 7];
+ * packed: (numel + 1) / 2 bytes, byte j = ((q[2j+1]+8) << 4) | (q[2j]+8), the
+ * high nibble of the last byte 0 when numel is odd. */
+int tiq_pack_int4(const int8_t* q, int64_t numel, uint8_t* packed, void* stream);
+
+/* unpack_int4(packed, numel)  -- quantization.py:152-158. */
+int tiq_unpack_int4(const uint8_t* packed, int64_t numel, int8_t* q, void* stream);
+
+/* pack_int4(quantize_tensor(w, bits, "per_channel")[0]) in one pass, for
+ * bits in [2, 4] and an even number of contiguous columns: packed is the
+ * reference's flattened row-major nibble layout, rows * cols / 2 bytes, so row
+ * r starts at byte r * cols / 2. Odd `cols` returns TIQ_EUNSUPPORTED (use
+ * tiq_quantize_per_channel + tiq_pack_int4). */
+int tiq_quantize_per_channel_int4_packed(const float* w, int64_t rows, int64_t cols, int bits,
+                                         uint8_t* packed, float* scale, void* stream);
+
+/* Group-wise int4 with fp16 scales. No counterpart in the reference (its
+ * int4 scales are per row or per tensor); the format is this library's own:
+ * groups of `group` consecutive columns (even, >= 2; the last group ragged),
+ * scale = fp16_rne(amax_group / 7) with 0 replaced by the smallest positive
+ * fp16 and overflow saturated to 65504, codes clamp(rint(w / scale), -8, 7),
+ * nibbles per row (low = even column, +8 bias), row stride (cols + 1) / 2
+ * bytes, pad nibble 0. scale_f16 is (rows, ceil(cols / group)) fp16 bits. */
+int tiq_quantize_groupwise_int4(const float* w, int64_t rows, int64_t cols, int group,
+                                uint8_t* packed, uint16_t* scale_f16, void* stream);
+
+/* (q.float() * scale)  -- quantization.py:119-129,197. per_channel != 0
+ * reads scale[row], else scale[0]. Output w_hat (rows, cols) contiguous fp32. */
+int tiq_dequantize_int8(const int8_t* q, const float* scale, int per_channel, int64_t rows,
+                        int64_t cols, float* w_hat, void* stream);
+/* The same for the reference nibble layout (rows * cols / 2 bytes, cols even). */
+int tiq_dequantize_int4(const uint8_t* packed, const float* scale, int per_channel, int64_t rows,
+                        int64_t cols, float* w_hat, void* stream);
+/* The same for the group-wise int4 layout above. */
+int tiq_dequantize_groupwise_int4(const uint8_t* packed, const uint16_t* scale_f16, int group,
+                                  int64_t rows, int64_t cols, float* w_hat, void* stream);
+
+/* -------------------------------------------------------------- linear
+ * y[m, n] = sum_k x[m, k] * (q[n, k] * scale[n]) + bias[n]
+ * The quantized replacement of the fp32 F.linear on W_hat at model.py:254
+ * (c_attn), :319 (attn.c_proj), :352 (c_fc), :355 (mlp.c_proj).
+ * x: (M, K) with leading dim ldx, dtype x_dtype (TIQ_F32 or TIQ_BF16);
+ * y: (M, N) with leading dim ldy, dtype y_dtype; bias may be NULL;
+ * scale: N fp32 (a per-tensor scale is passed as N copies).
+ * Accumulation is fp32. Result matches dequantize-then-fp32-matmul within
+ * max|y - y_ref| <= 1e-3 * max|y_ref|; with fp32 x the error is at fp32
+ * rounding level.
+ */
+
+/* Dispatching entry point: picks the decode GEMV (small M) or the MFMA GEMM. */
+int tiq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const int8_t* q, const float* scale, const float* bias, int64_t N,
+                  void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* Decode GEMV on the vector ALUs: coalesced 128-bit weight loads, dequant in
+ * registers, wavefront reductions. Any M (processed in slices of up to 4
+ * rows); needs K % 16 == 0 and 16-byte aligned weight rows. */
+int tiq_gemv_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                const int8_t* q, const float* scale, const float* bias, int64_t N,
+                void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* Prefill GEMM: int8 tiles dequantized to bf16 in LDS, bf16 MFMA, fp32
+ * accumulate, scale + bias epilogue. x must be TIQ_BF16; K % 64 == 0. */
+int tiq_gemm_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                const int8_t* q, const float* scale, const float* bias, int64_t N,
+                void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* int4 weights in the reference's nibble layout (per-row scale, K even,
+ * row n at byte n * K / 2). Same contract as tiq_linear_w8. */
+int tiq_linear_w4(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const uint8_t* packed, const float* scale, const float* bias, int64_t N,
+                  void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* int4 weights in the group-wise layout (fp16 scale per group of `group`
+ * columns). No counterpart in the reference. */
+int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                   const uint8_t* packed, const uint16_t* scale_f16, int group,
+                   const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TIQ_H */

@@ -1,0 +1,135 @@
+"""The quantized model end to end on the GPU.
+
+Greedy tokens must be identical to the reference's: the fixtures in
+``golden/reference_decode.json`` were recorded from the reference package
+itself (seed-0 init, ``quantize_model``, ``generate``), and the oracle's
+restatement reproduces them bit for bit on the CPU (``test_oracle.py``).
+The GPU path computes the four quantized Linears with the HIP kernels in fp32
+(W8A32 / W4A32), everything else with fp32 torch ops.
+"""
+
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+import gpt2_harness_amd as g
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(cfg_dict, dev):
+    torch.manual_seed(0)
+    return g.GPT(g.GPTConfig(**cfg_dict)).to(dev).eval()
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_tiny_greedy_matches_reference(reference_decode, dev, bits):
+    e = reference_decode["tiny"]
+    qm, stats = g.quantize_model(_model(e["config"], dev), bits)
+    gr = e[f"greedy_int{bits}"]
+    prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
+    out = g.generate(qm, prompt, gr["new_tokens"])
+    assert out.cpu().tolist() == gr["ids"]
+    ref = e[f"stats_int{bits}"]
+    for k in ("bits", "granularity", "include_embedding", "n_quantized_tensors", "n_quantized_params",
+              "n_total_params", "fp32_bytes"):
+        assert stats[k] == ref[k], k
+
+
+def test_gpt2_small_int8_greedy_matches_reference(reference_decode, dev):
+    """The headline parity case: GPT-2 small, seed 0, int8 per-channel,
+    64-token prompt, 64 greedy tokens."""
+    e = reference_decode["gpt2_small"]
+    model = _model(e["config"], dev)
+    sd = model.state_dict()
+    for k, h in e["param_sha256"].items():
+        assert hashlib.sha256(sd[k].cpu().contiguous().numpy().tobytes()).hexdigest() == h, k
+    qm, stats = g.quantize_model(model, 8)
+    assert stats["n_quantized_tensors"] == 48 and stats["n_quantized_params"] == 84_934_656
+    assert abs(stats["packed_bytes"] - e["stats_int8"]["packed_bytes"]) < 0.01 * e["stats_int8"]["packed_bytes"]
+    gr = e["greedy_int8"]
+    prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
+    out = g.generate(qm, prompt, gr["new_tokens"])
+    assert out.cpu().tolist() == gr["ids"]
+
+
+def test_quantlinear_weight_is_reference_w_hat(reference_decode, dev):
+    e = reference_decode["tiny"]
+    model = _model(e["config"], dev)
+    original = model.h[0].mlp.c_fc.weight.detach().clone()
+    qm, _ = g.quantize_model(model, 8)
+    p = OM.init_params(OM.Shape(**{k: e["config"][k] for k in ("vocab_size", "n_positions", "n_layer", "n_head",
+                                                                 "n_embd")}), 0)
+    qp, _ = OM.quantize_params(p, 8)
+    for name in ("h.0.attn.c_attn", "h.1.attn.c_proj", "h.2.mlp.c_fc", "h.2.mlp.c_proj"):
+        got = qm.get_submodule(name).weight.cpu()
+        assert torch.equal(got, qp[name + ".weight"]), name
+    assert torch.equal(model.h[0].mlp.c_fc.weight, original), "quantize_model mutated its input"
+    assert isinstance(qm.h[0].mlp.c_fc, g.QuantLinear)
+    assert not torch.equal(qm.h[0].mlp.c_fc.weight, original)
+
+
+@pytest.mark.parametrize("granularity", ["per_tensor", "per_channel"])
+@pytest.mark.parametrize("bits", [8, 4, 6])
+def test_tiny_greedy_matches_oracle_all_schemes(reference_decode, dev, granularity, bits):
+    e = reference_decode["tiny"]
+    c = e["config"]
+    shp = OM.Shape(c["vocab_size"], c["n_positions"], c["n_layer"], c["n_head"], c["n_embd"])
+    qp, _ = OM.quantize_params(OM.init_params(shp, 0), bits, granularity)
+    prompt = OM.benchmark_prompt(shp.vocab_size, 2, 11)
+    want, margins = OM.generate_greedy(qp, shp, prompt, 30)
+    qm, _ = g.quantize_model(_model(c, dev), bits, granularity)
+    got = g.generate(qm, prompt.to(dev), 30)
+    assert got.cpu().tolist() == want.tolist(), f"min margin {min(margins):.3g}"
+
+
+def test_cached_equals_uncached_on_gpu(reference_decode, dev):
+    qm, _ = g.quantize_model(_model(reference_decode["tiny"]["config"], dev), 8)
+    prompt = OM.benchmark_prompt(97, 2, 5).to(dev)
+    a = g.generate(qm, prompt, 40, use_cache=True)
+    b = g.generate(qm, prompt, 40, use_cache=False)
+    assert torch.equal(a, b)
+
+
+def test_logits_close_to_oracle(reference_decode, dev):
+    e = reference_decode["tiny"]
+    c = e["config"]
+    shp = OM.Shape(c["vocab_size"], c["n_positions"], c["n_layer"], c["n_head"], c["n_embd"])
+    qp, _ = OM.quantize_params(OM.init_params(shp, 0), 8)
+    idx = OM.benchmark_prompt(shp.vocab_size, 2, 11)
+    want = OM.forward(qp, shp, idx)
+    qm, _ = g.quantize_model(_model(c, dev), 8)
+    with torch.no_grad():
+        got = qm(idx.to(dev))["logits"].cpu()
+    assert (got - want).abs().max().item() <= 1e-4 * want.abs().max().item()
+
+
+def test_include_embedding_writes_w_hat(reference_decode, dev):
+    e = reference_decode["tiny"]
+    model = _model(e["config"], dev)
+    qm, stats = g.quantize_model(model, 8, include_embedding=True)
+    assert stats["n_quantized_tensors"] == 4 * e["config"]["n_layer"] + 1
+    w = model.wte.weight.detach().cpu().numpy()
+    from oracle import quant as OQ
+
+    assert np.array_equal(qm.wte.weight.detach().cpu().numpy(), OQ.quantize_dequantize(w, 8))
+    assert qm.lm_head.weight is qm.wte.weight
+
+
+def test_groupwise_model_decodes(reference_decode, dev):
+    qm, stats = g.quantize_model(_model(reference_decode["tiny"]["config"], dev), 4, group_size=32)
+    assert stats["group_size"] == 32
+    out = g.generate(qm, OM.benchmark_prompt(97, 1, 4).to(dev), 8)
+    assert out.shape == (1, 12)
+
+
+def test_cpu_model_is_refused(reference_decode):
+    torch.manual_seed(0)
+    model = g.GPT(g.GPTConfig(**reference_decode["tiny"]["config"]))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        g.quantize_model(model, 8)

@@ -1,0 +1,126 @@
+"""Host-side checks that need no GPU.
+
+* the C-ABI library loads and exports every function ``include/tiq.h``
+  declares, with the signatures the binding assumes;
+* the Python API raises the reference's errors before touching a device, and
+  refuses CPU tensors loudly (there is no CPU fallback);
+* the host model mirrors the reference's init (seed-0 digests) and config
+  validation; ``generate`` keeps its greedy / cache / context-limit semantics.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import gpt2_harness_amd as g
+from gpt2_harness_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_functions() -> list[str]:
+    text = (ROOT / "include" / "tiq.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tiq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert len(declared) >= 16
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in tiq.h but not exported"
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with tiq.h"
+    assert lib.tiq_version() >= 100
+    assert lib.tiq_status_string(-2) == b"bits must be in [2, 8]"
+    assert lib.tiq_status_string(0) == b"ok"
+
+
+def test_arguments_checked_before_any_launch():
+    """Entry points validate arguments on the host and never launch on bad input
+    (no GPU is needed to see the error codes)."""
+    lib = _lib.load()
+    assert lib.tiq_quantize_per_channel(None, 4, 4, 4, 9, None, 4, None, None) == -2
+    assert lib.tiq_quantize_per_channel(None, 4, 4, 2, 8, None, 4, None, None) == -1
+    assert lib.tiq_quantize_per_channel(None, 0, 4, 4, 8, None, 4, None, None) == 0
+    assert lib.tiq_quantize_per_tensor(None, 16, 1, None, None, None, 0, None) == -2
+    assert lib.tiq_quantize_groupwise_int4(None, 4, 4, 3, None, None, None) == -1
+    assert lib.tiq_quantize_per_channel_int4_packed(None, 4, 5, 4, None, None, None) == -4
+    assert lib.tiq_linear_w8(None, 0, 0, 16, 16, None, None, None, 4, None, 0, 4, None) == 0
+    assert lib.tiq_linear_w8(None, 3, 1, 16, 16, None, None, None, 4, None, 0, 4, None) == -1
+    assert lib.tiq_linear_w4g(None, 0, 1, 16, 16, None, None, 3, None, 4, None, 0, 4, None) == -1
+    assert lib.tiq_quantize_per_tensor_workspace(1 << 20) >= 4
+
+
+def test_api_errors_match_reference_without_gpu():
+    w = torch.zeros(4, 4)
+    with pytest.raises(ValueError, match=r"bits must be in \[2, 8\], got 9"):
+        g.quantize_tensor(w, 9)
+    with pytest.raises(ValueError, match="unknown granularity 'per_row'"):
+        g.quantize_tensor(w, 8, "per_row")
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        g.quantize_tensor(w, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        g.pack_int4(torch.zeros(4, dtype=torch.int8))
+
+
+def test_config_validation_and_sizes():
+    with pytest.raises(ValueError, match="must be divisible"):
+        g.GPTConfig(n_embd=10, n_head=3)
+    with pytest.raises(ValueError, match="unknown GPT-2 size"):
+        g.gpt2_config("gpt2-huge")
+    xl = g.gpt2_config("gpt2-xl")
+    assert (xl.n_layer, xl.n_head, xl.n_embd) == (48, 25, 1600)
+    assert g.GPTConfig().kv_cache_bytes_per_token(4) == 73_728
+    assert xl.kv_cache_bytes_per_token(4) == 614_400
+
+
+@pytest.mark.parametrize("label", ["tiny", "gpt2_small"])
+def test_host_model_init_matches_reference(reference_decode, label):
+    e = reference_decode[label]
+    torch.manual_seed(0)
+    sd = g.GPT(g.GPTConfig(**e["config"])).state_dict()
+    for k, h in e["param_sha256"].items():
+        assert hashlib.sha256(sd[k].contiguous().numpy().tobytes()).hexdigest() == h, k
+
+
+def test_param_count_and_tying():
+    torch.manual_seed(0)
+    m = g.GPT(g.GPTConfig())
+    assert m.num_parameters() == 124_439_808
+    assert m.lm_head.weight is m.wte.weight
+
+
+def test_generate_semantics_on_cpu_float_model(reference_decode):
+    """The decode loop itself (unquantized fp32 model on the CPU): cached ==
+    uncached, context-limit stop, EOS stop, sampling refused."""
+    torch.manual_seed(0)
+    cfg = g.GPTConfig(vocab_size=64, n_positions=24, n_layer=2, n_head=4, n_embd=32)
+    m = g.GPT(cfg).eval()
+    p = torch.randint(0, 64, (2, 5))
+    a = g.generate(m, p, 12, use_cache=True)
+    b = g.generate(m, p, 12, use_cache=False)
+    assert torch.equal(a, b)
+    assert g.generate(m, p, 100).shape[1] == 24
+    first = int(a[0, 5])
+    out = g.generate(m, p[:1], 10, eos_token_id=first)
+    assert out.shape[1] == 6
+    with pytest.raises(NotImplementedError):
+        g.generate(m, p, 3, do_sample=True)
+    with pytest.raises(ValueError, match="exceeds n_positions"):
+        m(torch.zeros(1, 25, dtype=torch.long))
+
+
+def test_kv_cache_length_semantics():
+    c = g.KVCache.empty(2)
+    assert c.seq_len == 0 and c.length(1) == 0
+    k = torch.zeros(1, 2, 3, 4)
+    c.update(0, k, k)
+    assert c.seq_len == 3 and c.length(1) == 0
+    kk, _ = c.update(0, k[:, :, :1], k[:, :, :1])
+    assert kk.shape[-2] == 4

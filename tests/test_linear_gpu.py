@@ -1,0 +1,171 @@
+"""Quantized linear kernels on the GPU against dequantize-then-fp32-matmul.
+
+Contract: ``max|y - y_ref| <= 1e-3 * max|y_ref|`` with ``y_ref =
+F.linear(x.float(), q.float() * scale, b)`` computed by the oracle on the CPU
+from the same seeded inputs. Kernels write fp32 or bf16; a bf16 result must be
+exactly the round-to-nearest-even of the fp32 result the same kernel computes
+(so its only extra error is the storage rounding), and the fp32 result is held
+to the 1e-3 bound. Entry points are called through the C ABI.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpt2_harness_amd import _lib
+from oracle import linear as OL
+from oracle import quant as OQ
+
+pytestmark = pytest.mark.gpu
+
+SMALL = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]   # (K, N) as in K x N
+XL = [(1600, 4800), (1600, 1600), (1600, 6400), (6400, 1600)]
+TOL = 1e-3
+
+
+def _inputs(K, N, M, seed, x_dtype=torch.float32, bias=True):
+    gen = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen).to(x_dtype)
+    b = torch.randn(N, generator=gen) * 0.1 if bias else None
+    return w, x, b
+
+
+def _call(entry, x, q, scale, b, N, y, *extra):
+    L = _lib.lib()
+    fn = getattr(L, entry)
+    M, K = x.shape
+    xd, yd = _lib.dtype_code(x.dtype), _lib.dtype_code(y.dtype)
+    st = torch.cuda.current_stream().cuda_stream
+    bp = None if b is None else b.data_ptr()
+    if entry == "tiq_linear_w4g":
+        group = extra[0]
+        rc = fn(x.data_ptr(), xd, M, K, x.stride(0), q.data_ptr(), scale.data_ptr(), group, bp, N, y.data_ptr(), yd,
+                y.stride(0), st)
+    else:
+        rc = fn(x.data_ptr(), xd, M, K, x.stride(0), q.data_ptr(), scale.data_ptr(), bp, N, y.data_ptr(), yd,
+                y.stride(0), st)
+    _lib.check(rc, entry)
+    torch.cuda.synchronize()
+
+
+def _run_w8(entry, dev, c_oracle, K, N, M, x_dtype, seed=0, bias=True):
+    w, x, b = _inputs(K, N, M, seed, x_dtype, bias)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    qd, sd = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev)
+    bd = None if b is None else b.to(dev)
+    xd = x.to(dev)
+    y32 = torch.empty(M, N, device=dev)
+    ybf = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    _call(entry, xd, qd, sd, bd, N, y32)
+    _call(entry, xd, qd, sd, bd, N, ybf)
+    y_ref = OL.linear_ref(x, OL.dequantize(q, s), b)
+    ok, err, bound = OL.within_tolerance(y32, y_ref, TOL)
+    assert ok, f"{entry} M={M} K={K} N={N} {x_dtype}: max err {err:.3g} > {bound:.3g}"
+    assert torch.equal(ybf.cpu(), y32.cpu().to(torch.bfloat16)), "bf16 output is not RNE of the fp32 output"
+
+
+@pytest.mark.parametrize("KN", SMALL + XL)
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_gemv_w8(dev, c_oracle, KN, M, x_dtype):
+    _run_w8("tiq_gemv_w8", dev, c_oracle, *KN, M, x_dtype, seed=M)
+
+
+@pytest.mark.parametrize("M", [2, 3, 5, 7, 8, 33])
+def test_gemv_w8_odd_batches(dev, c_oracle, M):
+    _run_w8("tiq_gemv_w8", dev, c_oracle, 768, 2304, M, torch.float32, seed=M, bias=M % 2 == 0)
+
+
+@pytest.mark.parametrize("KN", XL)
+@pytest.mark.parametrize("M", [256, 300])
+def test_gemm_w8(dev, c_oracle, KN, M):
+    _run_w8("tiq_gemm_w8", dev, c_oracle, *KN, M, torch.bfloat16, seed=M)
+
+
+@pytest.mark.parametrize("KN", [(768, 2304), (3072, 768)])
+@pytest.mark.parametrize("M", [16, 17, 64, 1024])
+def test_gemm_w8_small_shapes(dev, c_oracle, KN, M):
+    _run_w8("tiq_gemm_w8", dev, c_oracle, *KN, M, torch.bfloat16, seed=M, bias=False)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64, 256])
+def test_linear_w8_dispatch(dev, c_oracle, M):
+    _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.bfloat16, seed=M)
+    _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.float32, seed=M)
+
+
+@pytest.mark.parametrize("K,N", [(100, 37), (24, 5), (1600, 1)])
+def test_generic_fallback_shapes(dev, c_oracle, K, N):
+    """K not a multiple of 16 (and N = 1): the scalar fallback kernel."""
+    _run_w8("tiq_linear_w8", dev, c_oracle, K, N, 3, torch.float32, seed=K)
+
+
+def test_strided_activations_and_outputs(dev, c_oracle):
+    K, N, M = 768, 2304, 4
+    w, x, b = _inputs(K, N, M, 5)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    xs = torch.zeros(M, K + 64, device=dev)
+    xs[:, :K] = x.to(dev)
+    ys = torch.full((M, N + 32), 7.0, device=dev)
+    _call("tiq_linear_w8", xs[:, :K], torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev),
+          b.to(dev), N, ys[:, :N])
+    ok, err, bound = OL.within_tolerance(ys[:, :N], OL.linear_ref(x, OL.dequantize(q, s), b))
+    assert ok, (err, bound)
+    assert torch.all(ys[:, N:] == 7.0), "kernel wrote outside its output rows"
+
+
+@pytest.mark.parametrize("KN", [(768, 2304), (1600, 6400), (6400, 1600)])
+@pytest.mark.parametrize("M", [1, 4, 256])
+def test_linear_w4_reference_layout(dev, c_oracle, KN, M):
+    K, N = KN
+    w, x, b = _inputs(K, N, M, M + K, torch.bfloat16 if M >= 16 else torch.float32)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 4)
+    packed = torch.from_numpy(c_oracle.pack_int4(q)).to(dev)
+    y = torch.empty(M, N, device=dev)
+    _call("tiq_linear_w4", x.to(dev), packed, torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), N, y)
+    ok, err, bound = OL.within_tolerance(y, OL.linear_ref(x, OL.dequantize(q, s), b))
+    assert ok, (err, bound)
+
+
+@pytest.mark.parametrize("KN", [(768, 2304), (1600, 4800), (6400, 1600)])
+@pytest.mark.parametrize("M", [1, 4, 64])
+def test_linear_w4_groupwise(dev, c_oracle, KN, M):
+    K, N = KN
+    w, x, b = _inputs(K, N, M, M + 2 * K)
+    packed, s16 = c_oracle.quantize_groupwise_int4(w.numpy(), 128)
+    y = torch.empty(M, N, device=dev)
+    _call("tiq_linear_w4g", x.to(dev), torch.from_numpy(packed).to(dev),
+          torch.from_numpy(s16.view(np.uint16).copy()).to(dev), b.to(dev), N, y, 128)
+    w_hat = torch.from_numpy(OQ.dequantize_groupwise_int4(packed, s16, K, 128))
+    ok, err, bound = OL.within_tolerance(y, OL.linear_ref(x, w_hat, b))
+    assert ok, (err, bound)
+
+
+def test_zero_rows_is_a_no_op(dev):
+    L = _lib.lib()
+    y = torch.full((1, 4), 3.0, device=dev)
+    x = torch.zeros(1, 16, device=dev)
+    q = torch.zeros(4, 16, dtype=torch.int8, device=dev)
+    s = torch.ones(4, device=dev)
+    rc = L.tiq_linear_w8(x.data_ptr(), 0, 0, 16, 16, q.data_ptr(), s.data_ptr(), None, 4, y.data_ptr(), 0, 4,
+                         torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert torch.all(y == 3.0)
+
+
+def test_bad_arguments_are_rejected(dev):
+    L = _lib.lib()
+    x = torch.zeros(2, 16, device=dev)
+    q = torch.zeros(4, 16, dtype=torch.int8, device=dev)
+    s = torch.ones(4, device=dev)
+    y = torch.zeros(2, 4, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    # ldx smaller than K, bad dtype code, null weight pointer
+    assert L.tiq_linear_w8(x.data_ptr(), 0, 2, 16, 8, q.data_ptr(), s.data_ptr(), None, 4, y.data_ptr(), 0, 4, st) == -1
+    assert L.tiq_linear_w8(x.data_ptr(), 7, 2, 16, 16, q.data_ptr(), s.data_ptr(), None, 4, y.data_ptr(), 0, 4, st) == -1
+    assert L.tiq_linear_w8(x.data_ptr(), 0, 2, 16, 16, None, s.data_ptr(), None, 4, y.data_ptr(), 0, 4, st) == -1
+    # fp32 activations have no MFMA kernel: the explicit GEMM entry refuses them
+    assert L.tiq_gemm_w8(x.data_ptr(), 0, 2, 16, 16, q.data_ptr(), s.data_ptr(), None, 4, y.data_ptr(), 0, 4, st) == -4
