@@ -1,0 +1,398 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Headline (``value``): W8A16 decode GEMV throughput at GPT-2 small Linear
+shapes -- one step is the decode-time pass over all 48 quantized Linears of
+GPT-2 small (12 layers x {c_attn 768x2304, attn.c_proj 768x768, c_fc
+768x3072, mlp.c_proj 3072x768}, K x N) at M = 1 with bf16 activations, int8
+per-channel weights and bf16 outputs. Weights are synthetic (N(0, 0.02),
+quantized by this library) and rotated over 6 model copies (510 MB) so every
+step reads them cold from HBM, past the 256 MB Infinity Cache. Algorithmic
+bytes per launch = N*K + 4*N + 2*M*K + 2*M*N; value = bytes / wall time of
+the K timed steps (HIP events on the launch stream; one step is one replay
+of a captured HIP graph of the 48 launches).
+
+``detail`` adds the other configurations: M = 4 / 16 at the same shapes,
+GPT-2-XL layer shapes at M = 1 (per shape), the int8->bf16 MFMA GEMM at
+GPT-2-XL shapes with M = 4096, the quantize kernels, and GPT-2 small int8
+greedy decode (64-token prompt, 64 new tokens) with its token parity against
+the reference fixture. ``cpu_baseline`` times the oracle's dequantize-then-
+fp32-matmul (the reference's runtime arithmetic) on the host cores over a
+bounded sample of the same GEMV workload.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "gpt2-harness_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "quantized-linear HBM GB/s (decode GEMV) + GPT-2 int8 decode tokens/sec, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+SMALL_KN = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+XL_KN = [(1600, 4800), (1600, 1600), (1600, 6400), (6400, 1600)]
+
+
+def host_cores() -> int:
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if quota != "max":
+            n = max(1, min(n, int(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def gemv_bytes(M: int, K: int, N: int, x_bytes: int = 2, y_bytes: int = 2) -> int:
+    return N * K + 4 * N + x_bytes * M * K + y_bytes * M * N
+
+
+class LinearSet:
+    """Quantized weights of `copies` x `layers` Linears of the given shapes,
+    with activation / output buffers, launched through the C ABI."""
+
+    def __init__(self, kn, layers, copies, M, dev, seed=0, x_dtype=None, y_dtype=None):
+        import torch
+
+        import gpt2_harness_amd as g
+        from gpt2_harness_amd import _lib
+
+        self.torch, self.lib = torch, _lib.lib()
+        self.M = M
+        x_dtype = x_dtype or torch.bfloat16
+        y_dtype = y_dtype or torch.bfloat16
+        self.xd, self.yd = _lib.dtype_code(x_dtype), _lib.dtype_code(y_dtype)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        self.items = []  # per copy: list of (K, N, q, s, x, y)
+        xs = {K: torch.randn(M, K, generator=gen, device=dev).to(x_dtype) for K, _ in kn}
+        for _c in range(copies):
+            items = []
+            for _l in range(layers):
+                for K, N in kn:
+                    w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+                    q, s = g.quantize_tensor(w, 8)
+                    del w
+                    y = torch.empty(M, N, device=dev, dtype=y_dtype)
+                    items.append((K, N, q, s.reshape(-1).contiguous(), xs[K], y))
+            self.items.append(items)
+        torch.cuda.synchronize()
+        self.bytes_per_copy = sum(gemv_bytes(M, K, N, x_dtype.itemsize, y_dtype.itemsize)
+                                  for K, N, *_ in self.items[0])
+        self.launches_per_copy = len(self.items[0])
+
+    def launch_copy(self, c: int, entry: str = "tiq_linear_w8") -> None:
+        fn = getattr(self.lib, entry)
+        st = self.torch.cuda.current_stream().cuda_stream
+        for K, N, q, s, x, y in self.items[c]:
+            rc = fn(x.data_ptr(), self.xd, self.M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), self.yd,
+                    N, st)
+            if rc:
+                raise RuntimeError(f"{entry} failed with status {rc}")
+
+
+def timed_graph_steps(ls: LinearSet, steps: int, warmup: int, entry: str = "tiq_linear_w8"):
+    """Capture one HIP graph per weight copy; time `steps` replays (rotating)."""
+    import torch
+
+    copies = len(ls.items)
+    graphs = []
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in range(copies):  # warm once eagerly (module load), then capture
+            ls.launch_copy(c, entry)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for c in range(copies):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            ls.launch_copy(c, entry)
+        graphs.append(gr)
+    for i in range(warmup):
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % copies].replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    return ms / steps
+
+
+def per_launch_times(ls: LinearSet, reps: int, entry: str = "tiq_linear_w8"):
+    """Event pair around every launch (eager), weights rotated: per-shape ms."""
+    import torch
+
+    out: dict[tuple[int, int], list[float]] = {}
+    copies = len(ls.items)
+    for r in range(reps):
+        items = ls.items[r % copies]
+        evs = []
+        st = torch.cuda.current_stream().cuda_stream
+        fn = getattr(ls.lib, entry)
+        for K, N, q, s, x, y in items:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            rc = fn(x.data_ptr(), ls.xd, ls.M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), ls.yd, N, st)
+            b.record()
+            if rc:
+                raise RuntimeError(f"{entry} failed with status {rc}")
+            evs.append((K, N, a, b))
+        torch.cuda.synchronize()
+        for K, N, a, b in evs:
+            out.setdefault((K, N), []).append(a.elapsed_time(b))
+    return {kn: statistics.median(v) for kn, v in out.items()}
+
+
+def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed):
+    ls = LinearSet(kn, layers, copies, M, dev, seed)
+    ms = timed_graph_steps(ls, steps, warmup)
+    gbs = ls.bytes_per_copy / (ms * 1e-3) / 1e9
+    per = per_launch_times(ls, max(2, copies))
+    shapes = {f"{K}x{N}": {"us": per[(K, N)] * 1e3,
+                           "GB/s": gemv_bytes(M, K, N) / (per[(K, N)] * 1e-3) / 1e9} for K, N in kn}
+    res = {"M": M, "ms_per_step": ms, "GB/s": gbs, "launches_per_step": ls.launches_per_copy,
+           "bytes_per_step": ls.bytes_per_copy, "avg_launch_us": ms * 1e3 / ls.launches_per_copy,
+           "per_shape_eager": shapes}
+    del ls
+    return res
+
+
+def gemm_section(M, kn, dev, reps=5):
+    import torch
+
+    import gpt2_harness_amd as g
+    from gpt2_harness_amd import _lib
+
+    L = _lib.lib()
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(1)
+    for K, N in kn:
+        w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+        q, s = g.quantize_tensor(w, 8)
+        s = s.reshape(-1).contiguous()
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        st = torch.cuda.current_stream().cuda_stream
+
+        def run():
+            rc = L.tiq_gemm_w8(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1, N, st)
+            if rc:
+                raise RuntimeError(f"tiq_gemm_w8 status {rc}")
+
+        run()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            run()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        ms = statistics.median(ts)
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out[f"{K}x{N}"] = {"us": ms * 1e3, "TFLOP/s": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS}
+    return {"M": M, "per_shape": out}
+
+
+def quantize_section(dev, reps=5):
+    import torch
+
+    import gpt2_harness_amd as g
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(2)
+    for K, N in XL_KN:
+        w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+        n_out = max(1, N * K // 1000)
+        idx = torch.randperm(N * K, generator=gen, device=dev)[:n_out]
+        w.view(-1)[idx] *= 20.0
+        for label, fn, nbytes in (
+            ("int8_per_channel", lambda: g.quantize_tensor(w, 8), 5 * N * K + 4 * N),
+            ("int4_g128", lambda: g.quantize_groupwise_int4(w, 128), 4 * N * K + N * K // 2 + 2 * N * -(-K // 128)),
+        ):
+            fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                fn()
+                b.record()
+                torch.cuda.synchronize()
+                ts.append(a.elapsed_time(b))
+            ms = statistics.median(ts)
+            out[f"{label}_{K}x{N}"] = {"us": ms * 1e3, "GB/s": nbytes / (ms * 1e-3) / 1e9}
+    return out
+
+
+def decode_section(dev, repeats=3):
+    import torch
+
+    import gpt2_harness_amd as g
+
+    golden = json.loads((ROOT / "tests" / "golden" / "reference_decode.json").read_text())["gpt2_small"]
+    torch.manual_seed(0)
+    model = g.GPT(g.GPTConfig()).to(dev).eval()
+    qm, _ = g.quantize_model(model, 8)
+    del model
+    torch.manual_seed(0)
+    prompt = torch.randint(0, 50257, (1, 64)).to(dev)
+    out = g.generate(qm, prompt, 64)
+    match = out.cpu().tolist() == golden["greedy_int8"]["ids"]
+    ts = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.generate(qm, prompt, 64)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    return {"model": "gpt2 (124M) seed 0, int8 per-channel", "prompt": 64, "new_tokens": 64,
+            "tokens_per_s": 64 / med, "ms_per_token": 1e3 * med / 64, "tokens_match_reference": match}
+
+
+def cpu_baseline(budget_s: float = 10.0):
+    """The oracle's dequantize-then-fp32-matmul over the GEMV workload on the host."""
+    import torch
+
+    from oracle import linear as OL
+    from oracle import quant as OQ
+
+    cores = host_cores()
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(0)
+    layers = []
+    for _ in range(12):
+        for K, N in SMALL_KN:
+            w = (torch.randn(N, K, generator=gen) * 0.02).numpy()
+            q, s = OQ.quantize_tensor(w, 8)
+            layers.append((K, N, OL.dequantize(q, s)))
+    xs = {K: torch.randn(1, K, generator=gen).to(torch.bfloat16) for K, _ in SMALL_KN}
+    step_bytes = sum(gemv_bytes(1, K, N) for K, N, _ in layers)
+
+    def step():
+        for K, _N, w_hat in layers:
+            OL.linear_ref(xs[K], w_hat)
+
+    step()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(ts) < 3:
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    return {"value": step_bytes / med / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(ts)} steps of the same 48-Linear M=1 GEMV workload, oracle F.linear(x.float(), "
+                      f"q.float()*scale) in fp32 on {cores} host threads; GB/s counts the same int8 "
+                      f"algorithmic bytes as the GPU value (the CPU path reads 4-byte fp32 W_hat)",
+            "ms_per_step": med * 1e3}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
+    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode"], default=None,
+                    help="run one section alone (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+
+    if args.only == "gemm":
+        print(json.dumps(gemm_section(4096, XL_KN, dev)))
+        return 0
+    if args.only == "quantize":
+        print(json.dumps(quantize_section(dev)))
+        return 0
+    if args.only == "decode":
+        print(json.dumps(decode_section(dev)))
+        return 0
+
+    head = gemv_section(1, SMALL_KN, 12, 6, args.steps, args.warmup, dev, seed=0)
+    print(f"# headline gemv M=1: {head['GB/s']:.1f} GB/s, {head['ms_per_step']:.4f} ms/step", file=sys.stderr,
+          flush=True)
+    detail: dict = {}
+    cpu = None
+    if not args.quick and args.only is None:
+        for M in (4, 16):
+            detail[f"gemv_small_M{M}"] = gemv_section(M, SMALL_KN, 12, 6, max(10, args.steps // 2), 2, dev, seed=M)
+        detail["gemv_xl_M1"] = gemv_section(1, XL_KN, 12, 3, 10, 2, dev, seed=7)
+        print("# gemv detail done", file=sys.stderr, flush=True)
+        detail["gemm_xl_M4096"] = gemm_section(4096, XL_KN, dev)
+        print("# gemm done", file=sys.stderr, flush=True)
+        detail["quantize_xl"] = quantize_section(dev)
+        detail["decode_gpt2_small_int8"] = decode_section(dev)
+        print("# decode done", file=sys.stderr, flush=True)
+        cpu = cpu_baseline()
+
+    avg_launch_s = head["avg_launch_us"] * 1e-6
+    bytes_per_launch = head["bytes_per_step"] / head["launches_per_step"]
+    achieved = bytes_per_launch / avg_launch_s / 1e9
+    line = {
+        "metric": METRIC,
+        "value": head["GB/s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights quantized int8 per-channel, N(0,1) bf16 activations)",
+        "config": {
+            "workload": "W8A16 decode GEMV over the 48 quantized Linears of GPT-2 small "
+                        "(12 x K x N in 768x2304, 768x768, 768x3072, 3072x768), M=1, "
+                        "weights rotated over 6 copies (510 MB) per step",
+            "M": 1, "layers": 12, "weight_copies": 6,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "gemv_kernel (tiq_linear_w8, M=1)",
+            "bytes_per_launch": bytes_per_launch,
+            "avg_launch_us": head["avg_launch_us"],
+        },
+        "cpu_baseline": cpu,
+        "detail": {"gemv_small_M1": head, **detail},
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
