@@ -312,8 +312,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode"], default=None,
-                    help="run one section alone (for profiling)")
+    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode", "copy"], default=None,
+                    help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
+                         "used to calibrate the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
@@ -327,6 +328,14 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
 
+    if args.only == "copy":
+        src = torch.randn(64 << 20, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 5}))
+        return 0
     if args.only == "gemm":
         print(json.dumps(gemm_section(4096, XL_KN, dev)))
         return 0
@@ -342,11 +351,12 @@ def main() -> int:
           flush=True)
     detail: dict = {}
     cpu = None
-    if not args.quick and args.only is None:
+    if not args.quick and args.only in (None, "gemv"):
         for M in (4, 16):
             detail[f"gemv_small_M{M}"] = gemv_section(M, SMALL_KN, 12, 6, max(10, args.steps // 2), 2, dev, seed=M)
         detail["gemv_xl_M1"] = gemv_section(1, XL_KN, 12, 3, 10, 2, dev, seed=7)
         print("# gemv detail done", file=sys.stderr, flush=True)
+    if not args.quick and args.only is None:
         detail["gemm_xl_M4096"] = gemm_section(4096, XL_KN, dev)
         print("# gemm done", file=sys.stderr, flush=True)
         detail["quantize_xl"] = quantize_section(dev)
@@ -354,6 +364,14 @@ def main() -> int:
         print("# decode done", file=sys.stderr, flush=True)
         cpu = cpu_baseline()
 
+    traffic = None
+    tfile = ROOT / "profiles" / "gemv_w8a16_gpt2small_m1.traffic.json"
+    if tfile.exists():
+        from gpt2_harness_amd import _lib
+
+        t = json.loads(tfile.read_text())
+        if t.get("tiq_version") == _lib.lib().tiq_version():
+            traffic = t["traffic_bytes_per_launch"]
     avg_launch_s = head["avg_launch_us"] * 1e-6
     bytes_per_launch = head["bytes_per_step"] / head["launches_per_step"]
     achieved = bytes_per_launch / avg_launch_s / 1e9
@@ -382,7 +400,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "gemv_kernel (tiq_linear_w8, M=1)",
             "bytes_per_launch": bytes_per_launch,
             "avg_launch_us": head["avg_launch_us"],

@@ -100,10 +100,33 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
     const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int N, int K) {
     constexpr int KC = Fmt<FMT>::KC;
     constexpr int P = KC / 4;  // float4 planes per chunk
+    constexpr int U = 4;       // chunks per row in flight per lane
     extern __shared__ float4 xs[];
     const int K4 = K >> 2;
     const int NC = K / KC;
     const int m0 = blockIdx.y * MT;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * kWavesPerBlock + wave) * R;
+    const bool active = n0 < N;  // wave-uniform
+
+    const uint8_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = w + (int64_t)((n0 + r < N) ? n0 + r : (active ? n0 : 0)) * ldw;
+
+    // weight chunks c0 + 64u of every row, zero past the end of the row
+    uint4 wv[U][R];
+    auto load_block = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + 64 * u;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                wv[u][r] = (c < NC) ? *reinterpret_cast<const uint4*>(wrow[r] + 16 * (int64_t)c) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    // The first weight block goes out before the activations are staged, so
+    // its HBM latency overlaps the staging and the barrier.
+    if (active) load_block(lane);
 
     // stage MT activation rows as fp32 planes: xs[m][p][c]
     for (int t = threadIdx.x; t < MT * K4; t += blockDim.x) {
@@ -114,10 +137,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
         xs[m * K4 + p * NC + c] = v;
     }
     __syncthreads();
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n0 = (blockIdx.x * kWavesPerBlock + wave) * R;
-    if (n0 >= N) return;  // wave-uniform, after the only barrier
+    if (!active) return;  // after the only barrier
 
     float acc[R][MT];
 #pragma unroll
@@ -125,21 +145,14 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 
-    const uint8_t* wrow[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) wrow[r] = w + (int64_t)((n0 + r < N) ? n0 + r : n0) * ldw;
-
-    // U chunks per row in flight per lane before the first use
-    constexpr int U = 4;
+    const int ng = (FMT == kW4G) ? (K + group - 1) / group : 0;
     for (int c0 = lane; c0 < NC; c0 += 64 * U) {
-        uint4 wv[U][R];
+        uint4 cur[U][R];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + 64 * u;
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                wv[u][r] = (c < NC) ? *reinterpret_cast<const uint4*>(wrow[r] + 16 * (int64_t)c) : make_uint4(0, 0, 0, 0);
-        }
+            for (int r = 0; r < R; ++r) cur[u][r] = wv[u][r];
+        if (c0 + 64 * U < NC) load_block(c0 + 64 * U);  // next block in flight during this one's math
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int c = c0 + 64 * u;
@@ -147,7 +160,6 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
             float gs[R];
             if (FMT == kW4G) {
                 const int g = (c * KC) / group;
-                const int ng = (K + group - 1) / group;
 #pragma unroll
                 for (int r = 0; r < R; ++r)
                     gs[r] = f16_bits_to_f32(scale16[(int64_t)((n0 + r < N) ? n0 + r : n0) * ng + g]);
@@ -159,7 +171,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
                 for (int p = 0; p < P; ++p) xv[p] = xs[m * K4 + p * NC + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float part = (FMT == kW8) ? dot_w8(wv[u][r], xv) : dot_w4(wv[u][r], xv);
+                    const float part = (FMT == kW8) ? dot_w8(cur[u][r], xv) : dot_w4(cur[u][r], xv);
                     if (FMT == kW4G) acc[r][m] = fmaf(gs[r], part, acc[r][m]);
                     else acc[r][m] += part;
                 }

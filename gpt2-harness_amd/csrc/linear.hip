@@ -21,8 +21,9 @@ int check_linear(const LinearArgs& a) {
 
 namespace {
 
-// Rows of M at and above which the MFMA GEMM beats the vector-ALU GEMV.
-constexpr int64_t kGemmMinRows = 16;
+// Rows of M at and above which the 128 x 128-tile MFMA GEMM beats the
+// vector-ALU GEMV (below it the GEMM wastes most of each tile).
+constexpr int64_t kGemmMinRows = 128;
 
 LinearArgs make_args(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w, int64_t ldw,
                      const float* scale, const uint16_t* scale16, int group, const float* bias, int64_t N, void* y,
