@@ -254,18 +254,23 @@ def decode_section(dev, repeats=3):
     del model
     torch.manual_seed(0)
     prompt = torch.randint(0, 50257, (1, 64)).to(dev)
-    out = g.generate(qm, prompt, 64)
-    match = out.cpu().tolist() == golden["greedy_int8"]["ids"]
-    ts = []
-    for _ in range(repeats):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        g.generate(qm, prompt, 64)
-        torch.cuda.synchronize()
-        ts.append(time.perf_counter() - t0)
-    med = statistics.median(ts)
-    return {"model": "gpt2 (124M) seed 0, int8 per-channel", "prompt": 64, "new_tokens": 64,
-            "tokens_per_s": 64 / med, "ms_per_token": 1e3 * med / 64, "tokens_match_reference": match}
+    want = golden["greedy_int8"]["ids"]
+    res = {"model": "gpt2 (124M) seed 0, int8 per-channel", "prompt": 64, "new_tokens": 64}
+    dec = g.GraphDecoder(qm, 1, 128)
+    for label, fn in (("eager", lambda: g.generate(qm, prompt, 64)),
+                      ("graph", lambda: g.generate_graph(qm, prompt, 64, decoder=dec))):
+        out = fn()
+        match = out.cpu().tolist() == want
+        ts = []
+        for _ in range(repeats):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        med = statistics.median(ts)
+        res[label] = {"tokens_per_s": 64 / med, "ms_per_token": 1e3 * med / 64, "tokens_match_reference": match}
+    return res
 
 
 def cpu_baseline(budget_s: float = 10.0):

@@ -3,18 +3,27 @@
 //     y[m, n] = scale[n] * sum_k x[m, k] * q[n, k] + bias[n]
 //
 //   * workgroup tile BM x BN over (M, N), BK = 64 columns of K per step;
-//     four wavefronts in a 2 x 2 arrangement, each owning a
-//     (BM/2) x (BN/2) block of 16 x 16 v_mfma_f32_16x16x32_bf16 tiles;
+//     WAVES_M x WAVES_N wavefronts, each owning a (BM/WAVES_M) x (BN/WAVES_N)
+//     block of 32 x 32 v_mfma_f32_32x32x16_bf16 tiles (fp32 accumulators;
+//     measured on this chip the 32 x 32 x 16 form sustains 87% of the bf16
+//     peak from one wave per SIMD, the 16 x 16 x 32 form 42%);
 //   * activations (bf16) and weights (int8 or int4 nibbles) stream from HBM
-//     with 128-bit loads; the weight codes are converted to bf16 in registers
+//     with 128-bit loads; weight codes are converted to bf16 in registers
 //     (exact: every int8 value is a bf16) before they are written to LDS, so
-//     the MFMA reads bf16 operands for both sides;
-//   * LDS rows are padded by 16 bytes so that the 16 lanes reading one
-//     fragment column hit 16 disjoint bank quads;
-//   * the next k-step's global loads are issued before the current step's
-//     MFMAs (register prefetch), so HBM latency hides behind the matrix cores;
+//     the MFMA reads bf16 operands on both sides;
+//   * LDS is double buffered: the global loads of step k+1 are in flight
+//     while step k's MFMAs run, and their LDS store goes to the other buffer,
+//     so each step needs one barrier;
+//   * LDS tiles are XOR-swizzled (see gemm32_kernel) so fragment reads and
+//     tile stores are free of bank conflicts without padding;
+//   * workgroups are renumbered so that the ones sharing an XCD (dispatch
+//     order round-robins over the 8 XCDs) take neighbouring tiles, and
+//     within an XCD tiles are walked in column groups so the A panel and the
+//     weight panel they share stay in that XCD's L2;
 //   * the epilogue multiplies the fp32 accumulators by the per-channel scale
 //     and adds the bias, exactly once per output.
+#include <cstdlib>
+
 #include "tiq_internal.hpp"
 
 namespace tiq {
@@ -24,19 +33,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;
-constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row (16-byte pad)
-constexpr int kThreads = 256;
+constexpr int kXcds = 8;
 
 // two sign-extended bytes -> two bf16 in one dword (exact)
 __device__ __forceinline__ uint32_t bf16x2_of_bytes(uint32_t d, int shift_lo) {
     const float lo = (float)((int32_t)(d << (24 - shift_lo)) >> 24);
     const float hi = (float)((int32_t)(d << (16 - shift_lo)) >> 24);
     return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
-}
-
-// 4 int8 codes of a dword -> 4 bf16 (two dwords)
-__device__ __forceinline__ uint2 bf16x4_of_i8x4(uint32_t d) {
-    return make_uint2(bf16x2_of_bytes(d, 0), bf16x2_of_bytes(d, 16));
 }
 
 // two biased nibbles -> two bf16 in one dword
@@ -46,122 +49,170 @@ __device__ __forceinline__ uint32_t bf16x2_of_nibbles(uint32_t d, int sh) {
     return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
 }
 
-template <int BM, int BN, int FMT, typename TY>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                        const uint8_t* __restrict__ w, int64_t ldw,
-                                                        const float* __restrict__ scale,
-                                                        const float* __restrict__ bias, TY* __restrict__ y,
-                                                        int64_t ldy, int M, int N, int K) {
-    constexpr int WM = BM / 2, WN = BN / 2;      // wave tile
-    constexpr int TM = WM / 16, TN = WN / 16;    // MFMA tiles per wave
-    constexpr int A_VEC = BM * BK / 8 / kThreads;  // uint4 (8 bf16) per thread
-    // weights: int8 -> 16 codes per uint4; int4 -> 32 codes per uint4
-    constexpr int CODES = (FMT == kW8) ? 16 : 32;
-    constexpr int B_VEC = BN * BK / CODES / kThreads;
-    static_assert(A_VEC >= 1 && B_VEC >= 1, "tile too small for the workgroup");
+// Workgroup id -> (tile_m, tile_n): XCD-contiguous, then column groups of
+// GROUP_M row tiles.
+__device__ __forceinline__ void tile_of(int& tm, int& tn, int tiles_m, int tiles_n) {
+    const int total = tiles_m * tiles_n;
+    int id = blockIdx.x;
+    if (total % kXcds == 0) {
+        const int per = total / kXcds;
+        id = (id % kXcds) * per + id / kXcds;
+    }
+    constexpr int GROUP_M = 8;
+    const int group = id / (GROUP_M * tiles_n);
+    const int first_m = group * GROUP_M;
+    const int gm = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+    const int in = id % (GROUP_M * tiles_n);
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
 
-    __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * LDS_STRIDE];
+// Version with 32 x 32 x 16 MFMA tiles and an XOR-swizzled LDS layout.
+// Each LDS row of a tile holds BK = 64 bf16 (eight 16-byte chunks); chunk c
+// of row r is stored at chunk position c ^ (r % 8), so the 32 lanes that read
+// one fragment (32 consecutive rows, same logical chunk) and the 8 lanes that
+// write one row both touch 8 distinct chunk positions: no bank conflicts and
+// no padding, which lets two 128 x 128 workgroups share a CU.
+// v_mfma_f32_32x32x16_bf16 operands: lane l holds A[l % 32][8 (l / 32) + 0..7]
+// and B[8 (l / 32) + 0..7][l % 32]; result register r of lane l is
+// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int OCC, int FMT, typename TY>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
+    int K) {
+    constexpr int NT = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
+    constexpr int TM = WM / 32, TN = WN / 32;            // 32 x 32 MFMA tiles per wave
+    constexpr int A_VEC = BM * BK / 8 / NT;              // 16-byte chunks of A per thread
+    constexpr int CODES = (FMT == kW8) ? 16 : 32;        // weight codes per 16-byte load
+    constexpr int B_VEC = BN * BK / CODES / NT;
+    constexpr int B_PER_ROW = BK / CODES;
+    static_assert(A_VEC >= 1 && B_VEC >= 1 && BM * BK % (8 * NT) == 0 && BN * BK % (CODES * NT) == 0,
+                  "tile does not divide over the workgroup");
+
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * BK];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * BK];
+
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(tm, tn, tiles_m, tiles_n);
+    const int m_blk = tm * BM, n_blk = tn * BN;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
-    const int m_blk = blockIdx.y * BM, n_blk = blockIdx.x * BN;
+    const int wm = (wave / WAVES_N) * WM, wn = (wave % WAVES_N) * WN;
 
-    // global -> register staging
-    uint4 ra[A_VEC], rb[B_VEC];
-    auto load_tiles = [&](int k0) {
+    int64_t a_off[A_VEC];
+    int a_dst[A_VEC];
 #pragma unroll
-        for (int j = 0; j < A_VEC; ++j) {
-            const int i = tid + kThreads * j;
-            const int row = i / (BK / 8), c8 = i % (BK / 8);
-            int gm = m_blk + row;
-            gm = gm < M ? gm : M - 1;
-            ra[j] = *reinterpret_cast<const uint4*>(x + (int64_t)gm * ldx + k0 + c8 * 8);
-        }
+    for (int j = 0; j < A_VEC; ++j) {
+        const int i = tid + NT * j;
+        const int row = i / (BK / 8), c8 = i % (BK / 8);
+        const int gm = (m_blk + row < M) ? m_blk + row : M - 1;
+        a_off[j] = (int64_t)gm * ldx + c8 * 8;
+        a_dst[j] = swz(row, c8);
+    }
+    int64_t b_off[B_VEC];
+    int b_row[B_VEC], b_c8[B_VEC];
 #pragma unroll
-        for (int j = 0; j < B_VEC; ++j) {
-            const int i = tid + kThreads * j;
-            constexpr int PER_ROW = BK / CODES;
-            const int row = i / PER_ROW, cc = i % PER_ROW;
-            int gn = n_blk + row;
-            gn = gn < N ? gn : N - 1;
-            const int64_t byte = (FMT == kW8) ? (int64_t)k0 + cc * 16 : (int64_t)(k0 / 2) + cc * 16;
-            rb[j] = *reinterpret_cast<const uint4*>(w + (int64_t)gn * ldw + byte);
-        }
-    };
-    auto store_tiles = [&]() {
-#pragma unroll
-        for (int j = 0; j < A_VEC; ++j) {
-            const int i = tid + kThreads * j;
-            const int row = i / (BK / 8), c8 = i % (BK / 8);
-            *reinterpret_cast<uint4*>(&As[row * LDS_STRIDE + c8 * 8]) = ra[j];
-        }
-#pragma unroll
-        for (int j = 0; j < B_VEC; ++j) {
-            const int i = tid + kThreads * j;
-            constexpr int PER_ROW = BK / CODES;
-            const int row = i / PER_ROW, cc = i % PER_ROW;
-            const uint32_t d[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};
-            uint16_t* dst = &Bs[row * LDS_STRIDE + cc * CODES];
-            if (FMT == kW8) {
-                const uint2 a0 = bf16x4_of_i8x4(d[0]), a1 = bf16x4_of_i8x4(d[1]);
-                const uint2 a2 = bf16x4_of_i8x4(d[2]), a3 = bf16x4_of_i8x4(d[3]);
-                reinterpret_cast<uint4*>(dst)[0] = make_uint4(a0.x, a0.y, a1.x, a1.y);
-                reinterpret_cast<uint4*>(dst)[1] = make_uint4(a2.x, a2.y, a3.x, a3.y);
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    reinterpret_cast<uint4*>(dst)[q] =
-                        make_uint4(bf16x2_of_nibbles(d[q], 0), bf16x2_of_nibbles(d[q], 8),
-                                   bf16x2_of_nibbles(d[q], 16), bf16x2_of_nibbles(d[q], 24));
-                }
-            }
-        }
-    };
+    for (int j = 0; j < B_VEC; ++j) {
+        const int i = tid + NT * j;
+        const int row = i / B_PER_ROW, cc = i % B_PER_ROW;
+        const int gn = (n_blk + row < N) ? n_blk + row : N - 1;
+        b_off[j] = (int64_t)gn * ldw + cc * 16;
+        b_row[j] = row;
+        b_c8[j] = cc * (CODES / 8);  // first 8-column chunk this load fills
+    }
 
-    floatx4 acc[TM][TN];
+    floatx16 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    const int frag_row = lane & 15, frag_k = (lane >> 4) * 8;
-    load_tiles(0);
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        __syncthreads();  // previous step's LDS reads are done
-        store_tiles();
-        __syncthreads();
-        if (k0 + BK < K) load_tiles(k0 + BK);
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int sub = 0; sub < BK / 32; ++sub) {
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int frag_row = lane & 31, frag_c = lane >> 5;  // row in the tile, chunk within a k16 step
+    const int nk = K / BK;
+    uint4 ra[A_VEC], rb[B_VEC];
+
+#define TIQ_LOAD_TILES(k0)                                                                         \
+    {                                                                                              \
+        const int kb_ = (FMT == kW8) ? (k0) : (k0) / 2;                                            \
+        _Pragma("unroll") for (int j = 0; j < A_VEC; ++j) ra[j] =                                  \
+            *reinterpret_cast<const uint4*>(x + a_off[j] + (k0));                                  \
+        _Pragma("unroll") for (int j = 0; j < B_VEC; ++j) rb[j] =                                  \
+            *reinterpret_cast<const uint4*>(w + b_off[j] + kb_);                                   \
+    }
+#define TIQ_STORE_TILES(buf)                                                                       \
+    {                                                                                              \
+        _Pragma("unroll") for (int j = 0; j < A_VEC; ++j)                                          \
+            *reinterpret_cast<uint4*>(&As[buf][a_dst[j]]) = ra[j];                                 \
+        _Pragma("unroll") for (int j = 0; j < B_VEC; ++j) {                                        \
+            uint16_t* base = &Bs[buf][0];                                                          \
+            const int r_ = b_row[j], c_ = b_c8[j];                                                 \
+            if (FMT == kW8) {                                                                      \
+                *reinterpret_cast<uint4*>(base + swz(r_, c_)) =                                    \
+                    make_uint4(bf16x2_of_bytes(rb[j].x, 0), bf16x2_of_bytes(rb[j].x, 16),          \
+                               bf16x2_of_bytes(rb[j].y, 0), bf16x2_of_bytes(rb[j].y, 16));         \
+                *reinterpret_cast<uint4*>(base + swz(r_, c_ + 1)) =                                \
+                    make_uint4(bf16x2_of_bytes(rb[j].z, 0), bf16x2_of_bytes(rb[j].z, 16),          \
+                               bf16x2_of_bytes(rb[j].w, 0), bf16x2_of_bytes(rb[j].w, 16));         \
+            } else {                                                                               \
+                const uint32_t d_[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};                       \
+                _Pragma("unroll") for (int q = 0; q < 4; ++q)                                      \
+                    *reinterpret_cast<uint4*>(base + swz(r_, c_ + q)) =                            \
+                        make_uint4(bf16x2_of_nibbles(d_[q], 0), bf16x2_of_nibbles(d_[q], 8),       \
+                                   bf16x2_of_nibbles(d_[q], 16), bf16x2_of_nibbles(d_[q], 24));    \
+            }                                                                                      \
+        }                                                                                          \
+    }
+
+    TIQ_LOAD_TILES(0)
+    TIQ_STORE_TILES(0)
+    __syncthreads();
+    for (int s = 0; s < nk; ++s) {
+        const int buf = s & 1;
+        const int kn = (s + 1 < nk) ? (s + 1) * BK : s * BK;
+        TIQ_LOAD_TILES(kn)
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
             bf16x8 af[TM], bfr[TN];
+            const int c = 2 * kk + frag_c;
 #pragma unroll
             for (int i = 0; i < TM; ++i)
-                af[i] = *reinterpret_cast<const bf16x8*>(&As[(wm + i * 16 + frag_row) * LDS_STRIDE + sub * 32 + frag_k]);
+                af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][swz(wm + i * 32 + frag_row, c)]);
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[(wn + j * 16 + frag_row) * LDS_STRIDE + sub * 32 + frag_k]);
+                bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][swz(wn + j * 32 + frag_row, c)]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
+        TIQ_STORE_TILES(buf ^ 1)
+        __syncthreads();
     }
+#undef TIQ_LOAD_TILES
+#undef TIQ_STORE_TILES
 
-    // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each tile
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        const int n = n_blk + wn + j * 16 + (lane & 15);
+        const int n = n_blk + wn + j * 32 + (lane & 31);
         if (n >= N) continue;
         const float s = scale[n];
         const float b = bias ? bias[n] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m_blk + wm + i * 16 + (lane >> 4) * 4 + r;
+            for (int r = 0; r < 16; ++r) {
+                const int m = m_blk + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < M) {
                     const float v = fmaf(acc[i][j][r], s, b);
                     if constexpr (sizeof(TY) == 4) y[(int64_t)m * ldy + n] = v;
@@ -172,19 +223,45 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restri
     }
 }
 
-template <int BM, int BN, int FMT, typename TY>
-int run_gemm(const LinearArgs& a) {
-    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM));
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, FMT, TY>), grid, dim3(kThreads), 0, a.stream,
-                       static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, static_cast<TY*>(a.y),
-                       a.ldy, (int)a.M, (int)a.N, (int)a.K);
+template <int BM, int BN, int WMW, int WNW, int OCC, int FMT, typename TY>
+int run_gemm32(const LinearArgs& a) {
+    const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    hipLaunchKernelGGL((gemm32_kernel<BM, BN, WMW, WNW, OCC, FMT, TY>), dim3((unsigned)tiles), dim3(WMW * WNW * 64),
+                       0, a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
+                       static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K);
     return launch_status();
+}
+
+// Tile configurations, selectable for measurement through TIQ_GEMM_TILE
+// (0 = automatic).
+template <int FMT, typename TY>
+int dispatch_tile(const LinearArgs& a, int tile) {
+    switch (tile) {
+        case 1: return run_gemm32<128, 128, 2, 2, 1, FMT, TY>(a);
+        case 2: return run_gemm32<256, 128, 2, 2, 1, FMT, TY>(a);
+        case 3: return run_gemm32<128, 256, 2, 2, 1, FMT, TY>(a);
+        case 4:
+            if constexpr (FMT == kW8) return run_gemm32<256, 128, 4, 2, 1, FMT, TY>(a);
+            else return run_gemm32<256, 128, 2, 2, 1, FMT, TY>(a);
+        default: break;
+    }
+    // 128 x 128 tiles, two workgroups per CU (64 KB of LDS each)
+    return run_gemm32<128, 128, 2, 2, 2, FMT, TY>(a);
+}
+
+int tile_override() {
+    static const int t = [] {
+        const char* e = getenv("TIQ_GEMM_TILE");
+        return e ? atoi(e) : 0;
+    }();
+    return t;
 }
 
 template <int FMT>
 int dispatch_gemm(const LinearArgs& a) {
-    if (a.y_dtype == TIQ_F32) return run_gemm<128, 128, FMT, float>(a);
-    return run_gemm<128, 128, FMT, uint16_t>(a);
+    const int tile = tile_override();
+    if (a.y_dtype == TIQ_F32) return dispatch_tile<FMT, float>(a, tile);
+    return dispatch_tile<FMT, uint16_t>(a, tile);
 }
 
 }  // namespace

@@ -8,6 +8,7 @@ raises if it is missing or no ROCm GPU is visible.
 """
 
 from .config import GPT2_SIZES, GPTConfig, gpt2_config
+from .decode import GraphDecoder, generate_graph
 from .model import GPT, KVCache
 from .qlinear import QuantLinear
 from .quantization import (
@@ -29,11 +30,13 @@ __all__ = [
     "GPT",
     "GPT2_SIZES",
     "GPTConfig",
+    "GraphDecoder",
     "KVCache",
     "QuantLinear",
     "QuantResult",
     "TARGET_SUFFIXES",
     "generate",
+    "generate_graph",
     "gpt2_config",
     "pack_int4",
     "packed_size_bytes",

@@ -133,3 +133,30 @@ def test_cpu_model_is_refused(reference_decode):
     model = g.GPT(g.GPTConfig(**reference_decode["tiny"]["config"]))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         g.quantize_model(model, 8)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_graph_decode_matches_reference_tiny(reference_decode, dev, bits):
+    """The captured decode step gives the reference's tokens, and a reused
+    graph replays identically after eager work in between."""
+    e = reference_decode["tiny"]
+    qm, _ = g.quantize_model(_model(e["config"], dev), bits)
+    gr = e[f"greedy_int{bits}"]
+    prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
+    dec = g.GraphDecoder(qm, prompt.size(0), prompt.size(1) + gr["new_tokens"])
+    first = g.generate_graph(qm, prompt, gr["new_tokens"], decoder=dec)
+    assert first.cpu().tolist() == gr["ids"]
+    eager = g.generate(qm, prompt, 5)  # eager work between replays
+    torch.cuda.synchronize()
+    again = g.generate_graph(qm, prompt, gr["new_tokens"], decoder=dec)
+    assert torch.equal(first, again)
+    assert eager.cpu().tolist() == [r[: prompt.size(1) + 5] for r in gr["ids"]]
+
+
+def test_graph_decode_matches_reference_gpt2_small(reference_decode, dev):
+    e = reference_decode["gpt2_small"]
+    qm, _ = g.quantize_model(_model(e["config"], dev), 8)
+    gr = e["greedy_int8"]
+    prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
+    out = g.generate_graph(qm, prompt, gr["new_tokens"])
+    assert out.cpu().tolist() == gr["ids"]
