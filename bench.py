@@ -256,9 +256,11 @@ def decode_section(dev, repeats=3):
     prompt = torch.randint(0, 50257, (1, 64)).to(dev)
     want = golden["greedy_int8"]["ids"]
     res = {"model": "gpt2 (124M) seed 0, int8 per-channel", "prompt": 64, "new_tokens": 64}
-    dec = g.GraphDecoder(qm, 1, 128)
+    dec_t = g.GraphDecoder(qm, 1, 128)
+    dec_f = g.FusedDecoder(qm, 1, 128)
     for label, fn in (("eager", lambda: g.generate(qm, prompt, 64)),
-                      ("graph", lambda: g.generate_graph(qm, prompt, 64, decoder=dec))):
+                      ("graph_torch_ops", lambda: g.generate_graph(qm, prompt, 64, decoder=dec_t)),
+                      ("graph_fused", lambda: g.generate_graph(qm, prompt, 64, decoder=dec_f))):
         out = fn()
         match = out.cpu().tolist() == want
         ts = []

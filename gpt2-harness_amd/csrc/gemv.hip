@@ -10,13 +10,20 @@
 //     words: no bank conflicts;
 //   * each wavefront owns R weight rows; lane l streams 16-byte chunks
 //     l, l+64, ... of each row (global_load_dwordx4, fully coalesced: a
-//     wavefront instruction covers 1 KB of one row);
+//     wavefront instruction covers 1 KB of one row), four chunks per row in
+//     flight, the first ones issued before the activations are staged;
 //   * the chunk is dequantized in registers (sign-extended bytes or biased
-//     nibbles -> fp32) once and reused for all MT activation rows;
+//     nibbles -> fp32, one v_cvt_f32_i32_sdwa per int8 code) once and reused
+//     for all MT activation rows;
 //   * per-row partial sums are reduced across the wavefront with xor
 //     shuffles; the per-channel scale and the bias are applied once per
 //     output; the group-wise format scales each 32-column chunk's partial sum
 //     by its group's fp16 scale.
+// Optional fusions for the decode step of a GPT-2 block (model.py:410-427):
+// LayerNorm of the staged activation rows (two-pass mean / variance over the
+// row held in LDS), GELU(tanh) of the output (model.py:57-75) and a residual
+// added to it (x + f(x)), so one launch replaces LayerNorm + Linear + GELU or
+// Linear + add. The fp32 weight format serves the unquantized tied lm_head.
 // No MFMA: at M <= 4 the int8->fp32 convert plus M FMAs per weight byte stay
 // within the VALU budget of the HBM stream.
 #include "tiq_internal.hpp"
@@ -25,10 +32,12 @@ namespace tiq {
 namespace {
 
 constexpr int kWavesPerBlock = 8;
+constexpr int kThreads = kWavesPerBlock * 64;
 
 template <int FMT>
 struct Fmt {
-    static constexpr int KC = (FMT == kW8) ? 16 : 32;  // columns per 16-byte chunk
+    // columns per 16-byte weight chunk
+    static constexpr int KC = (FMT == kW8) ? 16 : (FMT == kF32) ? 4 : 32;
 };
 
 template <typename TX>
@@ -93,15 +102,58 @@ __device__ __forceinline__ float dot_w4(const uint4& w, const float4* xv) {
     return s;
 }
 
+// sum over the 4 columns of an fp32 chunk
+__device__ __forceinline__ float dot_f32(const uint4& w, const float4* xv) {
+    const float4 xx = xv[0];
+    float s = __uint_as_float(w.x) * xx.x;
+    s = fmaf(__uint_as_float(w.y), xx.y, s);
+    s = fmaf(__uint_as_float(w.z), xx.z, s);
+    return fmaf(__uint_as_float(w.w), xx.w, s);
+}
+
+template <int FMT>
+__device__ __forceinline__ float dot_chunk(const uint4& w, const float4* xv) {
+    if constexpr (FMT == kW8) return dot_w8(w, xv);
+    else if constexpr (FMT == kF32) return dot_f32(w, xv);
+    else return dot_w4(w, xv);
+}
+
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k = 0.7978845608028654f;
+    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+// Sum of v over the workgroup, for MT rows at once. red holds MT * 8 floats.
+template <int MT>
+__device__ __forceinline__ void block_sum(float (&v)[MT], float* red) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const float s = wave_sum(v[m]);
+        if (lane == 0) red[m * kWavesPerBlock + wave] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWavesPerBlock; ++i) s += red[m * kWavesPerBlock + i];
+        v[m] = s;
+    }
+    __syncthreads();
+}
+
 template <int MT, int R, int FMT, typename TX, typename TY>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
+__global__ __launch_bounds__(kThreads) void gemv_kernel(
     const TX* __restrict__ x, int64_t ldx, int M, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const uint16_t* __restrict__ scale16, int group,
-    const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int N, int K) {
+    const float* __restrict__ bias, TY* y, int64_t ldy, int N, int K, Fusion fz) {
     constexpr int KC = Fmt<FMT>::KC;
     constexpr int P = KC / 4;  // float4 planes per chunk
     constexpr int U = 4;       // chunks per row in flight per lane
     extern __shared__ float4 xs[];
+    __shared__ float red[MT * kWavesPerBlock];
     const int K4 = K >> 2;
     const int NC = K / KC;
     const int m0 = blockIdx.y * MT;
@@ -129,15 +181,68 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
     if (active) load_block(lane);
 
     // stage MT activation rows as fp32 planes: xs[m][p][c]
+    float rsum[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) rsum[m] = 0.f;
     for (int t = threadIdx.x; t < MT * K4; t += blockDim.x) {
         const int m = t / K4, k4 = t - m * K4;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (m0 + m < M) v = load_x4<TX>(x + (int64_t)(m0 + m) * ldx + 4 * k4);
         const int c = k4 / P, p = k4 - c * P;
         xs[m * K4 + p * NC + c] = v;
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm)
+            if (mm == m) rsum[mm] += (v.x + v.y) + (v.z + v.w);
+    }
+    if (fz.ln_w) {
+        // LayerNorm over each staged row: mean, then the mean squared
+        // deviation (biased, as torch), then normalise in place.
+        block_sum<MT>(rsum, red);
+        float mean[MT], dev[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            mean[m] = rsum[m] / (float)K;
+            dev[m] = 0.f;
+        }
+        for (int t = threadIdx.x; t < MT * K4; t += blockDim.x) {
+            const int m = t / K4, k4 = t - m * K4;
+            const int c = k4 / P, p = k4 - c * P;
+            const float4 v = xs[m * K4 + p * NC + c];
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) {
+                if (mm == m) {
+                    const float a = v.x - mean[mm], b = v.y - mean[mm], cc = v.z - mean[mm], d = v.w - mean[mm];
+                    dev[mm] += (a * a + b * b) + (cc * cc + d * d);
+                }
+            }
+        }
+        block_sum<MT>(dev, red);
+        float rstd[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) rstd[m] = 1.0f / sqrtf(dev[m] / (float)K + fz.ln_eps);
+        for (int t = threadIdx.x; t < MT * K4; t += blockDim.x) {
+            const int m = t / K4, k4 = t - m * K4;
+            const int c = k4 / P, p = k4 - c * P;
+            float4 v = xs[m * K4 + p * NC + c];
+            float mu = 0.f, rs = 0.f;
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm)
+                if (mm == m) {
+                    mu = mean[mm];
+                    rs = rstd[mm];
+                }
+            const float4 g = *reinterpret_cast<const float4*>(fz.ln_w + 4 * k4);
+            const float4 b = *reinterpret_cast<const float4*>(fz.ln_b + 4 * k4);
+            v.x = (v.x - mu) * rs * g.x + b.x;
+            v.y = (v.y - mu) * rs * g.y + b.y;
+            v.z = (v.z - mu) * rs * g.z + b.z;
+            v.w = (v.w - mu) * rs * g.w + b.w;
+            if (m0 + m >= M) v = make_float4(0.f, 0.f, 0.f, 0.f);
+            xs[m * K4 + p * NC + c] = v;
+        }
     }
     __syncthreads();
-    if (!active) return;  // after the only barrier
+    if (!active) return;  // after the last barrier
 
     float acc[R][MT];
 #pragma unroll
@@ -171,7 +276,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
                 for (int p = 0; p < P; ++p) xv[p] = xs[m * K4 + p * NC + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float part = (FMT == kW8) ? dot_w8(cur[u][r], xv) : dot_w4(cur[u][r], xv);
+                    const float part = dot_chunk<FMT>(cur[u][r], xv);
                     if (FMT == kW4G) acc[r][m] = fmaf(gs[r], part, acc[r][m]);
                     else acc[r][m] += part;
                 }
@@ -191,8 +296,10 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void gemv_kernel(
         for (int m = 0; m < MT; ++m) {
             if (lane == r * MT + m && n < N && m0 + m < M) {
                 float v = acc[r][m];
-                if (FMT != kW4G) v *= scale[n];
+                if (FMT == kW8 || FMT == kW4) v *= scale[n];
                 if (bias) v += bias[n];
+                if (fz.act == 1) v = gelu_tanh(v);
+                if (fz.res) v += fz.res[(int64_t)(m0 + m) * fz.ldr + n];
                 store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
             }
         }
@@ -222,6 +329,8 @@ __global__ __launch_bounds__(256) void gemv_generic(const TX* __restrict__ x, in
         float wv;
         if (FMT == kW8) {
             wv = (float)(int8_t)wr[k];
+        } else if (FMT == kF32) {
+            wv = reinterpret_cast<const float*>(wr)[k];
         } else {
             const uint8_t b = wr[k >> 1];
             wv = (float)((int)((k & 1) ? (b >> 4) : (b & 0xf)) - 8);
@@ -231,7 +340,7 @@ __global__ __launch_bounds__(256) void gemv_generic(const TX* __restrict__ x, in
     }
     s = wave_sum(s);
     if (lane == 0) {
-        if (FMT != kW4G) s *= scale[n];
+        if (FMT == kW8 || FMT == kW4) s *= scale[n];
         if (bias) s += bias[n];
         store_y<TY>(y + (int64_t)m * ldy + n, s);
     }
@@ -244,9 +353,9 @@ int run_gemv(const LinearArgs& a) {
     const int N = (int)a.N, K = (int)a.K, M = (int)a.M;
     const size_t lds = (size_t)MT * K * sizeof(float);
     const dim3 grid((unsigned)((N + kWavesPerBlock * R - 1) / (kWavesPerBlock * R)), (unsigned)((M + MT - 1) / MT));
-    hipLaunchKernelGGL((gemv_kernel<MT, R, FMT, TX, TY>), grid, dim3(kWavesPerBlock * 64), lds, a.stream,
+    hipLaunchKernelGGL((gemv_kernel<MT, R, FMT, TX, TY>), grid, dim3(kThreads), lds, a.stream,
                        static_cast<const TX*>(a.x), a.ldx, M, a.w, a.ldw, a.scale, a.scale16, a.group, a.bias,
-                       static_cast<TY*>(a.y), a.ldy, N, K);
+                       static_cast<TY*>(a.y), a.ldy, N, K, a.fuse);
     return launch_status();
 }
 
@@ -263,10 +372,15 @@ template <int FMT, typename TX, typename TY>
 int dispatch_fmt(const LinearArgs& a) {
     constexpr int KC = Fmt<FMT>::KC;
     const size_t xb = (a.x_dtype == TIQ_F32) ? 16 : 8;
-    const bool vec = (a.K % KC == 0) && aligned(a.w, 16) && (a.ldw % 16 == 0) && aligned(a.x, xb) &&
-                     (a.ldx % 4 == 0) && (FMT != kW4G || a.group % KC == 0) && a.K * sizeof(float) <= kMaxLds &&
-                     a.N <= 0x7fffffff;
-    if (!vec) return run_generic<FMT, TX, TY>(a);
+    const bool fused = a.fuse.ln_w || a.fuse.act || a.fuse.res;
+    const bool vec = (a.K % KC == 0) && (a.K % 4 == 0) && aligned(a.w, 16) && (a.ldw % 16 == 0) &&
+                     aligned(a.x, xb) && (a.ldx % 4 == 0) && (FMT != kW4G || a.group % KC == 0) &&
+                     a.K * sizeof(float) <= kMaxLds && a.N <= 0x7fffffff &&
+                     (!a.fuse.ln_w || (aligned(a.fuse.ln_w, 16) && aligned(a.fuse.ln_b, 16)));
+    if (!vec) {
+        if (fused) return TIQ_EUNSUPPORTED;
+        return run_generic<FMT, TX, TY>(a);
+    }
     const size_t row_lds = (size_t)a.K * sizeof(float);
     int mt = 4;
     while (mt > 1 && (size_t)mt * row_lds > kMaxLds) mt >>= 1;
@@ -295,6 +409,7 @@ int launch_gemv(const LinearArgs& a) {
         case kW8: return dispatch_types<kW8>(a);
         case kW4: return dispatch_types<kW4>(a);
         case kW4G: return dispatch_types<kW4G>(a);
+        case kF32: return dispatch_types<kF32>(a);
     }
     return TIQ_EINVAL;
 }

@@ -111,6 +111,31 @@ extern "C" int tiq_linear_w4(const void* x, int x_dtype, int64_t M, int64_t K, i
                                 stream, kW4));
 }
 
+extern "C" int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w,
+                                int w_format, const float* scale, const uint16_t* scale_f16, int group,
+                                const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                                const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                                const float* residual, int64_t ld_residual, void* stream) {
+    if (w_format < TIQ_WF_INT8 || w_format > TIQ_WF_F32) return TIQ_EINVAL;
+    if (activation != TIQ_ACT_NONE && activation != TIQ_ACT_GELU_TANH) return TIQ_EINVAL;
+    if ((ln_weight == nullptr) != (ln_bias == nullptr)) return TIQ_EINVAL;
+    if (residual && ld_residual < N) return TIQ_EINVAL;
+    const WFormat fmt = (WFormat)w_format;
+    const int64_t ldw = fmt == kW8 ? K : fmt == kW4 ? K / 2 : fmt == kW4G ? (K + 1) / 2 : K * 4;
+    if (fmt == kF32 && scale == nullptr) scale = reinterpret_cast<const float*>(w);  // unused, keeps checks simple
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, static_cast<const uint8_t*>(w), ldw, scale, scale_f16, group,
+                             bias, N, y, y_dtype, ldy, stream, fmt);
+    a.fuse.ln_w = ln_weight;
+    a.fuse.ln_b = ln_bias;
+    a.fuse.ln_eps = ln_eps;
+    a.fuse.act = activation;
+    a.fuse.res = residual;
+    a.fuse.ldr = ld_residual;
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    return launch_gemv(a);
+}
+
 extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                               const uint16_t* scale_f16, int group, const float* bias, int64_t N, void* y,
                               int y_dtype, int64_t ldy, void* stream) {

@@ -10,6 +10,18 @@ enum WFormat : int {
     kW8 = 0,   // int8 codes, row n at byte n * ldw
     kW4 = 1,   // reference nibble layout, row n at byte n * K / 2 (K even)
     kW4G = 2,  // group-wise nibbles, row n at byte n * ((K + 1) / 2), fp16 group scales
+    kF32 = 3,  // fp32 weights (an unquantized Linear such as the tied lm_head), no scale
+};
+
+// Optional work fused around a decode GEMV: LayerNorm of the activation rows
+// before the product, GELU(tanh) after it, and a residual added to the output.
+struct Fusion {
+    const float* ln_w = nullptr;  // LayerNorm weight (K), enables the prologue
+    const float* ln_b = nullptr;  // LayerNorm bias (K)
+    float ln_eps = 1e-5f;
+    int act = 0;                  // 0 none, 1 gelu_tanh
+    const float* res = nullptr;   // residual (M, N) with leading dim ldr, added last
+    int64_t ldr = 0;
 };
 
 struct LinearArgs {
@@ -28,6 +40,7 @@ struct LinearArgs {
     int64_t ldy;
     hipStream_t stream;
     WFormat fmt;
+    Fusion fuse;
 };
 
 // Validates the common arguments; TIQ_OK when they are consistent.

@@ -8,7 +8,7 @@ raises if it is missing or no ROCm GPU is visible.
 """
 
 from .config import GPT2_SIZES, GPTConfig, gpt2_config
-from .decode import GraphDecoder, generate_graph
+from .decode import FusedDecoder, GraphDecoder, generate_graph, make_decoder
 from .model import GPT, KVCache
 from .qlinear import QuantLinear
 from .quantization import (
@@ -29,6 +29,7 @@ from .sampling import generate
 __all__ = [
     "GPT",
     "GPT2_SIZES",
+    "FusedDecoder",
     "GPTConfig",
     "GraphDecoder",
     "KVCache",
@@ -38,6 +39,7 @@ __all__ = [
     "generate",
     "generate_graph",
     "gpt2_config",
+    "make_decoder",
     "pack_int4",
     "packed_size_bytes",
     "perplexity_with_error_bars",

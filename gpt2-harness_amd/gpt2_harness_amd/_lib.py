@@ -40,7 +40,15 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_gemm_w8": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_linear_w4": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_linear_w4g": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
+    "tiq_linear_fused": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
+                          _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp], _i32),
+    "tiq_decode_attention": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _i32),
+    "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
+    "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp], _i32),
 }
+
+WF_INT8, WF_INT4, WF_INT4G, WF_F32 = 0, 1, 2, 3
+ACT_NONE, ACT_GELU_TANH = 0, 1
 
 _LIB: ctypes.CDLL | None = None
 

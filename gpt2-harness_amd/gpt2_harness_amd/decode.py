@@ -4,21 +4,24 @@ The reference's ``generate`` (``sampling.py:100-181``) runs one Python-level
 forward pass per token over a ``torch.cat``-grown cache (``model.py:153-172``):
 every op is a separate launch issued from the host. Here the prompt is
 processed by the model's ordinary forward (prefill), and every later token by
-one replay of a captured HIP graph that holds the whole decode step:
+one replay of a captured HIP graph holding the whole decode step. The KV cache
+is preallocated, ``(B, kv_heads, T_max, head_dim)`` per layer, and the fill
+level is a device scalar, so the captured step is the same for every token.
 
-* the KV cache is preallocated, ``(B, kv_heads, T_max, head_dim)`` per layer,
-  and the new key / value are written at the current position (a device
-  tensor, so the graph does not change from step to step);
-* attention runs over all ``T_max`` cache slots with the slots after the
-  current position masked to ``-inf`` before the softmax, which gives them
-  probability exactly 0 -- the reference's attention over the ``T_total``
-  filled slots (``model.py:286-309``);
-* the quantized Linears are the HIP kernels (launched on the capture stream);
-* greedy ``argmax`` picks the next token, which is written to the output ids
-  and fed to the next replay; the position advances inside the graph.
+Two step implementations:
 
-Token ids are the reference's; the logits agree with an eager forward to fp32
-rounding (the matmuls see padded shapes).
+* :class:`FusedDecoder` (used when the model fits: four quantized Linears per
+  block, pre-LN, learned positions, ``gelu_tanh``, head_dim 64, fp32 tied
+  head): the library's decode kernels only -- an embedding kernel, then per
+  block LayerNorm+``c_attn``, attention over the cache, ``c_proj``+residual,
+  LayerNorm+``c_fc``+GELU, ``c_proj``+residual (5 launches), then
+  LayerNorm+``lm_head`` and ``argmax`` -- 5 * n_layer + 4 launches per token;
+* :class:`GraphDecoder`: the model's own modules as torch ops with attention
+  over all ``T_max`` slots, the slots after the current position masked to
+  ``-inf`` (probability exactly 0), for any other model layout.
+
+Greedy token ids are the reference's; logits agree with an eager forward to
+fp32 rounding.
 """
 
 from __future__ import annotations
@@ -28,14 +31,13 @@ import math
 import torch
 import torch.nn.functional as F
 
-__all__ = ["GraphDecoder", "generate_graph"]
+from . import _lib
+from .qlinear import FMT_W4, FMT_W4G, FMT_W8, QuantLinear
+
+__all__ = ["FusedDecoder", "GraphDecoder", "generate_graph", "make_decoder"]
 
 
-class GraphDecoder:
-    """Captures one decode step of ``model`` for ``batch`` sequences of up to
-    ``max_len`` positions. ``model`` is a GPT with the reference's module
-    layout (pre-LN or post-LN, learned or sinusoidal positions) on a GPU."""
-
+class _DecoderBase:
     def __init__(self, model, batch: int, max_len: int) -> None:
         cfg = model.config
         if max_len > cfg.n_positions:
@@ -44,18 +46,16 @@ class GraphDecoder:
         self.cfg = cfg
         self.B, self.T = batch, max_len
         dev = next(model.parameters()).device
+        _lib.require_gpu(next(model.parameters()), "model parameters")
         self.dev = dev
-        H, Hkv, hd = cfg.n_head, cfg.kv_heads, cfg.head_dim
-        self.H, self.Hkv, self.hd = H, Hkv, hd
-        self.k = [torch.zeros(batch, Hkv, max_len, hd, device=dev) for _ in range(cfg.n_layer)]
-        self.v = [torch.zeros(batch, Hkv, max_len, hd, device=dev) for _ in range(cfg.n_layer)]
+        self.H, self.Hkv, self.hd = cfg.n_head, cfg.kv_heads, cfg.head_dim
+        self.k = [torch.zeros(batch, self.Hkv, max_len, self.hd, device=dev) for _ in range(cfg.n_layer)]
+        self.v = [torch.zeros(batch, self.Hkv, max_len, self.hd, device=dev) for _ in range(cfg.n_layer)]
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)        # position of the token being fed
         self.tok = torch.zeros(batch, 1, dtype=torch.long, device=dev)  # token being fed
         self.out = torch.zeros(batch, max_len, dtype=torch.long, device=dev)
-        self.slots = torch.arange(max_len, device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
 
-    # ------------------------------------------------------------ prefill
     @torch.no_grad()
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:
         """Run the prompt through the model's own forward, filling the cache.
@@ -73,46 +73,8 @@ class GraphDecoder:
         self.out[:, :T0].copy_(idx)
         return logits
 
-    # ------------------------------------------------------------ one step
-    def _step(self) -> None:
-        m, cfg = self.model, self.cfg
-        B, H, Hkv, hd, C = self.B, self.H, self.Hkv, self.hd, cfg.n_embd
-        pos = self.pos
-        x = m.wte(self.tok) + m.position_embeddings(pos.view(1, 1).expand(B, 1))
-        visible = (self.slots <= pos).view(1, 1, 1, self.T)
-        pre = cfg.norm_position == "pre"
-        for i, block in enumerate(m.h):
-            attn = block.attn
-            h = block.ln_1(x) if pre else x
-            q, k, v = attn.c_attn(h).split([C, Hkv * hd, Hkv * hd], dim=2)
-            q = q.view(B, 1, H, hd).transpose(1, 2)
-            k = k.view(B, 1, Hkv, hd).transpose(1, 2)
-            v = v.view(B, 1, Hkv, hd).transpose(1, 2)
-            self.k[i].index_copy_(2, pos, k)
-            self.v[i].index_copy_(2, pos, v)
-            K, V = self.k[i], self.v[i]
-            if Hkv != H:
-                K = K.repeat_interleave(H // Hkv, dim=1)
-                V = V.repeat_interleave(H // Hkv, dim=1)
-            att = (q @ K.transpose(-2, -1)) / math.sqrt(hd)
-            att = att.masked_fill(~visible, float("-inf"))
-            att = F.softmax(att, dim=-1)
-            if attn.head_mask is not None:
-                y = (att @ V) * attn.head_mask.to(att.device, att.dtype).view(1, -1, 1, 1)
-            else:
-                y = att @ V
-            a = attn.c_proj(y.transpose(1, 2).contiguous().view(B, 1, C))
-            if pre:
-                x = x + a
-                x = x + block.mlp(block.ln_2(x))
-            else:
-                x = block.ln_1(x + a)
-                x = block.ln_2(x + block.mlp(x))
-        logits = m.lm_head(m.ln_f(x))[:, -1, :]
-        nxt = logits.argmax(dim=-1, keepdim=True)
-        self.tok.copy_(nxt)
-        self.pos.add_(1)
-        self.out.index_copy_(1, pos, nxt)  # pos was advanced: writes slot of the new token
+    def _step(self) -> None:  # pragma: no cover - provided by subclasses
+        raise NotImplementedError
 
     @torch.no_grad()
     def capture(self) -> None:
@@ -150,11 +112,149 @@ class GraphDecoder:
         return self.out[:, : T0 + n].clone()
 
 
+class GraphDecoder(_DecoderBase):
+    """Decode step from the model's own modules (any reference layout)."""
+
+    def __init__(self, model, batch: int, max_len: int) -> None:
+        super().__init__(model, batch, max_len)
+        self.slots = torch.arange(max_len, device=self.dev)
+
+    def _step(self) -> None:
+        m, cfg = self.model, self.cfg
+        B, H, Hkv, hd, C = self.B, self.H, self.Hkv, self.hd, cfg.n_embd
+        pos = self.pos
+        x = m.wte(self.tok) + m.position_embeddings(pos.view(1, 1).expand(B, 1))
+        visible = (self.slots <= pos).view(1, 1, 1, self.T)
+        pre = cfg.norm_position == "pre"
+        for i, block in enumerate(m.h):
+            attn = block.attn
+            h = block.ln_1(x) if pre else x
+            q, k, v = attn.c_attn(h).split([C, Hkv * hd, Hkv * hd], dim=2)
+            q = q.view(B, 1, H, hd).transpose(1, 2)
+            k = k.view(B, 1, Hkv, hd).transpose(1, 2)
+            v = v.view(B, 1, Hkv, hd).transpose(1, 2)
+            self.k[i].index_copy_(2, pos, k)
+            self.v[i].index_copy_(2, pos, v)
+            K, V = self.k[i], self.v[i]
+            if Hkv != H:
+                K = K.repeat_interleave(H // Hkv, dim=1)
+                V = V.repeat_interleave(H // Hkv, dim=1)
+            att = (q @ K.transpose(-2, -1)) / math.sqrt(hd)
+            att = att.masked_fill(~visible, float("-inf"))
+            att = F.softmax(att, dim=-1)
+            y = att @ V
+            if attn.head_mask is not None:
+                y = y * attn.head_mask.to(att.device, att.dtype).view(1, -1, 1, 1)
+            a = attn.c_proj(y.transpose(1, 2).contiguous().view(B, 1, C))
+            if pre:
+                x = x + a
+                x = x + block.mlp(block.ln_2(x))
+            else:
+                x = block.ln_1(x + a)
+                x = block.ln_2(x + block.mlp(x))
+        logits = m.lm_head(m.ln_f(x))[:, -1, :]
+        nxt = logits.argmax(dim=-1, keepdim=True)
+        self.tok.copy_(nxt)
+        self.pos.add_(1)
+        self.out.index_copy_(1, pos, nxt)  # pos was advanced: the new token's slot
+
+
+_WF = {FMT_W8: _lib.WF_INT8, FMT_W4: _lib.WF_INT4, FMT_W4G: _lib.WF_INT4G}
+
+
+def fused_supported(model) -> str | None:
+    """``None`` when :class:`FusedDecoder` can run ``model``, else the reason."""
+    cfg = model.config
+    if cfg.norm_position != "pre" or cfg.pos_embedding != "learned" or cfg.activation != "gelu_tanh":
+        return "needs pre-LN, learned positions and gelu_tanh"
+    if cfg.head_dim != 64 or cfg.n_positions > 1024:
+        return "needs head_dim 64 and n_positions <= 1024"
+    if cfg.n_embd % 32:
+        return "needs n_embd % 32 == 0"
+    for block in model.h:
+        for lin in (block.attn.c_attn, block.attn.c_proj, block.mlp.c_fc, block.mlp.c_proj):
+            if not isinstance(lin, QuantLinear):
+                return "every target Linear must be quantized"
+        if block.attn.head_mask is not None or block.mlp.neuron_mask is not None:
+            return "head / neuron masks are not fused"
+    w = model.lm_head.weight
+    if w.dtype != torch.float32 or model.lm_head.bias is not None or model.wte.weight.dtype != torch.float32:
+        return "needs an fp32 bias-free lm_head"
+    return None
+
+
+class FusedDecoder(_DecoderBase):
+    """Decode step built from the library's fused decode kernels."""
+
+    def __init__(self, model, batch: int, max_len: int) -> None:
+        why = fused_supported(model)
+        if why is not None:
+            raise ValueError(f"fused decode unavailable: {why}")
+        super().__init__(model, batch, max_len)
+        cfg, dev, B = self.cfg, self.dev, batch
+        C = cfg.n_embd
+        self.x = torch.zeros(B, C, device=dev)
+        self.qkv = torch.zeros(B, C + 2 * self.Hkv * self.hd, device=dev)
+        self.att = torch.zeros(B, C, device=dev)
+        self.hid = torch.zeros(B, model.h[0].mlp.c_fc.out_features, device=dev)
+        self.logits = torch.zeros(B, cfg.vocab_size, device=dev)
+        self.tok_flat = self.tok.view(-1)
+        self.head_w = model.lm_head.weight.detach().contiguous()
+        self.L = _lib.lib()
+
+    def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
+        M, K = x.shape
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        scale16 = lin.scale.data_ptr() if lin.fmt == FMT_W4G else None
+        scale = None if lin.fmt == FMT_W4G else lin.scale.data_ptr()
+        rc = self.L.tiq_linear_fused(
+            x.data_ptr(), _lib.F32, M, K, x.stride(0), lin.codes.data_ptr(), _WF[lin.fmt], scale, scale16,
+            lin.group_size, _lib.ptr(lin.bias), lin.out_features, y.data_ptr(), _lib.F32, y.stride(0),
+            None if ln is None else ln.weight.data_ptr(), None if ln is None else ln.bias.data_ptr(),
+            float(ln.eps) if ln is not None else 1e-5, act, None if res is None else res.data_ptr(),
+            0 if res is None else res.stride(0), st)
+        _lib.check(rc, "fused decode linear")
+
+    def _step(self) -> None:
+        m, cfg, L = self.model, self.cfg, self.L
+        B, C = self.B, cfg.n_embd
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        _lib.check(L.tiq_embed_tokens(self.tok_flat.data_ptr(), self.pos.data_ptr(), m.wte.weight.data_ptr(),
+                                      cfg.vocab_size, m.wpe.weight.data_ptr(), cfg.n_positions, B, C,
+                                      self.x.data_ptr(), st), "embed")
+        for i, block in enumerate(m.h):
+            attn, mlp = block.attn, block.mlp
+            self._linear(attn.c_attn, self.x, self.qkv, ln=block.ln_1)
+            _lib.check(L.tiq_decode_attention(self.qkv.data_ptr(), self.qkv.stride(0), B, self.H, self.Hkv, self.hd,
+                                              self.k[i].data_ptr(), self.v[i].data_ptr(), self.T,
+                                              self.pos.data_ptr(), self.att.data_ptr(), self.att.stride(0), st),
+                       "decode attention")
+            self._linear(attn.c_proj, self.att, self.x, res=self.x)
+            self._linear(mlp.c_fc, self.x, self.hid, ln=block.ln_2, act=_lib.ACT_GELU_TANH)
+            self._linear(mlp.c_proj, self.hid, self.x, res=self.x)
+        ln = m.ln_f
+        rc = L.tiq_linear_fused(self.x.data_ptr(), _lib.F32, B, C, C, self.head_w.data_ptr(), _lib.WF_F32, None,
+                                None, 0, None, cfg.vocab_size, self.logits.data_ptr(), _lib.F32, cfg.vocab_size,
+                                ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps), 0, None, 0, st)
+        _lib.check(rc, "lm_head")
+        _lib.check(L.tiq_argmax_rows(self.logits.data_ptr(), B, cfg.vocab_size, cfg.vocab_size,
+                                     self.tok_flat.data_ptr(), self.out.data_ptr(), self.T, self.pos.data_ptr(), st),
+                   "argmax")
+        self.pos.add_(1)
+
+
+def make_decoder(model, batch: int, max_len: int):
+    """The fused decoder when the model fits it, else the torch-op one."""
+    if fused_supported(model) is None:
+        return FusedDecoder(model, batch, max_len)
+    return GraphDecoder(model, batch, max_len)
+
+
 @torch.no_grad()
-def generate_graph(model, idx: torch.Tensor, max_new_tokens: int, decoder: GraphDecoder | None = None):
+def generate_graph(model, idx: torch.Tensor, max_new_tokens: int, decoder=None):
     """Greedy generation with a captured decode step; the same token ids as
     ``generate(model, idx, max_new_tokens)``. Pass a ``decoder`` built for
     this batch / length to reuse its captured graph across calls."""
     if decoder is None:
-        decoder = GraphDecoder(model, idx.size(0), min(model.config.n_positions, idx.size(1) + max_new_tokens))
+        decoder = make_decoder(model, idx.size(0), min(model.config.n_positions, idx.size(1) + max_new_tokens))
     return decoder.run(idx, max_new_tokens)

@@ -40,6 +40,12 @@ enum tiq_status {
 
 enum tiq_dtype { TIQ_F32 = 0, TIQ_BF16 = 1 };
 
+/* Weight storage formats accepted by tiq_linear_fused. */
+enum tiq_weight_format { TIQ_WF_INT8 = 0, TIQ_WF_INT4 = 1, TIQ_WF_INT4_GROUPWISE = 2, TIQ_WF_F32 = 3 };
+
+/* Activations fused after a linear. */
+enum tiq_activation { TIQ_ACT_NONE = 0, TIQ_ACT_GELU_TANH = 1 };
+
 /* Library version (major*10000 + minor*100 + patch). */
 int tiq_version(void);
 /* Static string naming a status code (never NULL). */
@@ -142,6 +148,54 @@ int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx
                    const uint8_t* packed, const uint16_t* scale_f16, int group,
                    const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
                    void* stream);
+
+/* ------------------------------------------------------- decode step
+ * Kernels of one GPT-2 decode step (one token per sequence) over a
+ * preallocated KV cache whose fill level `pos` is a device int64 scalar, so
+ * the step is the same sequence of launches for every token (capturable in a
+ * HIP graph). Device-side values (pos, token ids) are range-checked in the
+ * kernels: an out-of-range value yields NaN outputs, never an out-of-bounds
+ * access.
+ */
+
+/* The fused decode linear, for M <= a few rows (the GEMV path):
+ *   y = act(LayerNorm(x) @ W^T * scale + bias) + residual
+ * Replaces Block.forward's ln_1 -> attn.c_attn, ln_2 -> mlp.c_fc -> gelu_tanh,
+ * and the residual adds x + attn(..), x + mlp(..) (model.py:410-427,57-75,
+ * 351-355). ln_weight/ln_bias NULL: no LayerNorm (else both given, eps
+ * ln_eps, statistics over the K inputs of each row); activation
+ * TIQ_ACT_NONE or TIQ_ACT_GELU_TANH; residual NULL or (M, N) with leading dim
+ * ld_residual (may alias y: the update is in place). w_format selects the
+ * layout of w: TIQ_WF_INT8 / TIQ_WF_INT4 (per-row fp32 scale),
+ * TIQ_WF_INT4_GROUPWISE (fp16 group scales), TIQ_WF_F32 (fp32 weights, scale
+ * ignored: the unquantized tied lm_head, model.py:585). Needs K % 32 == 0,
+ * K * 4 <= 65536 and 16-byte aligned rows; returns TIQ_EUNSUPPORTED otherwise. */
+int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w,
+                     int w_format, const float* scale, const uint16_t* scale_f16, int group,
+                     const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                     const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                     const float* residual, int64_t ld_residual, void* stream);
+
+/* Self-attention of one new token per sequence (model.py:248-318 at T = 1,
+ * KVCache.update model.py:153-172): qkv is the (batch, (n_head + 2 n_kv_head)
+ * * head_dim) output of c_attn (leading dim ld_qkv); its k and v are written
+ * into k_cache / v_cache ((batch, n_kv_head, t_max, head_dim) fp32) at slot
+ * *pos; the query attends to slots 0..*pos with softmax(q k^T / sqrt(hd));
+ * y (batch, n_head * head_dim) gets the head outputs. head_dim must be 64,
+ * t_max <= 1024. */
+int tiq_decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head, int64_t n_kv_head,
+                         int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
+                         float* y, int64_t ldy, void* stream);
+
+/* x[b] = wte[tokens[b]] + wpe[*pos]  (model.py:561-564 for one position). */
+int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte, int64_t vocab,
+                     const float* wpe, int64_t n_positions, int64_t batch, int64_t n_embd, float* x,
+                     void* stream);
+
+/* out[r] = argmax of row r of x (first index of the maximum; sampling.py:164).
+ * If ids is not NULL the index is also written to ids[r * ld_ids + *pos + 1]. */
+int tiq_argmax_rows(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t* out, int64_t* ids,
+                    int64_t ld_ids, const int64_t* pos, void* stream);
 
 #ifdef __cplusplus
 }

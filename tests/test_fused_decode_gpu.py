@@ -1,0 +1,195 @@
+"""The fused decode-step kernels (C ABI) against torch fp32 computations of the
+same reference ops, and the fused decoder end to end.
+
+* ``tiq_linear_fused``: LayerNorm prologue (``model.py:413,422``), GELU(tanh)
+  epilogue (``model.py:57-75``), residual add in place (``model.py:419,427``),
+  fp32 weights (the tied ``lm_head``, ``model.py:585``) -- within the 1e-3
+  output contract;
+* ``tiq_decode_attention``: one query over the cache (``model.py:286-309`` at
+  T = 1) -- within fp32 rounding of torch's softmax attention;
+* ``tiq_embed_tokens`` exact; ``tiq_argmax_rows`` exact, first index on ties;
+* a position outside the cache yields NaN outputs (no access out of bounds);
+* greedy tokens of the fused decoder equal the reference's (GPT-2 small int8)
+  and the eager path's (int4, group-wise int4).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import gpt2_harness_amd as g
+from gpt2_harness_amd import _lib
+from oracle import linear as OL
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _gelu(x):
+    return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x.pow(3))))
+
+
+@pytest.mark.parametrize("M", [1, 3, 4, 8])
+@pytest.mark.parametrize("K,N", [(768, 2304), (1600, 6400), (3072, 768)])
+def test_fused_ln_gelu_linear(dev, c_oracle, M, K, N):
+    gen = torch.Generator().manual_seed(M * 7 + K)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen) * 2 + 0.5
+    lw = 1 + 0.1 * torch.randn(K, generator=gen)
+    lb = 0.1 * torch.randn(K, generator=gen)
+    b = 0.1 * torch.randn(N, generator=gen)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    y = torch.empty(M, N, device=dev)
+    # device copies stay referenced until the kernel has run
+    xd, qd, sd, bd = x.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
+    lwd, lbd = lw.to(dev), lb.to(dev)
+    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
+                                     bd.data_ptr(), N, y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5,
+                                     _lib.ACT_GELU_TANH, None, 0, _st())
+    _lib.check(rc, "fused")
+    ref = _gelu(OL.linear_ref(F.layer_norm(x, (K,), lw, lb, 1e-5), OL.dequantize(q, s), b))
+    ok, err, bound = OL.within_tolerance(y, ref)
+    assert ok, (err, bound)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_fused_residual_in_place_and_int4(dev, c_oracle, M):
+    K, N = 3072, 768
+    gen = torch.Generator().manual_seed(3)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    h = torch.randn(M, K, generator=gen)
+    x0 = torch.randn(M, N, generator=gen)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 4)
+    packed = torch.from_numpy(c_oracle.pack_int4(q)).to(dev)
+    x = x0.to(dev).clone()
+    hd, sd = h.to(dev), torch.from_numpy(s.reshape(-1)).to(dev)
+    rc = _lib.lib().tiq_linear_fused(hd.data_ptr(), 0, M, K, K, packed.data_ptr(), _lib.WF_INT4, sd.data_ptr(), None,
+                                     0, None, N, x.data_ptr(), 0, N, None, None, 1e-5, 0, x.data_ptr(), N, _st())
+    _lib.check(rc, "fused residual")
+    ref = x0 + OL.linear_ref(h, OL.dequantize(q, s))
+    assert (x.cpu() - ref).abs().max() <= 1e-3 * ref.abs().max()
+
+
+def test_fused_f32_head_with_ln(dev):
+    K, N, M = 768, 50257, 2
+    gen = torch.Generator().manual_seed(4)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen)
+    y = torch.empty(M, N, device=dev)
+    lw, lb = torch.ones(K), torch.zeros(K)
+    xd, wd, lwd, lbd = x.to(dev), w.to(dev), lw.to(dev), lb.to(dev)
+    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, wd.data_ptr(), _lib.WF_F32, None, None, 0, None, N,
+                                     y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5, 0, None, 0, _st())
+    _lib.check(rc, "head")
+    ref = F.linear(F.layer_norm(x, (K,), lw, lb, 1e-5), w)
+    assert (y.cpu() - ref).abs().max() <= 1e-4 * ref.abs().max()
+
+
+@pytest.mark.parametrize("B,H,Hkv,pos", [(1, 12, 12, 0), (1, 12, 12, 127), (3, 25, 25, 200), (2, 8, 2, 63)])
+def test_decode_attention(dev, B, H, Hkv, pos):
+    hd, T = 64, 256
+    gen = torch.Generator().manual_seed(pos + H)
+    qkv = torch.randn(B, (H + 2 * Hkv) * hd, generator=gen)
+    kc = torch.randn(B, Hkv, T, hd, generator=gen)
+    vc = torch.randn(B, Hkv, T, hd, generator=gen)
+    kd, vd = kc.to(dev), vc.to(dev)
+    p = torch.tensor([pos], device=dev)
+    y = torch.empty(B, H * hd, device=dev)
+    qkvd = qkv.to(dev)
+    rc = _lib.lib().tiq_decode_attention(qkvd.data_ptr(), qkv.shape[1], B, H, Hkv, hd, kd.data_ptr(),
+                                         vd.data_ptr(), T, p.data_ptr(), y.data_ptr(), H * hd, _st())
+    _lib.check(rc, "attention")
+    q = qkv[:, : H * hd].view(B, H, 1, hd)
+    knew = qkv[:, H * hd : (H + Hkv) * hd].view(B, Hkv, hd)
+    vnew = qkv[:, (H + Hkv) * hd :].view(B, Hkv, hd)
+    kc[:, :, pos] = knew
+    vc[:, :, pos] = vnew
+    K = kc[:, :, : pos + 1].repeat_interleave(H // Hkv, dim=1)
+    V = vc[:, :, : pos + 1].repeat_interleave(H // Hkv, dim=1)
+    ref = (F.softmax((q @ K.transpose(-2, -1)) / math.sqrt(hd), dim=-1) @ V).view(B, H * hd)
+    assert (y.cpu() - ref).abs().max() < 2e-5
+    assert torch.equal(kd.cpu()[:, :, pos], knew) and torch.equal(vd.cpu()[:, :, pos], vnew)
+    assert torch.equal(kd.cpu()[:, :, pos + 1 :], kc[:, :, pos + 1 :])
+
+
+def test_out_of_range_position_gives_nan_without_writes(dev):
+    B, H, hd, T = 1, 2, 64, 16
+    qkv = torch.ones(B, 3 * H * hd, device=dev)
+    kc = torch.zeros(B, H, T, hd, device=dev)
+    vc = torch.zeros(B, H, T, hd, device=dev)
+    y = torch.zeros(B, H * hd, device=dev)
+    for bad in (T, T + 5, -1):
+        p = torch.tensor([bad], device=dev)
+        rc = _lib.lib().tiq_decode_attention(qkv.data_ptr(), qkv.shape[1], B, H, H, hd, kc.data_ptr(), vc.data_ptr(),
+                                             T, p.data_ptr(), y.data_ptr(), H * hd, _st())
+        assert rc == 0
+        assert torch.isnan(y).all() and not kc.any() and not vc.any()
+    x = torch.zeros(1, 8, device=dev)
+    tok, p0 = torch.tensor([99], device=dev), torch.tensor([0], device=dev)
+    wte, wpe = torch.ones(10, 8, device=dev), torch.ones(4, 8, device=dev)
+    rc = _lib.lib().tiq_embed_tokens(tok.data_ptr(), p0.data_ptr(), wte.data_ptr(), 10, wpe.data_ptr(), 4, 1, 8,
+                                     x.data_ptr(), _st())
+    assert rc == 0 and torch.isnan(x).all()
+
+
+def test_embed_and_argmax(dev):
+    V, P, C, B = 97, 32, 64, 3
+    gen = torch.Generator().manual_seed(5)
+    wte, wpe = torch.randn(V, C, generator=gen), torch.randn(P, C, generator=gen)
+    tok = torch.tensor([3, 96, 0])
+    x = torch.empty(B, C, device=dev)
+    tokd, p7, wted, wped = tok.to(dev), torch.tensor([7], device=dev), wte.to(dev), wpe.to(dev)
+    rc = _lib.lib().tiq_embed_tokens(tokd.data_ptr(), p7.data_ptr(), wted.data_ptr(), V, wped.data_ptr(), P, B, C,
+                                     x.data_ptr(), _st())
+    _lib.check(rc, "embed")
+    assert torch.equal(x.cpu(), wte[tok] + wpe[7])
+    logits = torch.randn(B, 50257, generator=gen)
+    logits[1, 100] = logits[1, 40000] = 50.0  # a tie: the first index wins
+    out = torch.zeros(B, dtype=torch.long, device=dev)
+    ids = torch.zeros(B, 16, dtype=torch.long, device=dev)
+    ld, p4 = logits.to(dev), torch.tensor([4], device=dev)
+    rc = _lib.lib().tiq_argmax_rows(ld.data_ptr(), B, 50257, 50257, out.data_ptr(), ids.data_ptr(), 16, p4.data_ptr(),
+                                    _st())
+    _lib.check(rc, "argmax")
+    assert torch.equal(out.cpu(), logits.argmax(-1)) and int(out[1]) == 100
+    assert torch.equal(ids.cpu()[:, 5], logits.argmax(-1))
+
+
+def _model(cfg, dev):
+    torch.manual_seed(0)
+    return g.GPT(cfg).to(dev).eval()
+
+
+def test_fused_decoder_gpt2_small_matches_reference(reference_decode, dev):
+    e = reference_decode["gpt2_small"]
+    qm, _ = g.quantize_model(_model(g.GPTConfig(**e["config"]), dev), 8)
+    gr = e["greedy_int8"]
+    prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
+    dec = g.make_decoder(qm, 1, 128)
+    assert isinstance(dec, g.FusedDecoder)
+    out = g.generate_graph(qm, prompt, gr["new_tokens"], decoder=dec)
+    assert out.cpu().tolist() == gr["ids"]
+    again = g.generate_graph(qm, prompt, gr["new_tokens"], decoder=dec)  # graph reuse
+    assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("scheme", [(8, None), (4, None), (4, 64)])
+def test_fused_decoder_matches_eager_mini(dev, scheme):
+    bits, group = scheme
+    cfg = g.GPTConfig(vocab_size=97, n_positions=96, n_layer=2, n_head=2, n_embd=128)
+    qm, _ = g.quantize_model(_model(cfg, dev), bits, group_size=group)
+    prompt = OM.benchmark_prompt(97, 2, 9).to(dev)
+    want = g.generate(qm, prompt, 40)
+    dec = g.make_decoder(qm, 2, 49)
+    assert isinstance(dec, g.FusedDecoder)
+    got = g.generate_graph(qm, prompt, 40, decoder=dec)
+    assert torch.equal(got, want)
