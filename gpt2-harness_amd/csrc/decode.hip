@@ -20,7 +20,12 @@ namespace {
 constexpr int kHeadDim = 64;    // every released GPT-2 size
 constexpr int kMaxSlots = 1024;  // n_positions of GPT-2
 
-// One workgroup (4 wavefronts) per (sequence, head).
+// One workgroup (4 wavefronts) per (sequence, head). Every global load the
+// kernel needs for the first kPre key / value slots (the whole cache at
+// GPT-2 decode lengths) is issued before the first barrier, so the kernel
+// waits for HBM once; longer histories stream the rest in a second pass.
+constexpr int kPreKeys = 128;  // slots whose key rows / values are prefetched
+
 __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __restrict__ qkv, int64_t ld_qkv, int H,
                                                                int Hkv, float* __restrict__ kc,
                                                                float* __restrict__ vc, int64_t t_max,
@@ -42,6 +47,27 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     const int C = H * kHeadDim, KV = Hkv * kHeadDim;
     float* kb = kc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
     float* vb = vc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
+
+    // ---- issue every load of the first kPreKeys slots ----
+    // keys: slot t = (tid / 4) + 64 j, this lane's 16 dims at qd
+    const int qd = (lane & 3) * 16;
+    const int kslot = (wave * 16) + (lane >> 2);  // 0..63
+    float4 kr[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t t = kslot + 64 * j;
+        const bool ld = t < pos;  // slot pos comes from qkv, not the cache
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            kr[j][q] = ld ? reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // values: slot t = wave + 4 i, this lane's dim
+    float vr[kPreKeys / 4];
+#pragma unroll
+    for (int i = 0; i < kPreKeys / 4; ++i) {
+        const int64_t t = wave + 4 * i;
+        vr[i] = (t < pos) ? vb[t * kHeadDim + lane] : 0.f;
+    }
     if (tid < kHeadDim) {
         qs[tid] = row[h * kHeadDim + tid];
         kn[tid] = row[C + hk * kHeadDim + tid];
@@ -53,26 +79,30 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     }
     __syncthreads();
 
-    // scores: 16 keys per wavefront pass, 4 lanes per key (16 dims each)
+    // ---- scores ----
     const float inv_div = 1.0f / sqrtf((float)kHeadDim);  // exactly 1/8
-    const int qd = (lane & 3) * 16;
-    for (int64_t t0 = wave * 16; t0 <= pos; t0 += 64) {
-        const int64_t t = t0 + (lane >> 2);
+    for (int64_t t0 = 0; t0 <= pos; t0 += 64) {
+        const int64_t t = t0 + kslot;
+        const int j = (int)(t0 >> 6);
         float s = 0.f;
-        if (t <= pos) {
-            if (t == pos) {
+        if (t == pos) {
 #pragma unroll
-                for (int d = 0; d < 16; ++d) s = fmaf(qs[qd + d], kn[qd + d], s);
+            for (int d = 0; d < 16; ++d) s = fmaf(qs[qd + d], kn[qd + d], s);
+        } else if (t < pos) {
+            float4 k4[4];
+            if (j < 2) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) k4[q] = (j == 0) ? kr[0][q] : kr[1][q];
             } else {
-                const float4* kr = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float4 k4 = kr[j];
-                    s = fmaf(qs[qd + 4 * j], k4.x, s);
-                    s = fmaf(qs[qd + 4 * j + 1], k4.y, s);
-                    s = fmaf(qs[qd + 4 * j + 2], k4.z, s);
-                    s = fmaf(qs[qd + 4 * j + 3], k4.w, s);
-                }
+                for (int q = 0; q < 4; ++q) k4[q] = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                s = fmaf(qs[qd + 4 * q], k4[q].x, s);
+                s = fmaf(qs[qd + 4 * q + 1], k4[q].y, s);
+                s = fmaf(qs[qd + 4 * q + 2], k4[q].z, s);
+                s = fmaf(qs[qd + 4 * q + 3], k4[q].w, s);
             }
         }
         s += __shfl_xor(s, 1, 64);
@@ -81,7 +111,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     }
     __syncthreads();
 
-    // softmax over slots 0..pos
+    // ---- softmax over slots 0..pos ----
     float mx = -INFINITY;
     for (int64_t t = tid; t <= pos; t += 256) mx = fmaxf(mx, sc[t]);
 #pragma unroll
@@ -101,12 +131,15 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     __syncthreads();
     sum = (red[0] + red[1]) + (red[2] + red[3]);
 
-    // weighted sum of values: wavefront w takes slots t = w mod 4, lane = dim
+    // ---- weighted sum of values: wavefront w takes slots t = w mod 4, lane = dim ----
     float acc = 0.f;
-    for (int64_t t = wave; t <= pos; t += 4) {
-        const float v = (t == pos) ? vn[lane] : vb[t * kHeadDim + lane];
-        acc = fmaf(sc[t], v, acc);
+#pragma unroll
+    for (int i = 0; i < kPreKeys / 4; ++i) {
+        const int64_t t = wave + 4 * i;
+        if (t < pos) acc = fmaf(sc[t], vr[i], acc);
     }
+    for (int64_t t = wave + kPreKeys; t < pos; t += 4) acc = fmaf(sc[t], vb[t * kHeadDim + lane], acc);
+    if ((pos & 3) == wave) acc = fmaf(sc[pos], vn[lane], acc);
     part[wave][lane] = acc;
     __syncthreads();
     if (tid < kHeadDim) {
@@ -124,49 +157,73 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
     for (int64_t c = threadIdx.x; c < C; c += blockDim.x) x[b * C + c] = ok ? wte[t * C + c] + wpe[p * C + c] : NAN;
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int64_t cols, int64_t ld,
-                                                      int64_t* __restrict__ out, int64_t* __restrict__ ids,
-                                                      int64_t ld_ids, const int64_t* __restrict__ pos_p) {
-    __shared__ float bv[16];
-    __shared__ int64_t bi[16];
-    const int64_t r = blockIdx.x;
+// Row maximum in two stages: kArgParts workgroups per row each reduce a slice
+// to (value, first index), then one workgroup reduces every row's partials,
+// writes the token (and its id slot) and advances the position.
+constexpr int kArgParts = 64;
+
+__device__ __forceinline__ void better(float& v, int64_t& i, float ov, int64_t oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int64_t cols, int64_t ld,
+                                                             float* __restrict__ pv, int64_t* __restrict__ pi) {
+    __shared__ float bv[4];
+    __shared__ int64_t bi[4];
+    const int64_t r = blockIdx.y;
+    const int part = blockIdx.x;
+    const int64_t span = (cols + kArgParts - 1) / kArgParts;
+    const int64_t c0 = part * span, c1 = (c0 + span < cols) ? c0 + span : cols;
     const float* xr = x + r * ld;
     float v = -INFINITY;
-    int64_t idx = 0;
-    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-        const float a = xr[c];
-        if (a > v) {
-            v = a;
-            idx = c;
-        }
+    int64_t idx = c0 < cols ? c0 : 0;
+    // four independent loads in flight per thread
+    for (int64_t c = c0 + threadIdx.x; c < c1; c += 4 * 256) {
+        float a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = (c + u * 256 < c1) ? xr[c + u * 256] : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (a[u] > v) {
+                v = a[u];
+                idx = c + u * 256;
+            }
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const int64_t oi = __shfl_xor(idx, off, 64);
-        if (ov > v || (ov == v && oi < idx)) {
-            v = ov;
-            idx = oi;
-        }
-    }
+    for (int off = 32; off >= 1; off >>= 1) better(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
     if (lane == 0) {
         bv[wave] = v;
         bi[wave] = idx;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int i = 1; i < (int)(blockDim.x >> 6); ++i)
-            if (bv[i] > v || (bv[i] == v && bi[i] < idx)) {
-                v = bv[i];
-                idx = bi[i];
-            }
-        out[r] = idx;
-        if (ids) {
-            const int64_t col = *pos_p + 1;
-            if (col >= 0 && col < ld_ids) ids[r * ld_ids + col] = idx;
+        for (int i = 1; i < 4; ++i) better(v, idx, bv[i], bi[i]);
+        pv[r * kArgParts + part] = v;
+        pi[r * kArgParts + part] = idx;
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pv, const int64_t* __restrict__ pi,
+                                                          int64_t rows, int64_t* __restrict__ out,
+                                                          int64_t* __restrict__ ids, int64_t ld_ids,
+                                                          int64_t* __restrict__ pos_p) {
+    const int lane = threadIdx.x;
+    const int64_t col = pos_p ? *pos_p + 1 : 0;
+    for (int64_t r = 0; r < rows; ++r) {
+        float v = pv[r * kArgParts + lane];
+        int64_t idx = pi[r * kArgParts + lane];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) better(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
+        if (lane == 0) {
+            out[r] = idx;
+            if (ids && col >= 0 && col < ld_ids) ids[r * ld_ids + col] = idx;
         }
     }
+    if (lane == 0 && pos_p && ids) *pos_p = col;  // every read of the position in this step came before
 }
 
 }  // namespace
@@ -199,12 +256,24 @@ extern "C" int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const
     return launch_status();
 }
 
+extern "C" size_t tiq_argmax_rows_workspace(int64_t rows) {
+    return (size_t)(rows < 0 ? 0 : rows) * kArgParts * (sizeof(float) + sizeof(int64_t));
+}
+
 extern "C" int tiq_argmax_rows(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t* out, int64_t* ids,
-                               int64_t ld_ids, const int64_t* pos, void* stream) {
-    if (rows < 0 || cols <= 0 || ld < cols) return TIQ_EINVAL;
+                               int64_t ld_ids, int64_t* pos, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+    if (rows < 0 || cols <= 0 || ld < cols || rows > 65535) return TIQ_EINVAL;
     if (rows == 0) return TIQ_OK;
-    if (!x || !out || (ids && !pos)) return TIQ_EINVAL;
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, as_stream(stream), x, cols, ld, out, ids,
-                       ld_ids, pos);
+    if (!x || !out || (ids && !pos) || !workspace) return TIQ_EINVAL;
+    if (workspace_bytes < tiq_argmax_rows_workspace(rows)) return TIQ_EWORKSPACE;
+    if (!aligned(workspace, 8)) return TIQ_EALIGN;
+    int64_t* pi = reinterpret_cast<int64_t*>(workspace);
+    float* pv = reinterpret_cast<float*>(pi + rows * kArgParts);
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgParts, (unsigned)rows), dim3(256), 0, st, x, cols, ld, pv, pi);
+    int rc = launch_status();
+    if (rc) return rc;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64), 0, st, pv, pi, rows, out, ids, ld_ids, pos);
     return launch_status();
 }

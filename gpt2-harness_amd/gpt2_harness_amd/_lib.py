@@ -44,7 +44,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                           _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp], _i32),
     "tiq_decode_attention": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
-    "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp], _i32),
+    "tiq_argmax_rows_workspace": ([_i64], _sz),
+    "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _vp], _i32),
 }
 
 WF_INT8, WF_INT4, WF_INT4G, WF_F32 = 0, 1, 2, 3

@@ -55,6 +55,8 @@ class _DecoderBase:
         self.tok = torch.zeros(batch, 1, dtype=torch.long, device=dev)  # token being fed
         self.out = torch.zeros(batch, max_len, dtype=torch.long, device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
+        # captured prefills by prompt length: (graph, static prompt)
+        self.prefill_graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
 
     @torch.no_grad()
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:
@@ -93,6 +95,35 @@ class _DecoderBase:
             self._step()
         self.graph = g
 
+    def _start(self, idx: torch.Tensor) -> None:
+        """Prefill, then set up the first generated token (position T0)."""
+        T0 = idx.size(1)
+        logits = self.prefill(idx)
+        first = logits.argmax(dim=-1, keepdim=True)
+        self.out[:, T0 : T0 + 1].copy_(first)
+        self.tok.copy_(first)
+        self.pos.fill_(T0)
+
+    @torch.no_grad()
+    def start(self, idx: torch.Tensor) -> None:
+        """:meth:`_start` from a graph captured for this prompt length (the
+        prompt is copied into the graph's static input first)."""
+        T0 = idx.size(1)
+        if T0 not in self.prefill_graphs:
+            static = idx.clone()
+            s = torch.cuda.Stream(device=self.dev)
+            s.wait_stream(torch.cuda.current_stream(self.dev))
+            with torch.cuda.stream(s):
+                self._start(static)  # warm-up (also the result of this call)
+            torch.cuda.current_stream(self.dev).wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._start(static)
+            self.prefill_graphs[T0] = (g, static)
+        g, static = self.prefill_graphs[T0]
+        static.copy_(idx)
+        g.replay()
+
     @torch.no_grad()
     def run(self, idx: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
         """Greedy decode: prefill, then ``max_new_tokens - 1`` graph replays."""
@@ -100,11 +131,9 @@ class _DecoderBase:
         n = min(max_new_tokens, self.cfg.n_positions - T0, self.T - T0)
         if n <= 0:
             return idx
-        logits = self.prefill(idx)
-        first = logits.argmax(dim=-1, keepdim=True)
-        self.out[:, T0 : T0 + 1].copy_(first)
-        self.tok.copy_(first)
-        self.pos.fill_(T0)
+        if B != self.B or T0 > self.T:
+            raise ValueError(f"prompt {tuple(idx.shape)} does not fit batch={self.B}, max_len={self.T}")
+        self.start(idx)
         if n > 1 and self.graph is None:
             self.capture()
         for _ in range(n - 1):
@@ -201,6 +230,7 @@ class FusedDecoder(_DecoderBase):
         self.tok_flat = self.tok.view(-1)
         self.head_w = model.lm_head.weight.detach().contiguous()
         self.L = _lib.lib()
+        self.argmax_ws = torch.empty(int(self.L.tiq_argmax_rows_workspace(B)), dtype=torch.uint8, device=dev)
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
@@ -237,10 +267,10 @@ class FusedDecoder(_DecoderBase):
                                 None, 0, None, cfg.vocab_size, self.logits.data_ptr(), _lib.F32, cfg.vocab_size,
                                 ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps), 0, None, 0, st)
         _lib.check(rc, "lm_head")
+        # argmax also records the token at slot pos + 1 and advances pos
         _lib.check(L.tiq_argmax_rows(self.logits.data_ptr(), B, cfg.vocab_size, cfg.vocab_size,
-                                     self.tok_flat.data_ptr(), self.out.data_ptr(), self.T, self.pos.data_ptr(), st),
-                   "argmax")
-        self.pos.add_(1)
+                                     self.tok_flat.data_ptr(), self.out.data_ptr(), self.T, self.pos.data_ptr(),
+                                     self.argmax_ws.data_ptr(), self.argmax_ws.numel(), st), "argmax")
 
 
 def make_decoder(model, batch: int, max_len: int):

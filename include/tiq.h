@@ -192,10 +192,15 @@ int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte
                      const float* wpe, int64_t n_positions, int64_t batch, int64_t n_embd, float* x,
                      void* stream);
 
-/* out[r] = argmax of row r of x (first index of the maximum; sampling.py:164).
- * If ids is not NULL the index is also written to ids[r * ld_ids + *pos + 1]. */
+/* Workspace bytes tiq_argmax_rows needs for `rows` rows. */
+size_t tiq_argmax_rows_workspace(int64_t rows);
+
+/* out[r] = argmax of row r of x (first index of the maximum; sampling.py:164),
+ * rows <= 65535. If ids is not NULL the index is also written to
+ * ids[r * ld_ids + *pos + 1] and then *pos is advanced by one (the decode
+ * step's last kernel: the new token now sits at the position). */
 int tiq_argmax_rows(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t* out, int64_t* ids,
-                    int64_t ld_ids, const int64_t* pos, void* stream);
+                    int64_t ld_ids, int64_t* pos, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -157,11 +157,20 @@ def test_embed_and_argmax(dev):
     out = torch.zeros(B, dtype=torch.long, device=dev)
     ids = torch.zeros(B, 16, dtype=torch.long, device=dev)
     ld, p4 = logits.to(dev), torch.tensor([4], device=dev)
+    ws = torch.empty(int(_lib.lib().tiq_argmax_rows_workspace(B)), dtype=torch.uint8, device=dev)
     rc = _lib.lib().tiq_argmax_rows(ld.data_ptr(), B, 50257, 50257, out.data_ptr(), ids.data_ptr(), 16, p4.data_ptr(),
-                                    _st())
+                                    ws.data_ptr(), ws.numel(), _st())
     _lib.check(rc, "argmax")
     assert torch.equal(out.cpu(), logits.argmax(-1)) and int(out[1]) == 100
     assert torch.equal(ids.cpu()[:, 5], logits.argmax(-1))
+    assert int(p4) == 5  # the position advanced
+    for cols in (1, 10, 63, 65, 1000):  # short rows: partial slices may be empty
+        x = torch.randn(2, cols, generator=gen)
+        xd = x.to(dev)
+        rc = _lib.lib().tiq_argmax_rows(xd.data_ptr(), 2, cols, cols, out.data_ptr(), None, 0, None, ws.data_ptr(),
+                                        ws.numel(), _st())
+        _lib.check(rc, "argmax")
+        assert torch.equal(out.cpu()[:2], x.argmax(-1)), cols
 
 
 def _model(cfg, dev):
@@ -193,3 +202,19 @@ def test_fused_decoder_matches_eager_mini(dev, scheme):
     assert isinstance(dec, g.FusedDecoder)
     got = g.generate_graph(qm, prompt, 40, decoder=dec)
     assert torch.equal(got, want)
+
+
+def test_graph_replays_with_different_prompts(reference_decode, dev):
+    """Captured prefill and decode graphs replayed for several prompts of the
+    same length, with eager work in between, match eager generation each time."""
+    cfg = g.GPTConfig(vocab_size=97, n_positions=96, n_layer=2, n_head=2, n_embd=128)
+    qm, _ = g.quantize_model(_model(cfg, dev), 8)
+    dec = g.make_decoder(qm, 2, 40)
+    for seed in range(4):
+        torch.manual_seed(seed)
+        prompt = torch.randint(0, 97, (2, 8), device=dev)
+        want = g.generate(qm, prompt, 30)
+        got = g.generate_graph(qm, prompt, 30, decoder=dec)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), seed
+    assert len(dec.prefill_graphs) == 1
