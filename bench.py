@@ -344,7 +344,7 @@ def main() -> int:
         print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 5}))
         return 0
     if args.only == "gemm":
-        print(json.dumps(gemm_section(4096, XL_KN, dev)))
+        print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev) for M in (256, 1024, 4096)}))
         return 0
     if args.only == "quantize":
         print(json.dumps(quantize_section(dev)))
@@ -364,7 +364,8 @@ def main() -> int:
         detail["gemv_xl_M1"] = gemv_section(1, XL_KN, 12, 3, 10, 2, dev, seed=7)
         print("# gemv detail done", file=sys.stderr, flush=True)
     if not args.quick and args.only is None:
-        detail["gemm_xl_M4096"] = gemm_section(4096, XL_KN, dev)
+        for M in (256, 1024, 4096):
+            detail[f"gemm_xl_M{M}"] = gemm_section(M, XL_KN, dev)
         print("# gemm done", file=sys.stderr, flush=True)
         detail["quantize_xl"] = quantize_section(dev)
         detail["decode_gpt2_small_int8"] = decode_section(dev)

@@ -223,6 +223,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     }
 }
 
+
 template <int BM, int BN, int WMW, int WNW, int OCC, int FMT, typename TY>
 int run_gemm32(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
@@ -250,16 +251,17 @@ int dispatch_tile(const LinearArgs& a, int tile) {
 }
 
 int tile_override() {
-    static const int t = [] {
-        const char* e = getenv("TIQ_GEMM_TILE");
-        return e ? atoi(e) : 0;
-    }();
-    return t;
+    // read on every call (a getenv is far cheaper than a launch) so that one
+    // process can measure or test each tile configuration
+    const char* e = getenv("TIQ_GEMM_TILE");
+    return e ? atoi(e) : 0;
 }
 
 template <int FMT>
 int dispatch_gemm(const LinearArgs& a) {
     const int tile = tile_override();
+    if (FMT == kW8 && (tile == 0 || tile >= 10) && staged_gemm_supported(a))
+        return launch_staged_gemm(a, tile >= 10 ? tile - 10 : staged_gemm_choice(a.M, a.N, a.K));
     if (a.y_dtype == TIQ_F32) return dispatch_tile<FMT, float>(a, tile);
     return dispatch_tile<FMT, uint16_t>(a, tile);
 }

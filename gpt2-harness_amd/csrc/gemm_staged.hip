@@ -1,0 +1,321 @@
+// Prefill GEMM for large M on the matrix cores (gfx950): int8 weights,
+// bf16 activations, the reference's quantized Linears over a whole prompt
+// (model.py:254,319,352,355 with M = B*T):
+//     y[m, n] = scale[n] * sum_k x[m, k] * q[n, k] + bias[n]
+// Built without -amdgpu-mfma-vgpr-form: its 128 x 128 accumulator blocks live
+// in AGPRs.
+#include "tiq_internal.hpp"
+
+namespace tiq {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;
+constexpr int kXcds = 8;
+
+// ------------------------------------------------------------ staged GEMM
+// The int8 GEMM used for large M. One workgroup of 4 wavefronts (one per
+// SIMD) owns a BM x BN output tile; each wavefront a (BM/2) x (BN/2) block of
+// 32 x 32 x 16 bf16 MFMA tiles (accumulators in AGPRs).
+//
+//   * Staging through registers: every k64 step each thread loads 16-byte
+//     chunks of x (bf16) and of the int8 weight rows into one of two register
+//     sets; a chunk is written to LDS one step after it was loaded, so global
+//     load latency is hidden behind a full step of MFMAs. Weight codes become
+//     bf16 once per workgroup, on the LDS store (exact: every int8 is a bf16).
+//   * LDS double buffered: 128-byte rows (64 bf16 of K), 16-byte chunks
+//     XOR-swizzled by swz8(row) so that fragment reads (32 rows, one chunk)
+//     and staging stores (8 threads per row) are free of bank conflicts.
+//   * The k64 step is issued as bundles of one MFMA plus a slice of the other
+//     work (the next k16's fragment reads, one staging load or store), fenced
+//     with sched_barrier and an empty asm memory clobber so that neither the
+//     scheduler nor the IR passes regroup them. One barrier per step, placed
+//     before the last k16 group, whose fragments are already in registers.
+//   * Output through LDS: the accumulators are scaled, biased and converted,
+//     written to an XOR-swizzled LDS tile, then stored as whole 16-byte row
+//     chunks (a wavefront writes contiguous rows), which costs a few
+//     microseconds per tile instead of the tens a scattered 8-byte store of
+//     the MFMA register layout costs.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Bijective workgroup -> tile map: the tiles are split into 8 contiguous
+// ranges, one per XCD (dispatch round-robins workgroups over the XCDs), and
+// each range is walked in groups of 4 row tiles so that concurrently running
+// workgroups of an XCD share x and weight panels in its L2.
+__device__ __forceinline__ void staged_tile_of(int& tm, int& tn, int tiles_m, int tiles_n) {
+    const int total = tiles_m * tiles_n;
+    const int i = blockIdx.x;
+    const int q = total / kXcds, r = total % kXcds;
+    const int xcd = i % kXcds, local = i / kXcds;
+    const int id = (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+    constexpr int G = 4;
+    const int group = id / (G * tiles_n);
+    const int first_m = group * G;
+    const int gm = (tiles_m - first_m) < G ? (tiles_m - first_m) : G;
+    const int in = id % (G * tiles_n);
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
+
+__device__ __forceinline__ uint32_t bf16x2_of_bytes_perm(uint32_t d, int sh) {
+    const float lo = (float)((int32_t)(d << (24 - sh)) >> 24);
+    const float hi = (float)((int32_t)(d << (16 - sh)) >> 24);
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+template <int BM, int BN, typename TY>
+__global__ __launch_bounds__(256, 1) void gemm_w8_staged(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
+    int K) {
+    constexpr int NT = 256;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TMm = WM / 32, TNn = WN / 32;
+    constexpr int XS = BM * 128, WS = BN * 128, STAGE = XS + WS;
+    constexpr int XL = BM * 8 / NT, WL = BN * 4 / NT, NL = XL + WL;  // staging loads per thread per step
+    constexpr int NMF = TMm * TNn, NRD = TMm + TNn;                  // per k16
+    static_assert(XL * NT == BM * 8 && WL * NT == BN * 4, "staging split");
+    static_assert(NL <= 3 * NMF && NRD <= NMF, "one staging op per bundle");
+    constexpr int UNIT = 16 / (int)sizeof(TY);  // output elements per 16-byte chunk
+    constexpr int UNITS = BN / UNIT;            // chunks per output row
+    constexpr int PASSES = (BM * BN * (int)sizeof(TY) + 2 * STAGE - 1) / (2 * STAGE);
+    static_assert(PASSES == 1 || PASSES == 2, "output tile passes");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int tm, tn;
+    staged_tile_of(tm, tn, tiles_m, tiles_n);
+    const int m_blk = tm * BM, n_blk = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+
+    // staging: x rows xrow + 32 q (8 threads per row), weight rows wrow + 64 j
+    // (4 threads per row); rows are clamped for a partial tile
+    const int xrow = tid >> 3, xch = tid & 7;
+    const int wrow = tid >> 2, wch = tid & 3;
+    const uint32_t ldx2 = (uint32_t)ldx * 2u, ldw1 = (uint32_t)ldw;
+    const int xs0 = xrow * 128 + ((xch ^ swz8(xrow)) * 16);
+    const int ws00 = XS + wrow * 128 + (((2 * wch) ^ swz8(wrow)) * 16);
+    const int ws01 = XS + wrow * 128 + (((2 * wch + 1) ^ swz8(wrow)) * 16);
+    u32x4 sx[2][XL], sw[2][WL];
+    auto gload = [&](int k0, int p, int q) {
+        if (q < XL) {
+            const uint32_t off = (uint32_t)min(m_blk + xrow + 32 * q, M - 1) * ldx2 + xch * 16;
+            sx[p][q] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(x) + 2 * k0 + off);
+        } else {
+            const int j = q - XL;
+            const uint32_t off = (uint32_t)min(n_blk + wrow + 64 * j, N - 1) * ldw1 + wch * 16;
+            sw[p][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + k0 + off);
+        }
+    };
+    auto lstore = [&](uint8_t* base, int p, int q) {
+        if (q < XL) {
+            *reinterpret_cast<u32x4*>(base + xs0 + q * 32 * 128) = sx[p][q];
+        } else {
+            const int j = q - XL;
+            const u32x4 v = sw[p][j];
+            const u32x4 lo = {bf16x2_of_bytes_perm(v.x, 0), bf16x2_of_bytes_perm(v.x, 16),
+                              bf16x2_of_bytes_perm(v.y, 0), bf16x2_of_bytes_perm(v.y, 16)};
+            const u32x4 hi = {bf16x2_of_bytes_perm(v.z, 0), bf16x2_of_bytes_perm(v.z, 16),
+                              bf16x2_of_bytes_perm(v.w, 0), bf16x2_of_bytes_perm(v.w, 16)};
+            *reinterpret_cast<u32x4*>(base + ws00 + j * 64 * 128) = lo;
+            *reinterpret_cast<u32x4*>(base + ws01 + j * 64 * 128) = hi;
+        }
+    };
+
+    // fragments: lane (r, h) reads row base + r, chunk (2 kk + h) of a k16 step
+    const int r = lane & 31, h = lane >> 5;
+    int fo[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) fo[kk] = r * 128 + (((2 * kk + h) ^ swz8(r)) * 16);
+    bf16x8 FW[2][TNn], FX[2][TMm];
+    auto fread = [&](const uint8_t* base, int kk, int set, int q) {
+        if (q < TNn) FW[set][q] = *reinterpret_cast<const bf16x8*>(base + XS + (wn + 32 * q) * 128 + fo[kk]);
+        else FX[set][q - TNn] = *reinterpret_cast<const bf16x8*>(base + (wm + 32 * (q - TNn)) * 128 + fo[kk]);
+    };
+    // D[n][m] = sum_k w[n][k] x[m][k]: result register q of lane (r, h) holds
+    // n = 8 (q / 4) + 4 h + q % 4, m = r of its 32 x 32 tile
+    floatx16 acc[TNn][TMm];
+#pragma unroll
+    for (int i = 0; i < TNn; ++i)
+#pragma unroll
+        for (int j = 0; j < TMm; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+    auto mfma_set = [&](int set, int t) {
+        const int i = t / TMm, j = t % TMm;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FW[set][i], FX[set][j], acc[i][j], 0, 0, 0);
+    };
+
+    const int nk = K / BK;
+#pragma unroll
+    for (int q = 0; q < NL; ++q) gload(0, 0, q);
+#pragma unroll
+    for (int q = 0; q < NL; ++q) gload(min(1, nk - 1) * BK, 1, q);
+#pragma unroll
+    for (int q = 0; q < NL; ++q) lstore(smem, 0, q);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NRD; ++q) fread(smem, 0, 0, q);
+
+    // Step s: MFMAs on buffer s % 2; stage s + 1 (register set (s + 1) % 2)
+    // is stored to the other buffer over the first three k16 groups; stage
+    // s + 2 is loaded into set s % 2 over all four. Past the last stage the
+    // loads repeat it (clamped k), which keeps the loop body one path.
+    auto step = [&](int s, int p) {
+        uint8_t* cur = smem + (s & 1) * STAGE;
+        uint8_t* nxt = smem + ((s + 1) & 1) * STAGE;
+        const int k2 = min(s + 2, nk - 1) * BK;
+#pragma unroll
+        for (int kk = 0; kk < 3; ++kk) {
+            const int set = kk & 1;
+#pragma unroll
+            for (int t = 0; t < NMF; ++t) {
+                mfma_set(set, t);
+                if (t < NRD) fread(cur, kk + 1, set ^ 1, t);
+                const int b = kk * NMF + t;
+                if ((b + 1) * NL / (3 * NMF) > b * NL / (3 * NMF)) lstore(nxt, p ^ 1, b * NL / (3 * NMF));
+                if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NMF; ++t) {
+            mfma_set(1, t);
+            if (t < NRD) fread(nxt, 0, 0, t);
+            const int b = 3 * NMF + t;
+            if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    int s = 0;
+    for (; s + 1 < nk; s += 2) {
+        step(s, 0);
+        step(s + 1, 1);
+    }
+    if (s < nk) step(s, 0);
+    __syncthreads();
+
+    // epilogue: scale, bias, convert; LDS tile [rows of the pass][UNITS chunks],
+    // chunk u of row m at position u ^ (m % UNITS)
+    constexpr int ROWS = BM / PASSES;
+    constexpr int ROW_BYTES = BN * (int)sizeof(TY);
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+        if (PASSES == 1 || (wm / WM) == pass) {
+#pragma unroll
+            for (int i = 0; i < TNn; ++i) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int nl = wn + 32 * i + 8 * g + 4 * h;  // 4 consecutive outputs
+                    const int n0 = n_blk + nl < N ? n_blk + nl : N - 4;
+                    const float4 sc = *reinterpret_cast<const float4*>(scale + n0);
+                    float4 bi = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (bias) bi = *reinterpret_cast<const float4*>(bias + n0);
+#pragma unroll
+                    for (int j = 0; j < TMm; ++j) {
+                        const int ml = wm + 32 * j + r - pass * ROWS;
+                        const float v0 = fmaf(acc[i][j][4 * g + 0], sc.x, bi.x);
+                        const float v1 = fmaf(acc[i][j][4 * g + 1], sc.y, bi.y);
+                        const float v2 = fmaf(acc[i][j][4 * g + 2], sc.z, bi.z);
+                        const float v3 = fmaf(acc[i][j][4 * g + 3], sc.w, bi.w);
+                        const int u = nl / UNIT;
+                        uint8_t* dst = smem + ml * ROW_BYTES + ((u ^ (ml & (UNITS - 1))) * 16);
+                        if constexpr (sizeof(TY) == 4) {
+                            *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+                        } else {
+                            uint2 o;
+                            o.x = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
+                            o.y = (uint32_t)f32_to_bf16_bits(v2) | ((uint32_t)f32_to_bf16_bits(v3) << 16);
+                            *reinterpret_cast<uint2*>(dst + 8 * (nl % UNIT != 0)) = o;
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        constexpr int CH = ROWS * UNITS / NT;  // 16-byte chunks per thread
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int idx = tid + NT * c;
+            const int ml = idx / UNITS, u = idx % UNITS;
+            const int m = m_blk + pass * ROWS + ml, n = n_blk + u * UNIT;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(smem + ml * ROW_BYTES + ((u ^ (ml & (UNITS - 1))) * 16));
+            if (m < M && n < N) *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n) = v;
+        }
+        if (pass + 1 < PASSES) __syncthreads();
+    }
+}
+
+template <int BM, int BN, typename TY>
+int run_staged(const LinearArgs& a) {
+    const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    hipLaunchKernelGGL((gemm_w8_staged<BM, BN, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
+                       static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
+                       a.scale, a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K);
+    return launch_status();
+}
+
+bool staged_supported_impl(const LinearArgs& a) {
+    if (a.fmt != kW8 || a.x_dtype != TIQ_BF16 || a.K % BK != 0) return false;
+    const int unit = a.y_dtype == TIQ_F32 ? 4 : 8;
+    if (a.N % unit != 0 || a.ldy % unit != 0 || !aligned(a.y, 16)) return false;
+    if (!aligned(a.scale, 16) || (a.bias && !aligned(a.bias, 16))) return false;
+    if (!aligned(a.x, 16) || a.ldx % 8 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
+    // 32-bit byte offsets from the base pointers
+    if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + a.K > 0xffffffffLL) return false;
+    return true;
+}
+
+// Tile choice: rounds of co-resident workgroups (256x256 and 256x128 tiles
+// need most of a CU's LDS and registers: one per CU; 128x128 tiles fit two)
+// times the duration of one round, modelled as step_us per k64 step plus a
+// fixed term, both fitted to MI355X measurements of this kernel at the
+// GPT-2-XL Linear shapes with M = 4096 (all 256 CUs busy).
+int staged_choice(int64_t M, int64_t N, int64_t K) {
+    struct Opt { int bm, bn, per_cu; double step_us, fixed_us; };
+    static const Opt opts[] = {{256, 256, 1, 1.29, 23.0}, {256, 128, 1, 0.87, 8.4}, {128, 128, 2, 1.07, 0.5}};
+    const double nk = (double)(K / BK);
+    int best = 0;
+    double best_t = 1e30;
+    for (int o = 0; o < 3; ++o) {
+        const int64_t tiles = ((M + opts[o].bm - 1) / opts[o].bm) * ((N + opts[o].bn - 1) / opts[o].bn);
+        const int64_t slots = 256 * opts[o].per_cu;
+        const double rounds = (double)((tiles + slots - 1) / slots);
+        const double t = rounds * (nk * opts[o].step_us + opts[o].fixed_us);
+        if (t < best_t) { best_t = t; best = o; }
+    }
+    return best;
+}
+
+}  // namespace
+
+template <typename TY>
+int dispatch_staged_t(const LinearArgs& a, int choice) {
+    switch (choice) {
+        case 0: return run_staged<256, 256, TY>(a);
+        case 1: return run_staged<256, 128, TY>(a);
+        default: return run_staged<128, 128, TY>(a);
+    }
+}
+
+
+bool staged_gemm_supported(const LinearArgs& a) { return staged_supported_impl(a); }
+
+int staged_gemm_choice(int64_t M, int64_t N, int64_t K) { return staged_choice(M, N, K); }
+
+int launch_staged_gemm(const LinearArgs& a, int choice) {
+    if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
+    if (a.y_dtype == TIQ_F32) return dispatch_staged_t<float>(a, choice);
+    return dispatch_staged_t<uint16_t>(a, choice);
+}
+
+}  // namespace tiq

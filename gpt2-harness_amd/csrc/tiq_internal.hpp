@@ -51,4 +51,11 @@ int launch_gemm(const LinearArgs& a);
 // True when the MFMA GEMM has a kernel for these arguments.
 bool gemm_supported(const LinearArgs& a);
 
+// The register-staged int8 GEMM (gemm_staged.hip): whether it takes these
+// arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128) and
+// its launch.
+bool staged_gemm_supported(const LinearArgs& a);
+int staged_gemm_choice(int64_t M, int64_t N, int64_t K);
+int launch_staged_gemm(const LinearArgs& a, int choice);
+
 }  // namespace tiq

@@ -91,6 +91,16 @@ def test_gemm_w8_small_shapes(dev, c_oracle, KN, M):
     _run_w8("tiq_gemm_w8", dev, c_oracle, *KN, M, torch.bfloat16, seed=M, bias=False)
 
 
+# Every GEMM tile configuration (TIQ_GEMM_TILE: 10/11/12 the register-staged
+# int8 kernel at 256x256 / 256x128 / 128x128 tiles, 1 the 128x128 kernel that
+# also serves int4), on full, partial-row and partial-column tiles.
+@pytest.mark.parametrize("tile", [10, 11, 12, 1])
+@pytest.mark.parametrize("K,N,M", [(1600, 1600, 512), (1600, 4800, 300), (6400, 1600, 257), (768, 2304, 1024)])
+def test_gemm_w8_tiles(dev, c_oracle, monkeypatch, tile, K, N, M):
+    monkeypatch.setenv("TIQ_GEMM_TILE", str(tile))
+    _run_w8("tiq_gemm_w8", dev, c_oracle, K, N, M, torch.bfloat16, seed=tile + M, bias=M % 2 == 0)
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 256])
 def test_linear_w8_dispatch(dev, c_oracle, M):
     _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.bfloat16, seed=M)
