@@ -71,7 +71,7 @@ template <int BM, int BN, typename TY>
 __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
-    int K) {
+    int K, int kw) {
     constexpr int NT = 256;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TMm = WM / 32, TNn = WN / 32;
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
         } else {
             const int j = q - XL;
             const uint32_t off = (uint32_t)min(n_blk + wrow + 64 * j, N - 1) * ldw1 + wch * 16;
-            sw[p][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + k0 + off);
+            sw[p][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + (k0 % kw) + off);
         }
     };
     auto lstore = [&](uint8_t* base, int p, int q) {
@@ -260,18 +260,21 @@ int run_staged(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     hipLaunchKernelGGL((gemm_w8_staged<BM, BN, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
                        static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
-                       a.scale, a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K);
+                       a.scale, a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K,
+                       (int)(a.kw ? a.kw : a.K));
     return launch_status();
 }
 
 bool staged_supported_impl(const LinearArgs& a) {
     if (a.fmt != kW8 || a.x_dtype != TIQ_BF16 || a.K % BK != 0) return false;
+    if (a.kw && (a.kw % BK != 0 || a.K % a.kw != 0)) return false;
     const int unit = a.y_dtype == TIQ_F32 ? 4 : 8;
     if (a.N % unit != 0 || a.ldy % unit != 0 || !aligned(a.y, 16)) return false;
     if (!aligned(a.scale, 16) || (a.bias && !aligned(a.bias, 16))) return false;
     if (!aligned(a.x, 16) || a.ldx % 8 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
     // 32-bit byte offsets from the base pointers
-    if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + a.K > 0xffffffffLL) return false;
+    if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + (a.kw ? a.kw : a.K) > 0xffffffffLL)
+        return false;
     return true;
 }
 

@@ -49,6 +49,60 @@ LinearArgs make_args(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
     return a;
 }
 
+// x (M, K) fp32 -> x3 (M, 3K) bf16: [hi | lo | lo2] with hi = rne(x),
+// lo = rne(x - hi), lo2 = rne(x - hi - lo). Both differences are exact in fp32
+// and lo2 holds the last 8 significant bits, so hi + lo + lo2 == x; an int8
+// weight is exact in bf16, so every product the MFMA forms is exact and the
+// GEMM over the three planes is as accurate as an fp32 GEMM.
+__global__ void split_bf16x3_kernel(const float* __restrict__ x, int64_t ldx, int M, int K,
+                                    uint16_t* __restrict__ x3) {
+    const int k4 = K / 4;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)M * k4) return;
+    const int m = (int)(i / k4), k = (int)(i % k4) * 4;
+    const float4 v = *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k);
+    const float in[4] = {v.x, v.y, v.z, v.w};
+    uint16_t p[3][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint16_t hi = f32_to_bf16_bits(in[e]);
+        const float r1 = in[e] - bf16_bits_to_f32(hi);
+        const uint16_t lo = f32_to_bf16_bits(r1);
+        const float r2 = r1 - bf16_bits_to_f32(lo);
+        p[0][e] = hi;
+        p[1][e] = lo;
+        p[2][e] = f32_to_bf16_bits(r2);
+    }
+    uint16_t* row = x3 + (int64_t)m * 3 * K + k;
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+        *reinterpret_cast<uint2*>(row + (int64_t)q * K) =
+            make_uint2((uint32_t)p[q][0] | ((uint32_t)p[q][1] << 16), (uint32_t)p[q][2] | ((uint32_t)p[q][3] << 16));
+}
+
+size_t split_workspace(int64_t M, int64_t K) { return (size_t)(M * 3 * K * 2 + 255) / 256 * 256; }
+
+// fp32 activations through the matrix cores when the staged GEMM takes the
+// three-plane problem; TIQ_EUNSUPPORTED otherwise (the caller falls back).
+int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
+    if (a.x_dtype != TIQ_F32 || a.fmt != kW8 || a.M < kGemmMinRows || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
+    if (!aligned(a.x, 16) || a.ldx % 4 != 0 || a.M * 3 * a.K > 0x7fffffffLL) return TIQ_EUNSUPPORTED;
+    LinearArgs g = a;
+    g.x = ws;
+    g.x_dtype = TIQ_BF16;
+    g.K = 3 * a.K;
+    g.ldx = 3 * a.K;
+    g.kw = a.K;
+    if (!staged_gemm_supported(g)) return TIQ_EUNSUPPORTED;
+    if (!ws || ws_bytes < split_workspace(a.M, a.K) || !aligned(ws, 16)) return TIQ_EWORKSPACE;
+    const int64_t n = a.M * (a.K / 4);
+    hipLaunchKernelGGL(split_bf16x3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, a.stream,
+                       static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, static_cast<uint16_t*>(ws));
+    int rc = launch_status();
+    if (rc != TIQ_OK) return rc;
+    return launch_staged_gemm(g, staged_gemm_choice(g.M, g.N, g.K));
+}
+
 int run_linear(const LinearArgs& a) {
     int rc = check_linear(a);
     if (rc != TIQ_OK || a.M == 0 || a.N == 0) return rc;
@@ -82,6 +136,23 @@ extern "C" int tiq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, i
                              void* stream) {
     return run_linear(make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0,
                                 bias, N, y, y_dtype, ldy, stream, kW8));
+}
+
+extern "C" size_t tiq_linear_w8_workspace(int x_dtype, int64_t M, int64_t K) {
+    if (x_dtype != TIQ_F32 || M < kGemmMinRows || K <= 0 || K % 64 != 0) return 0;
+    return split_workspace(M, K);
+}
+
+extern "C" int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,
+                                const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0, bias,
+                             N, y, y_dtype, ldy, stream, kW8);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    rc = run_linear_split(a, workspace, workspace_bytes);
+    if (rc != TIQ_EUNSUPPORTED) return rc;
+    return run_linear(a);
 }
 
 extern "C" int tiq_gemv_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,

@@ -41,6 +41,10 @@ struct LinearArgs {
     hipStream_t stream;
     WFormat fmt;
     Fusion fuse;
+    // Period of K in the weight matrix: the GEMM reads weight column k % kw.
+    // 0 means K. The fp32-activation path passes K = 3 kw (x split into three
+    // bf16 planes laid side by side along K).
+    int64_t kw = 0;
 };
 
 // Validates the common arguments; TIQ_OK when they are consistent.

@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_dequantize_int4": ([_vp, _vp, _i32, _i64, _i64, _vp, _vp], _i32),
     "tiq_dequantize_groupwise_int4": ([_vp, _vp, _i32, _i64, _i64, _vp, _vp], _i32),
     "tiq_linear_w8": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
+    "tiq_linear_w8_workspace": ([_i32, _i64, _i64], _sz),
+    "tiq_linear_w8_ws": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp, _sz, _vp], _i32),
     "tiq_gemv_w8": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_gemm_w8": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_linear_w4": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),

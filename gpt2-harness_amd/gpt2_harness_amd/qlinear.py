@@ -107,8 +107,12 @@ def linear_into(m: QuantLinear, x2: torch.Tensor, y: torch.Tensor) -> None:
     st = _lib.stream_of(x2)
     b = _lib.ptr(m.bias)
     if m.fmt == FMT_W8:
-        rc = L.tiq_linear_w8(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b, N,
-                             y.data_ptr(), yd, y.stride(0), st)
+        # fp32 activations over many rows (a prefill) take the matrix cores as
+        # three exact bf16 planes; the library sizes the workspace (0: none)
+        ws_bytes = int(L.tiq_linear_w8_workspace(xd, M, K))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
+        rc = L.tiq_linear_w8_ws(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b, N,
+                                y.data_ptr(), yd, y.stride(0), None if ws is None else ws.data_ptr(), ws_bytes, st)
     elif m.fmt == FMT_W4:
         rc = L.tiq_linear_w4(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b, N,
                              y.data_ptr(), yd, y.stride(0), st)

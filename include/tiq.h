@@ -123,6 +123,24 @@ int tiq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const int8_t* q, const float* scale, const float* bias, int64_t N,
                   void* y, int y_dtype, int64_t ldy, void* stream);
 
+/* Workspace bytes tiq_linear_w8_ws needs (0: none). Nonzero for fp32
+ * activations with M >= 128 and K % 64 == 0: M * 3K * 2 bytes, rounded up
+ * to 256. */
+size_t tiq_linear_w8_workspace(int x_dtype, int64_t M, int64_t K);
+
+/* tiq_linear_w8 with a caller workspace -- the same quantized Linear slot
+ * (model.py:254,319,352,355), used by the prefill (M = B*T rows) of a model
+ * that keeps fp32 activations. With fp32 x and M >= 128 the activations are
+ * split exactly into three bf16 planes (x = hi + lo + lo2, written to the
+ * workspace) and the product runs on the matrix cores: every product is exact
+ * (int8 is exact in bf16), so the result is as accurate as an fp32 GEMM.
+ * Other cases behave as tiq_linear_w8. TIQ_EWORKSPACE when the workspace is
+ * smaller than tiq_linear_w8_workspace() or not 16-byte aligned. */
+int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                     const int8_t* q, const float* scale, const float* bias, int64_t N,
+                     void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
 /* Decode GEMV on the vector ALUs: coalesced 128-bit weight loads, dequant in
  * registers, wavefront reductions. Any M (processed in slices of up to 4
  * rows); needs K % 16 == 0 and 16-byte aligned weight rows. */

@@ -101,6 +101,40 @@ def test_gemm_w8_tiles(dev, c_oracle, monkeypatch, tile, K, N, M):
     _run_w8("tiq_gemm_w8", dev, c_oracle, K, N, M, torch.bfloat16, seed=tile + M, bias=M % 2 == 0)
 
 
+# fp32 activations through the matrix cores (three exact bf16 planes): the
+# contract bound, and fp32-level accuracy -- against a float64 product, the
+# error is within a small factor of the fp32 oracle's own error (both differ
+# from the exact result only by fp32 accumulation order).
+@pytest.mark.parametrize("K,N,M", [(1600, 4800, 256), (6400, 1600, 300), (768, 3072, 1024), (3072, 768, 129)])
+def test_linear_w8_fp32_matrix_cores(dev, c_oracle, K, N, M):
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, seed=M + K)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    qd, sd = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev)
+    xd, bd = x.to(dev), b.to(dev)
+    ws_bytes = int(L.tiq_linear_w8_workspace(_lib.F32, M, K))
+    assert ws_bytes >= M * 3 * K * 2
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    y = torch.empty(M, N, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    # too small a workspace is refused before any work
+    rc = L.tiq_linear_w8_ws(xd.data_ptr(), _lib.F32, M, K, K, qd.data_ptr(), sd.data_ptr(), bd.data_ptr(), N,
+                            y.data_ptr(), _lib.F32, N, ws.data_ptr(), ws_bytes - 256, st)
+    assert rc == -5
+    _lib.check(L.tiq_linear_w8_ws(xd.data_ptr(), _lib.F32, M, K, K, qd.data_ptr(), sd.data_ptr(), bd.data_ptr(), N,
+                                  y.data_ptr(), _lib.F32, N, ws.data_ptr(), ws_bytes, st), "tiq_linear_w8_ws")
+    torch.cuda.synchronize()
+    y_ref = OL.linear_ref(x, OL.dequantize(q, s), b)
+    ok, err, bound = OL.within_tolerance(y, y_ref, TOL)
+    assert ok, f"max err {err:.3g} > {bound:.3g}"
+    w_hat = OL.dequantize(q, s)
+    y64 = x.double() @ w_hat.double().T + b.double()
+    err_gpu = float((y.cpu().double() - y64).abs().max())
+    err_cpu = float((y_ref.double() - y64).abs().max())
+    floor = 2.0 ** -24 * float(y64.abs().max())
+    assert err_gpu <= 8 * max(err_cpu, floor), f"error {err_gpu:.3g} vs fp32 oracle {err_cpu:.3g}"
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 256])
 def test_linear_w8_dispatch(dev, c_oracle, M):
     _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.bfloat16, seed=M)
