@@ -106,6 +106,7 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
 int run_linear(const LinearArgs& a) {
     int rc = check_linear(a);
     if (rc != TIQ_OK || a.M == 0 || a.N == 0) return rc;
+    if (skinny_supported(a)) return launch_skinny(a);
     if (a.M >= kGemmMinRows && gemm_supported(a)) return launch_gemm(a);
     return launch_gemv(a);
 }
@@ -204,6 +205,7 @@ extern "C" int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K
     a.fuse.ldr = ld_residual;
     int rc = check_linear(a);
     if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    if (skinny_supported(a)) return launch_skinny(a);
     return launch_gemv(a);
 }
 

@@ -55,6 +55,12 @@ int launch_gemm(const LinearArgs& a);
 // True when the MFMA GEMM has a kernel for these arguments.
 bool gemm_supported(const LinearArgs& a);
 
+// Decode linear on the matrix cores for 5..64 rows of fp32 activations
+// (skinny.hip): int8 or fp32 weights, with the decode fusions.
+constexpr int64_t kSkinnyMinRows = 5;
+bool skinny_supported(const LinearArgs& a);
+int launch_skinny(const LinearArgs& a);
+
 // The register-staged int8 GEMM (gemm_staged.hip): whether it takes these
 // arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128) and
 // its launch.

@@ -160,3 +160,20 @@ def test_graph_decode_matches_reference_gpt2_small(reference_decode, dev):
     prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
     out = g.generate_graph(qm, prompt, gr["new_tokens"])
     assert out.cpu().tolist() == gr["ids"]
+
+
+@pytest.mark.parametrize("batch", [8, 32])
+def test_batched_fused_decode_matches_oracle(reference_decode, dev, batch):
+    """Batched greedy decode (the matrix-core decode linears at M = batch, the
+    three-plane prefill at M = batch * T >= 128) against the oracle's fp32
+    CPU generation of the same seed-0 model: identical token ids."""
+    c = dict(vocab_size=97, n_positions=96, n_layer=2, n_head=2, n_embd=128)  # head_dim 64: the fused decoder
+    shp = OM.Shape(c["vocab_size"], c["n_positions"], c["n_layer"], c["n_head"], c["n_embd"])
+    qp, _ = OM.quantize_params(OM.init_params(shp, 0), 8)
+    prompt = OM.benchmark_prompt(shp.vocab_size, batch, 16)
+    want, margins = OM.generate_greedy(qp, shp, prompt, 20)
+    qm, _ = g.quantize_model(_model(c, dev), 8)
+    dec = g.make_decoder(qm, batch, 36)
+    assert isinstance(dec, g.FusedDecoder)
+    got = g.generate_graph(qm, prompt.to(dev), 20, decoder=dec)
+    assert got.cpu().tolist() == want.tolist(), f"min margin {min(margins):.3g}"

@@ -61,6 +61,85 @@ def test_fused_ln_gelu_linear(dev, c_oracle, M, K, N):
     assert ok, (err, bound)
 
 
+# Batched decode rows (5..64) take the matrix-core kernel: activations split
+# exactly into three bf16 planes, so the result is fp32-accurate -- checked
+# against a float64 computation of the same ops: the kernel's error is within
+# a small factor of torch fp32's own error on the same inputs.
+def _f64_check(y, ref32, ref64):
+    err = float((y.cpu().double() - ref64).abs().max())
+    err32 = float((ref32.double() - ref64).abs().max())
+    floor = 2.0 ** -24 * float(ref64.abs().max())
+    assert err <= 8 * max(err32, floor), f"error {err:.3g} vs torch fp32 {err32:.3g}"
+
+
+@pytest.mark.parametrize("M", [5, 16, 32, 33, 64])
+@pytest.mark.parametrize("K,N", [(1600, 4800), (768, 2304)])
+def test_batched_ln_gelu_linear(dev, c_oracle, M, K, N):
+    gen = torch.Generator().manual_seed(M * 11 + K)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen) * 2 + 0.5
+    lw = 1 + 0.1 * torch.randn(K, generator=gen)
+    lb = 0.1 * torch.randn(K, generator=gen)
+    b = 0.1 * torch.randn(N, generator=gen)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    y = torch.empty(M, N, device=dev)
+    xd, qd, sd, bd = x.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
+    lwd, lbd = lw.to(dev), lb.to(dev)
+    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
+                                     bd.data_ptr(), N, y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5,
+                                     _lib.ACT_GELU_TANH, None, 0, _st())
+    _lib.check(rc, "fused batched")
+    torch.cuda.synchronize()
+    w_hat = OL.dequantize(q, s)
+    ref = _gelu(OL.linear_ref(F.layer_norm(x, (K,), lw, lb, 1e-5), w_hat, b))
+    ok, err, bound = OL.within_tolerance(y, ref)
+    assert ok, (err, bound)
+    xn64 = F.layer_norm(x.double(), (K,), lw.double(), lb.double(), 1e-5)
+    _f64_check(y, ref, _gelu(xn64 @ w_hat.double().T + b.double()))
+
+
+@pytest.mark.parametrize("M", [8, 32])
+@pytest.mark.parametrize("K,N", [(6400, 1600), (3072, 768)])
+def test_batched_residual_in_place(dev, c_oracle, M, K, N):
+    gen = torch.Generator().manual_seed(M + K)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    h = torch.randn(M, K, generator=gen)
+    x0 = torch.randn(M, N, generator=gen)
+    b = 0.1 * torch.randn(N, generator=gen)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    x = x0.to(dev).clone()
+    hd, qd, sd, bd = h.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
+    rc = _lib.lib().tiq_linear_fused(hd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None,
+                                     0, bd.data_ptr(), N, x.data_ptr(), 0, N, None, None, 1e-5, 0, x.data_ptr(), N,
+                                     _st())
+    _lib.check(rc, "fused batched residual")
+    torch.cuda.synchronize()
+    w_hat = OL.dequantize(q, s)
+    ref = x0 + OL.linear_ref(h, w_hat, b)
+    assert (x.cpu() - ref).abs().max() <= 1e-3 * ref.abs().max()
+    _f64_check(x, ref, x0.double() + h.double() @ w_hat.double().T + b.double())
+
+
+@pytest.mark.parametrize("M", [6, 32])
+def test_batched_fp32_head(dev, M):
+    """fp32 weights (the tied lm_head) with LayerNorm, N not a multiple of 32."""
+    K, N = 768, 5003
+    gen = torch.Generator().manual_seed(M)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen)
+    lw = 1 + 0.1 * torch.randn(K, generator=gen)
+    lb = 0.1 * torch.randn(K, generator=gen)
+    y = torch.empty(M, N, device=dev)
+    xd, wd, lwd, lbd = x.to(dev), w.to(dev), lw.to(dev), lb.to(dev)
+    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, wd.data_ptr(), _lib.WF_F32, None, None, 0, None, N,
+                                     y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5, 0, None, 0, _st())
+    _lib.check(rc, "fused batched fp32 head")
+    torch.cuda.synchronize()
+    ref = F.layer_norm(x, (K,), lw, lb, 1e-5) @ w.T
+    ref64 = F.layer_norm(x.double(), (K,), lw.double(), lb.double(), 1e-5) @ w.double().T
+    _f64_check(y, ref, ref64)
+
+
 @pytest.mark.parametrize("M", [1, 2])
 def test_fused_residual_in_place_and_int4(dev, c_oracle, M):
     K, N = 3072, 768
