@@ -183,11 +183,11 @@ extern "C" int tiq_linear_w4(const void* x, int x_dtype, int64_t M, int64_t K, i
                                 stream, kW4));
 }
 
-extern "C" int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w,
-                                int w_format, const float* scale, const uint16_t* scale_f16, int group,
-                                const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
-                                const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
-                                const float* residual, int64_t ld_residual, void* stream) {
+static int linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w, int w_format,
+                        const float* scale, const uint16_t* scale_f16, int group, const float* bias, int64_t N,
+                        void* y, int y_dtype, int64_t ldy, const float* ln_weight, const float* ln_bias,
+                        float ln_eps, int activation, const float* residual, int64_t ld_residual, void* workspace,
+                        size_t workspace_bytes, void* stream) {
     if (w_format < TIQ_WF_INT8 || w_format > TIQ_WF_F32) return TIQ_EINVAL;
     if (activation != TIQ_ACT_NONE && activation != TIQ_ACT_GELU_TANH) return TIQ_EINVAL;
     if ((ln_weight == nullptr) != (ln_bias == nullptr)) return TIQ_EINVAL;
@@ -203,10 +203,39 @@ extern "C" int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K
     a.fuse.act = activation;
     a.fuse.res = residual;
     a.fuse.ldr = ld_residual;
+    a.ws = workspace;
+    a.ws_bytes = workspace_bytes;
     int rc = check_linear(a);
     if (rc != TIQ_OK || M == 0 || N == 0) return rc;
     if (skinny_supported(a)) return launch_skinny(a);
     return launch_gemv(a);
+}
+
+extern "C" int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w,
+                                int w_format, const float* scale, const uint16_t* scale_f16, int group,
+                                const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                                const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                                const float* residual, int64_t ld_residual, void* stream) {
+    return linear_fused(x, x_dtype, M, K, ldx, w, w_format, scale, scale_f16, group, bias, N, y, y_dtype, ldy,
+                        ln_weight, ln_bias, ln_eps, activation, residual, ld_residual, nullptr, 0, stream);
+}
+
+extern "C" size_t tiq_linear_fused_workspace(int x_dtype, int w_format, int64_t M, int64_t K, int64_t N) {
+    if (x_dtype != TIQ_F32 || (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_F32)) return 0;
+    if (M < kSkinnyMinRows || M > 64 || K <= 0 || K % 32 != 0 || N <= 0) return 0;
+    return skinny_workspace(M, K);
+}
+
+extern "C" int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w,
+                                   int w_format, const float* scale, const uint16_t* scale_f16, int group,
+                                   const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                                   const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                                   const float* residual, int64_t ld_residual, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    if (workspace && !aligned(workspace, 16)) return TIQ_EALIGN;
+    return linear_fused(x, x_dtype, M, K, ldx, w, w_format, scale, scale_f16, group, bias, N, y, y_dtype, ldy,
+                        ln_weight, ln_bias, ln_eps, activation, residual, ld_residual, workspace, workspace_bytes,
+                        stream);
 }
 
 extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,

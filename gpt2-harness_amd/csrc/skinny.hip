@@ -14,10 +14,11 @@
 //     accurate as an fp32 product. fp32 weights are split the same way and
 //     the six plane products with combined weight >= 2^-16 are kept (the
 //     dropped ones are below fp32 rounding of the sum).
-//   * Each wavefront loads its weight slices straight into MFMA operand
-//     registers (lane (r, h) holds 16 consecutive K of weight row r), 4 units
-//     at a time (2 for fp32 weights), double buffered, and converts them in
-//     registers.
+//   * Each wavefront requests all of its weight slices at once, straight into
+//     MFMA operand registers (lane (r, h) holds 16 consecutive K of weight
+//     row r): the whole matrix is in flight together, which a decode linear
+//     (a few MB read once) needs to approach HBM bandwidth. They are converted
+//     in registers as the units are consumed.
 //   * LayerNorm statistics (two-pass mean and biased variance, as torch) are
 //     computed over the workgroup's activation rows, which needs K covered by
 //     one workgroup (at most 2048 with 8 wavefronts of 8 units).
@@ -33,9 +34,17 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
-// units per load batch: 4 for int8 weights, 2 for fp32 weights (4x the bytes)
+// Units (32 K each) a wavefront holds in registers: all of its share of K.
+// int8: 25 units (K <= 8 * 25 * 32 = 6400); fp32 weights (4x the bytes): 8.
 template <int WF>
-constexpr int chunk_units() { return WF == kW8 ? 4 : 2; }
+constexpr int max_units() { return WF == kW8 ? 25 : 8; }
+// activation units in flight per wavefront (ring): 4, 3 with fp32 weights
+template <int WF>
+constexpr int ring_units() { return WF == kW8 ? 4 : 3; }
+// With int8 weights and the plane input, up to kPlUnits units per wavefront
+// (K <= 8 * 7 * 32 = 1792) have every activation operand in flight at once;
+// longer K streams them through the ring.
+constexpr int kPlUnits = 7;
 constexpr int kLnMaxK = kWaves * 8 * 32;
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
@@ -81,18 +90,88 @@ __device__ __forceinline__ void store_out(TY* p, float v) {
     else *p = f32_to_bf16_bits(v);
 }
 
+// LayerNorm (optional) and the exact three-plane split of M activation rows,
+// once per linear, into MFMA operand order: for row tile t (32 rows), unit u
+// (32 K), plane q and half e, a 1 KB block holds the 16-byte operand of each
+// lane l = 32 h + r (row 32 t + r, K = 32 u + 16 h + 8 e + 0..7), so that
+// the product kernel reads each operand with one contiguous load.
+// One workgroup per row; two-pass mean and biased variance as torch.
+template <bool LN>
+__global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__ x, int64_t ldx, int K,
+                                                       const float* __restrict__ ln_w,
+                                                       const float* __restrict__ ln_b, float ln_eps,
+                                                       uint16_t* __restrict__ x3) {
+    __shared__ float part[4];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (int64_t)m * ldx;
+    float mu = 0.f, rs = 1.f;
+    if (LN) {
+        float s = 0.f;
+        for (int k = 4 * tid; k < K; k += 1024) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + k);
+            s += (v.x + v.y) + (v.z + v.w);
+        }
+        s = wave_sum(s);
+        if ((tid & 63) == 0) part[tid >> 6] = s;
+        __syncthreads();
+        mu = ((part[0] + part[1]) + (part[2] + part[3])) / (float)K;
+        __syncthreads();
+        float d = 0.f;
+        for (int k = 4 * tid; k < K; k += 1024) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + k);
+            const float a = v.x - mu, b = v.y - mu, c = v.z - mu, e = v.w - mu;
+            d += (a * a + b * b) + (c * c + e * e);
+        }
+        d = wave_sum(d);
+        if ((tid & 63) == 0) part[tid >> 6] = d;
+        __syncthreads();
+        rs = 1.0f / sqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)K + ln_eps);
+    }
+    const int U = K / 32, t = m >> 5, r = m & 31;
+    for (int c = tid; c < K / 8; c += 256) {  // 8 consecutive K per thread: one operand chunk
+        const int k = 8 * c, u = k >> 5, h = (k >> 4) & 1, e = (k >> 3) & 1;
+        float v[8];
+        *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(xr + k);
+        *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(xr + k + 4);
+        if (LN) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = (v[i] - mu) * rs * ln_w[k + i] + ln_b[k + i];
+        }
+        u32x4 pl[3];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = v[2 * i], x1 = v[2 * i + 1];
+            const uint32_t hh = pk_bf16(x0, x1);
+            const float r0 = x0 - bf_lo(hh), r1 = x1 - bf_hi(hh);
+            const uint32_t l = pk_bf16(r0, r1);
+            pl[0][i] = hh;
+            pl[1][i] = l;
+            pl[2][i] = pk_bf16(r0 - bf_lo(l), r1 - bf_hi(l));
+        }
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            const int64_t blk = (((int64_t)t * U + u) * 3 + q) * 2 + e;
+            *reinterpret_cast<u32x4*>(x3 + (blk * 64 + 32 * h + r) * 8) = pl[q];
+        }
+    }
+}
+
 // WF: kW8 (int8 codes, per-row scale) or kF32 (fp32 weights, no scale).
-template <int WF, typename TY>
+// PL: activations arrive as the three bf16 planes of ln_split_kernel (x is
+// then a uint16_t pointer with row stride 3 K and LayerNorm already applied)
+// instead of fp32 rows split here.
+template <int WF, bool PL, typename TY>
 __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int K, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, int N, TY* __restrict__ y, int64_t ldy,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps, int act,
     const float* __restrict__ res, int64_t ldr) {
     constexpr int WB = (WF == kW8) ? 16 : 64;  // weight bytes a lane loads per unit
-    constexpr int kChunk = chunk_units<WF>();
+    constexpr int kXp = ring_units<WF>();
     __shared__ float red[kWaves][32][33];      // partial output tiles, rows padded
     __shared__ float stat[kWaves][32];
     __shared__ float mean_s[32], rstd_s[32];
+    __shared__ __attribute__((aligned(16))) float gb_s[2][kLnMaxK];  // LayerNorm weight and bias
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int r = lane & 31, h = lane >> 5;
@@ -101,11 +180,31 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const int u0 = wave * U / kWaves, u1 = (wave + 1) * U / kWaves;
     const bool xrow_ok = m0 + r < M;
     const float* xr = x + (int64_t)(xrow_ok ? m0 + r : 0) * ldx + 16 * h;  // + 32 u
+    // plane input: this row tile's operand blocks, lane-contiguous
+    const uint16_t* x3t = reinterpret_cast<const uint16_t*>(x) + (int64_t)blockIdx.y * (K / 32) * 6 * 64 * 8 + lane * 8;
     const uint8_t* wr = w + (int64_t)min(n0 + r, N - 1) * ldw + WB * h;    // + 2 WB u
 
-    // LayerNorm statistics of the 32 activation rows (two-pass)
+    const int cnt = u1 - u0;  // <= kUnits (the host checks K)
+    constexpr int kUnits = max_units<WF>();
+    // every weight slice of the wavefront is requested first, so the whole
+    // matrix is in flight at once (behind the LayerNorm statistics);
+    // activations (L2 hits) follow through a ring of kXp unit registers
+    u32x4 wreg[kUnits][WB / 16];
+#pragma unroll
+    for (int c = 0; c < kUnits; ++c)
+        if (c < cnt)
+#pragma unroll
+            for (int q = 0; q < WB / 16; ++q)
+                wreg[c][q] = *reinterpret_cast<const u32x4*>(wr + 2 * WB * (u0 + c) + 16 * q);
+    // LayerNorm statistics of the 32 activation rows (two-pass); its weight
+    // and bias go to LDS (read there, they add no global loads to the unit
+    // loop, whose in-order waits would otherwise include the prefetches)
     float mu = 0.f, rs = 1.f;
-    if (ln_w) {
+    if (!PL && ln_w) {
+        for (int i = threadIdx.x; i < K / 4; i += kWaves * 64) {
+            reinterpret_cast<float4*>(gb_s[0])[i] = reinterpret_cast<const float4*>(ln_w)[i];
+            reinterpret_cast<float4*>(gb_s[1])[i] = reinterpret_cast<const float4*>(ln_b)[i];
+        }
         float s = 0.f;
         for (int u = u0; u < u1; ++u) {
 #pragma unroll
@@ -152,85 +251,141 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
 #pragma unroll
     for (int q = 0; q < 16; ++q) acc[q] = 0.f;
 
-    // register batches: kChunk units of activations (16 fp32) and weights
-    float xa[2][kChunk][16];
-    u32x4 wa[2][kChunk][WB / 16];
-    auto load = [&](int b, int ub) {
+    // compute one unit: activations v (16 fp32 of row r, K = 32 u + 16 h + 0..15)
+    // and the weight registers of the same K
+    auto unit = [&](int u, const float (&xv)[16], const u32x4 (&wv)[WB / 16]) {
+        const int k0 = 32 * u + 16 * h;
+        float v[16];
 #pragma unroll
-        for (int c = 0; c < kChunk; ++c) {
-            const int u = ub + c < u1 ? ub + c : u1 - 1;  // past the end: repeat (unused)
+        for (int i = 0; i < 16; ++i) v[i] = xrow_ok ? xv[i] : 0.f;
+        if (ln_w) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float4 v = *reinterpret_cast<const float4*>(xr + 32 * u + 4 * q);
-                xa[b][c][4 * q] = v.x;
-                xa[b][c][4 * q + 1] = v.y;
-                xa[b][c][4 * q + 2] = v.z;
-                xa[b][c][4 * q + 3] = v.w;
+                const float4 g = *reinterpret_cast<const float4*>(gb_s[0] + k0 + 4 * q);
+                const float4 bb = *reinterpret_cast<const float4*>(gb_s[1] + k0 + 4 * q);
+                v[4 * q] = xrow_ok ? (v[4 * q] - mu) * rs * g.x + bb.x : 0.f;
+                v[4 * q + 1] = xrow_ok ? (v[4 * q + 1] - mu) * rs * g.y + bb.y : 0.f;
+                v[4 * q + 2] = xrow_ok ? (v[4 * q + 2] - mu) * rs * g.z + bb.z : 0.f;
+                v[4 * q + 3] = xrow_ok ? (v[4 * q + 3] - mu) * rs * g.w + bb.w : 0.f;
             }
-#pragma unroll
-            for (int q = 0; q < WB / 16; ++q)
-                wa[b][c][q] = *reinterpret_cast<const u32x4*>(wr + 2 * WB * u + 16 * q);
         }
-    };
-    auto compute = [&](int b, int ub) {
 #pragma unroll
-        for (int c = 0; c < kChunk; ++c) {
-            if (ub + c >= u1) break;
-            const int k0 = 32 * (ub + c) + 16 * h;
-            float v[16];
+        for (int e = 0; e < 2; ++e) {
+            float ve[8];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = xrow_ok ? xa[b][c][i] : 0.f;
-            if (ln_w) {
+            for (int i = 0; i < 8; ++i) ve[i] = v[8 * e + i];
+            bf16x8 x0, x1, x2;
+            split3(ve, x0, x1, x2);
+            if constexpr (WF == kW8) {
+                const u32x4 d = wv[0];
+                const uint32_t s0 = e == 0 ? d.x : d.z, s1 = e == 0 ? d.y : d.w;
+                const u32x4 wq = {bf16x2_of_bytes(s0, 0), bf16x2_of_bytes(s0, 16), bf16x2_of_bytes(s1, 0),
+                                  bf16x2_of_bytes(s1, 16)};
+                const bf16x8 wf = __builtin_bit_cast(bf16x8, wq);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, x0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, x1, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, x2, acc, 0, 0, 0);
+            } else {
+                float wf[8];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 g = *reinterpret_cast<const float4*>(ln_w + k0 + 4 * q);
-                    const float4 bb = *reinterpret_cast<const float4*>(ln_b + k0 + 4 * q);
-                    v[4 * q] = xrow_ok ? (v[4 * q] - mu) * rs * g.x + bb.x : 0.f;
-                    v[4 * q + 1] = xrow_ok ? (v[4 * q + 1] - mu) * rs * g.y + bb.y : 0.f;
-                    v[4 * q + 2] = xrow_ok ? (v[4 * q + 2] - mu) * rs * g.z + bb.z : 0.f;
-                    v[4 * q + 3] = xrow_ok ? (v[4 * q + 3] - mu) * rs * g.w + bb.w : 0.f;
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                float ve[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) ve[i] = v[8 * e + i];
-                bf16x8 x0, x1, x2;
-                split3(ve, x0, x1, x2);
-                if constexpr (WF == kW8) {
-                    const u32x4 d = wa[b][c][0];
-                    const uint32_t s0 = e == 0 ? d.x : d.z, s1 = e == 0 ? d.y : d.w;
-                    const u32x4 wv = {bf16x2_of_bytes(s0, 0), bf16x2_of_bytes(s0, 16), bf16x2_of_bytes(s1, 0),
-                                      bf16x2_of_bytes(s1, 16)};
-                    const bf16x8 wf = __builtin_bit_cast(bf16x8, wv);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, x0, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, x1, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, x2, acc, 0, 0, 0);
-                } else {
-                    float wv[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) wv[i] = __uint_as_float(wa[b][c][2 * e + i / 4][i % 4]);
-                    bf16x8 w0, w1, w2;
-                    split3(wv, w0, w1, w2);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, x0, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, x1, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, x0, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, x2, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, x1, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w2, x0, acc, 0, 0, 0);
-                }
+                for (int i = 0; i < 8; ++i) wf[i] = __uint_as_float(wv[2 * e + i / 4][i % 4]);
+                bf16x8 w0, w1, w2;
+                split3(wf, w0, w1, w2);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, x0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, x1, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, x0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, x2, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, x1, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w2, x0, acc, 0, 0, 0);
             }
         }
     };
-    // two register batches, alternating (literal indices keep them in VGPRs)
-    if (u0 < u1) load(0, u0);
-    for (int ub = u0; ub < u1; ub += 2 * kChunk) {
-        if (ub + kChunk < u1) load(1, ub + kChunk);
-        compute(0, ub);
-        if (ub + kChunk >= u1) break;
-        if (ub + 2 * kChunk < u1) load(0, ub + 2 * kChunk);
-        compute(1, ub + kChunk);
+    // plane mode: the 6 operand registers of a unit come straight from x3
+    auto unit_pl = [&](const u32x4 (&xv)[3][2], const u32x4 (&wv)[WB / 16]) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            bf16x8 xq[3];
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                u32x4 t = xv[q][e];
+                if (!xrow_ok) t = u32x4{0u, 0u, 0u, 0u};
+                xq[q] = __builtin_bit_cast(bf16x8, t);
+            }
+            if constexpr (WF == kW8) {
+                const u32x4 d = wv[0];
+                const uint32_t s0 = e == 0 ? d.x : d.z, s1 = e == 0 ? d.y : d.w;
+                const u32x4 wq = {bf16x2_of_bytes(s0, 0), bf16x2_of_bytes(s0, 16), bf16x2_of_bytes(s1, 0),
+                                  bf16x2_of_bytes(s1, 16)};
+                const bf16x8 wf = __builtin_bit_cast(bf16x8, wq);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xq[0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xq[1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xq[2], acc, 0, 0, 0);
+            } else {
+                float wf[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) wf[i] = __uint_as_float(wv[2 * e + i / 4][i % 4]);
+                bf16x8 w0, w1, w2;
+                split3(wf, w0, w1, w2);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, xq[0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, xq[1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, xq[0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, xq[2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, xq[1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w2, xq[0], acc, 0, 0, 0);
+            }
+        }
+    };
+    auto xload_pl = [&](int u, u32x4 (&xv)[3][2]) {
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                xv[q][e] = *reinterpret_cast<const u32x4*>(x3t + (((int64_t)u * 3 + q) * 2 + e) * 64 * 8);
+    };
+    auto xload = [&](int u, float (&xv)[16]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + 32 * u + 4 * q);
+            xv[4 * q] = v.x;
+            xv[4 * q + 1] = v.y;
+            xv[4 * q + 2] = v.z;
+            xv[4 * q + 3] = v.w;
+        }
+    };
+
+    if (PL && WF == kW8 && cnt <= kPlUnits) {
+        // every activation unit in flight too
+        u32x4 pall[kPlUnits][3][2];
+#pragma unroll
+        for (int c = 0; c < kPlUnits; ++c)
+            if (c < cnt) xload_pl(u0 + c, pall[c]);
+#pragma unroll
+        for (int c = 0; c < kPlUnits; ++c)
+            if (c < cnt) unit_pl(pall[c], wreg[c]);
+    } else if constexpr (PL) {
+        u32x4 pring[kXp][3][2];
+#pragma unroll
+        for (int c = 0; c < kXp; ++c)
+            if (c < cnt) xload_pl(u0 + c, pring[c]);
+#pragma unroll
+        for (int c = 0; c < kUnits; ++c) {
+            if (c < cnt) {
+                unit_pl(pring[c % kXp], wreg[c]);
+                if (c + kXp < cnt) xload_pl(u0 + c + kXp, pring[c % kXp]);
+            }
+        }
+    } else {
+        float xring[kXp][16];
+#pragma unroll
+        for (int c = 0; c < kXp; ++c)
+            if (c < cnt) xload(u0 + c, xring[c]);
+#pragma unroll
+        for (int c = 0; c < kUnits; ++c) {
+            if (c < cnt) {
+                unit(u0 + c, xring[c % kXp], wreg[c]);
+                if (c + kXp < cnt) xload(u0 + c + kXp, xring[c % kXp]);
+            }
+        }
     }
 
     // partial tiles -> LDS: register q of lane (r, h) is output row
@@ -239,14 +394,22 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     for (int q = 0; q < 16; ++q) red[wave][r][8 * (q >> 2) + 4 * h + (q & 3)] = acc[q];
     __syncthreads();
     // 1024 outputs, two per thread: m = o / 32, n = o % 32 (a row of y per 32 threads)
+    float vsum[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int o = threadIdx.x + kWaves * 64 * t;
+        const int m = o >> 5, nn = o & 31;
+        float v = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) v += red[i][m][nn];
+        vsum[t] = v;
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int o = threadIdx.x + kWaves * 64 * t;
         const int m = o >> 5, nn = o & 31;
         const int gm = m0 + m, gn = n0 + nn;
-        float v = 0.f;
-#pragma unroll
-        for (int i = 0; i < kWaves; ++i) v += red[i][m][nn];
+        float v = vsum[t];
         if (gm < M && gn < N) {
             if (WF == kW8) v *= scale[gn];
             if (bias) v += bias[gn];
@@ -257,20 +420,48 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     }
 }
 
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace: the split activation planes, row tiles x 32 x 3K bf16 in operand order.
+size_t planes_bytes(int64_t M, int64_t K) { return round256((size_t)((M + 31) / 32) * 32 * 3 * K * 2); }
+
 template <int WF, typename TY>
 int run_skinny(const LinearArgs& a) {
     const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 31) / 32));
-    hipLaunchKernelGGL((skinny_kernel<WF, TY>), grid, dim3(kWaves * 64), 0, a.stream, static_cast<const float*>(a.x),
-                       a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N, static_cast<TY*>(a.y),
-                       a.ldy, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, a.fuse.act, a.fuse.res, a.fuse.ldr);
+    if (a.ws && a.ws_bytes >= planes_bytes(a.M, a.K)) {
+        // LayerNorm + split once, then the products on the planes
+        uint16_t* x3 = static_cast<uint16_t*>(a.ws);
+        if (a.fuse.ln_w)
+            hipLaunchKernelGGL(ln_split_kernel<true>, dim3((unsigned)a.M), dim3(256), 0, a.stream,
+                               static_cast<const float*>(a.x), a.ldx, (int)a.K, a.fuse.ln_w, a.fuse.ln_b,
+                               a.fuse.ln_eps, x3);
+        else
+            hipLaunchKernelGGL(ln_split_kernel<false>, dim3((unsigned)a.M), dim3(256), 0, a.stream,
+                               static_cast<const float*>(a.x), a.ldx, (int)a.K, nullptr, nullptr, 0.f, x3);
+        int rc = launch_status();
+        if (rc != TIQ_OK) return rc;
+        hipLaunchKernelGGL((skinny_kernel<WF, true, TY>), grid, dim3(kWaves * 64), 0, a.stream,
+                           reinterpret_cast<const float*>(x3), (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
+                           a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
+                           a.fuse.res, a.fuse.ldr);
+        return launch_status();
+    }
+    hipLaunchKernelGGL((skinny_kernel<WF, false, TY>), grid, dim3(kWaves * 64), 0, a.stream,
+                       static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias,
+                       (int)a.N, static_cast<TY*>(a.y), a.ldy, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, a.fuse.act,
+                       a.fuse.res, a.fuse.ldr);
     return launch_status();
 }
 
 }  // namespace
 
+size_t skinny_workspace(int64_t M, int64_t K) { return planes_bytes(M, K); }
+
 bool skinny_supported(const LinearArgs& a) {
     if (a.x_dtype != TIQ_F32 || (a.fmt != kW8 && a.fmt != kF32)) return false;
     if (a.M < kSkinnyMinRows || a.M > 64 || a.K % 32 != 0 || a.N > 0x7fffffff) return false;
+    const int64_t units = (a.K / 32 + kWaves - 1) / kWaves;
+    if (units > (a.fmt == kW8 ? max_units<kW8>() : max_units<kF32>())) return false;
     if (!aligned(a.x, 16) || a.ldx % 4 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
     if (a.fuse.ln_w && (a.K > kLnMaxK || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16))) return false;
     // the residual may alias y only element for element

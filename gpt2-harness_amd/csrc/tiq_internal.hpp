@@ -45,6 +45,10 @@ struct LinearArgs {
     // 0 means K. The fp32-activation path passes K = 3 kw (x split into three
     // bf16 planes laid side by side along K).
     int64_t kw = 0;
+    // Optional device workspace (the decode linears stage LayerNorm'd,
+    // split activations there when it is large enough).
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
 };
 
 // Validates the common arguments; TIQ_OK when they are consistent.
@@ -60,6 +64,8 @@ bool gemm_supported(const LinearArgs& a);
 constexpr int64_t kSkinnyMinRows = 5;
 bool skinny_supported(const LinearArgs& a);
 int launch_skinny(const LinearArgs& a);
+// Workspace bytes with which it splits the activations once per call.
+size_t skinny_workspace(int64_t M, int64_t K);
 
 // The register-staged int8 GEMM (gemm_staged.hip): whether it takes these
 // arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128) and

@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_linear_w4g": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_linear_fused": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
                           _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp], _i32),
+    "tiq_linear_fused_workspace": ([_i32, _i32, _i64, _i64, _i64], _sz),
+    "tiq_linear_fused_ws": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
+                             _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp, _sz, _vp], _i32),
     "tiq_decode_attention": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),

@@ -231,18 +231,27 @@ class FusedDecoder(_DecoderBase):
         self.head_w = model.lm_head.weight.detach().contiguous()
         self.L = _lib.lib()
         self.argmax_ws = torch.empty(int(self.L.tiq_argmax_rows_workspace(B)), dtype=torch.uint8, device=dev)
+        # batched steps stage LayerNorm'd, split activations here (0 bytes: the
+        # single-row GEMV path, which needs none)
+        hidden = model.h[0].mlp.c_fc.out_features
+        qkv = C + 2 * self.Hkv * self.hd
+        ws = max(int(self.L.tiq_linear_fused_workspace(_lib.F32, _lib.WF_INT8, B, k, n))
+                 for k, n in ((C, qkv), (C, C), (C, hidden), (hidden, C)))
+        ws = max(ws, int(self.L.tiq_linear_fused_workspace(_lib.F32, _lib.WF_F32, B, C, cfg.vocab_size)))
+        self.lin_ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
+        self.lin_ws_bytes = ws
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
         st = torch.cuda.current_stream(self.dev).cuda_stream
         scale16 = lin.scale.data_ptr() if lin.fmt == FMT_W4G else None
         scale = None if lin.fmt == FMT_W4G else lin.scale.data_ptr()
-        rc = self.L.tiq_linear_fused(
+        rc = self.L.tiq_linear_fused_ws(
             x.data_ptr(), _lib.F32, M, K, x.stride(0), lin.codes.data_ptr(), _WF[lin.fmt], scale, scale16,
             lin.group_size, _lib.ptr(lin.bias), lin.out_features, y.data_ptr(), _lib.F32, y.stride(0),
             None if ln is None else ln.weight.data_ptr(), None if ln is None else ln.bias.data_ptr(),
             float(ln.eps) if ln is not None else 1e-5, act, None if res is None else res.data_ptr(),
-            0 if res is None else res.stride(0), st)
+            0 if res is None else res.stride(0), self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
         _lib.check(rc, "fused decode linear")
 
     def _step(self) -> None:
@@ -263,9 +272,10 @@ class FusedDecoder(_DecoderBase):
             self._linear(mlp.c_fc, self.x, self.hid, ln=block.ln_2, act=_lib.ACT_GELU_TANH)
             self._linear(mlp.c_proj, self.hid, self.x, res=self.x)
         ln = m.ln_f
-        rc = L.tiq_linear_fused(self.x.data_ptr(), _lib.F32, B, C, C, self.head_w.data_ptr(), _lib.WF_F32, None,
-                                None, 0, None, cfg.vocab_size, self.logits.data_ptr(), _lib.F32, cfg.vocab_size,
-                                ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps), 0, None, 0, st)
+        rc = L.tiq_linear_fused_ws(self.x.data_ptr(), _lib.F32, B, C, C, self.head_w.data_ptr(), _lib.WF_F32, None,
+                                   None, 0, None, cfg.vocab_size, self.logits.data_ptr(), _lib.F32, cfg.vocab_size,
+                                   ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps), 0, None, 0,
+                                   self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
         _lib.check(rc, "lm_head")
         # argmax also records the token at slot pos + 1 and advances pos
         _lib.check(L.tiq_argmax_rows(self.logits.data_ptr(), B, cfg.vocab_size, cfg.vocab_size,

@@ -194,6 +194,29 @@ int tiq_linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
                      const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
                      const float* residual, int64_t ld_residual, void* stream);
 
+/* Workspace bytes tiq_linear_fused_ws uses for an (M, K) x (N, K) product
+ * (0: none). Nonzero for fp32 activations with 5 <= M <= 64 (a batched
+ * decode step) and int8 or fp32 weights: the split activations, 32-row tiles
+ * x 3K bf16 (ceil(M / 32) * 32 * 3K * 2 bytes, rounded up to 256). N does not
+ * change the size today. The contents need no initialisation and are not
+ * preserved; calls that share a workspace must not overlap. */
+size_t tiq_linear_fused_workspace(int x_dtype, int w_format, int64_t M, int64_t K, int64_t N);
+
+/* tiq_linear_fused with a caller workspace -- the same decode linear of
+ * Block.forward (model.py:410-427) and lm_head (model.py:585). For a batched
+ * decode step (5 <= M <= 64 rows of fp32 activations, int8 or fp32 weights)
+ * the rows are LayerNorm'd (if requested) and split exactly into three bf16
+ * planes once, into the workspace, and the product runs on the matrix cores
+ * from those planes; without a large enough workspace the same kernels split
+ * the rows themselves (more vector work per weight row). Results are
+ * fp32-accurate either way. The workspace must be 16-byte aligned. */
+int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* w,
+                        int w_format, const float* scale, const uint16_t* scale_f16, int group,
+                        const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                        const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                        const float* residual, int64_t ld_residual, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* Self-attention of one new token per sequence (model.py:248-318 at T = 1,
  * KVCache.update model.py:153-172): qkv is the (batch, (n_head + 2 n_kv_head)
  * * head_dim) output of c_attn (leading dim ld_qkv); its k and v are written

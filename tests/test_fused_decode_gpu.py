@@ -72,9 +72,22 @@ def _f64_check(y, ref32, ref64):
     assert err <= 8 * max(err32, floor), f"error {err:.3g} vs torch fp32 {err32:.3g}"
 
 
+def _fused_ws(*args):
+    """tiq_linear_fused_ws with a workspace of the queried size (args are
+    those of tiq_linear_fused; the stream comes last)."""
+    L = _lib.lib()
+    M, K, w_format, N = args[2], args[3], args[6], args[11]
+    n = int(L.tiq_linear_fused_workspace(args[1], w_format, M, K, N))
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+    rc = L.tiq_linear_fused_ws(*args[:-1], ws.data_ptr(), n, args[-1])
+    torch.cuda.synchronize()
+    return rc
+
+
+@pytest.mark.parametrize("use_ws", [False, True])
 @pytest.mark.parametrize("M", [5, 16, 32, 33, 64])
 @pytest.mark.parametrize("K,N", [(1600, 4800), (768, 2304)])
-def test_batched_ln_gelu_linear(dev, c_oracle, M, K, N):
+def test_batched_ln_gelu_linear(dev, c_oracle, M, K, N, use_ws):
     gen = torch.Generator().manual_seed(M * 11 + K)
     w = torch.randn(N, K, generator=gen) * 0.02
     x = torch.randn(M, K, generator=gen) * 2 + 0.5
@@ -85,9 +98,9 @@ def test_batched_ln_gelu_linear(dev, c_oracle, M, K, N):
     y = torch.empty(M, N, device=dev)
     xd, qd, sd, bd = x.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
     lwd, lbd = lw.to(dev), lb.to(dev)
-    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
-                                     bd.data_ptr(), N, y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5,
-                                     _lib.ACT_GELU_TANH, None, 0, _st())
+    args = (xd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0, bd.data_ptr(), N,
+            y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5, _lib.ACT_GELU_TANH, None, 0, _st())
+    rc = _fused_ws(*args) if use_ws else _lib.lib().tiq_linear_fused(*args)
     _lib.check(rc, "fused batched")
     torch.cuda.synchronize()
     w_hat = OL.dequantize(q, s)
@@ -98,30 +111,43 @@ def test_batched_ln_gelu_linear(dev, c_oracle, M, K, N):
     _f64_check(y, ref, _gelu(xn64 @ w_hat.double().T + b.double()))
 
 
+@pytest.mark.parametrize("use_ws", [False, True])
 @pytest.mark.parametrize("M", [8, 32])
 @pytest.mark.parametrize("K,N", [(6400, 1600), (3072, 768)])
-def test_batched_residual_in_place(dev, c_oracle, M, K, N):
+def test_batched_residual_in_place(dev, c_oracle, M, K, N, use_ws):
+    """Long K: with a workspace the K range is split over workgroups (the last
+    to finish sums the slices). Two calls in a row on one workspace, the
+    second with fewer rows, check that the tile counters start at zero."""
+    L = _lib.lib()
     gen = torch.Generator().manual_seed(M + K)
     w = torch.randn(N, K, generator=gen) * 0.02
-    h = torch.randn(M, K, generator=gen)
-    x0 = torch.randn(M, N, generator=gen)
     b = 0.1 * torch.randn(N, generator=gen)
     q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
-    x = x0.to(dev).clone()
-    hd, qd, sd, bd = h.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
-    rc = _lib.lib().tiq_linear_fused(hd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None,
-                                     0, bd.data_ptr(), N, x.data_ptr(), 0, N, None, None, 1e-5, 0, x.data_ptr(), N,
-                                     _st())
-    _lib.check(rc, "fused batched residual")
-    torch.cuda.synchronize()
+    qd, sd, bd = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
     w_hat = OL.dequantize(q, s)
-    ref = x0 + OL.linear_ref(h, w_hat, b)
-    assert (x.cpu() - ref).abs().max() <= 1e-3 * ref.abs().max()
-    _f64_check(x, ref, x0.double() + h.double() @ w_hat.double().T + b.double())
+    n_ws = int(L.tiq_linear_fused_workspace(0, _lib.WF_INT8, M, K, N))
+    ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=dev)
+    for rows in (M, M - 3):
+        h = torch.randn(rows, K, generator=gen)
+        x0 = torch.randn(rows, N, generator=gen)
+        x = x0.to(dev).clone()
+        hd = h.to(dev)
+        args = (hd.data_ptr(), 0, rows, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0, bd.data_ptr(), N,
+                x.data_ptr(), 0, N, None, None, 1e-5, 0, x.data_ptr(), N)
+        if use_ws:
+            rc = L.tiq_linear_fused_ws(*args, ws.data_ptr(), n_ws, _st())
+        else:
+            rc = L.tiq_linear_fused(*args, _st())
+        _lib.check(rc, "fused batched residual")
+        torch.cuda.synchronize()
+        ref = x0 + OL.linear_ref(h, w_hat, b)
+        assert (x.cpu() - ref).abs().max() <= 1e-3 * ref.abs().max()
+        _f64_check(x, ref, x0.double() + h.double() @ w_hat.double().T + b.double())
 
 
+@pytest.mark.parametrize("use_ws", [False, True])
 @pytest.mark.parametrize("M", [6, 32])
-def test_batched_fp32_head(dev, M):
+def test_batched_fp32_head(dev, M, use_ws):
     """fp32 weights (the tied lm_head) with LayerNorm, N not a multiple of 32."""
     K, N = 768, 5003
     gen = torch.Generator().manual_seed(M)
@@ -131,8 +157,9 @@ def test_batched_fp32_head(dev, M):
     lb = 0.1 * torch.randn(K, generator=gen)
     y = torch.empty(M, N, device=dev)
     xd, wd, lwd, lbd = x.to(dev), w.to(dev), lw.to(dev), lb.to(dev)
-    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, wd.data_ptr(), _lib.WF_F32, None, None, 0, None, N,
-                                     y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5, 0, None, 0, _st())
+    args = (xd.data_ptr(), 0, M, K, K, wd.data_ptr(), _lib.WF_F32, None, None, 0, None, N, y.data_ptr(), 0, N,
+            lwd.data_ptr(), lbd.data_ptr(), 1e-5, 0, None, 0, _st())
+    rc = _fused_ws(*args) if use_ws else _lib.lib().tiq_linear_fused(*args)
     _lib.check(rc, "fused batched fp32 head")
     torch.cuda.synchronize()
     ref = F.layer_norm(x, (K,), lw, lb, 1e-5) @ w.T
