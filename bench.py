@@ -275,6 +275,75 @@ def decode_section(dev, repeats=3):
     return res
 
 
+def decode_xl_section(dev, new_tokens=128):
+    """GPT-2-XL (48 layers, d 1600, 25 heads) seed 0, int8 per-channel, batch
+    32, 128-token random prompts, greedy +new_tokens: end-to-end tokens/s
+    (prefill + decode) and the per-Linear decode GB/s at M = 32."""
+    import torch
+
+    import gpt2_harness_amd as g
+    from gpt2_harness_amd import _lib
+
+    torch.manual_seed(0)
+    cfg = g.gpt2_config("gpt2-xl")
+    model = g.GPT(cfg).to(dev).eval()
+    qm, _ = g.quantize_model(model, 8)
+    del model
+    torch.manual_seed(0)
+    B, T0 = 32, 128
+    prompt = torch.randint(0, cfg.vocab_size, (B, T0)).to(dev)
+    dec = g.FusedDecoder(qm, B, T0 + new_tokens)
+    dec.start(prompt)
+    dec.capture()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.start(prompt)
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(new_tokens - 1):
+        dec.graph.replay()
+    torch.cuda.synchronize()
+    t_dec = time.perf_counter() - t0
+    res = {"model": "gpt2-xl (1.56B) seed 0, int8 per-channel", "batch": B, "prompt": T0, "new_tokens": new_tokens,
+           "prefill_ms": t_pre * 1e3, "decode_ms_per_step": t_dec * 1e3 / (new_tokens - 1),
+           "tokens_per_s": B * new_tokens / (t_pre + t_dec),
+           "decode_tokens_per_s": B * (new_tokens - 1) / t_dec}
+    # per-Linear decode GB/s of layer 0 at M = 32 (HIP events, 20 calls each)
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    blk = qm.h[0]
+    x = torch.randn(B, 4 * cfg.n_embd, device=dev)
+    per = {}
+    for name, lin in (("c_attn", blk.attn.c_attn), ("attn.c_proj", blk.attn.c_proj), ("c_fc", blk.mlp.c_fc),
+                      ("mlp.c_proj", blk.mlp.c_proj)):
+        K, N = lin.in_features, lin.out_features
+        y = torch.empty(B, N, device=dev)
+
+        def call():
+            rc = L.tiq_linear_fused_ws(x.data_ptr(), _lib.F32, B, K, x.stride(0), lin.codes.data_ptr(), _lib.WF_INT8,
+                                       lin.scale.data_ptr(), None, 0, _lib.ptr(lin.bias), N, y.data_ptr(), _lib.F32,
+                                       N, None, None, 1e-5, 0, None, 0, dec.lin_ws.data_ptr(), dec.lin_ws_bytes, st)
+            if rc:
+                raise RuntimeError(f"tiq_linear_fused_ws status {rc}")
+
+        call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(20):
+            call()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / 20
+        nbytes = N * K + 4 * N + 4 * B * K + 4 * B * N
+        per[f"{K}x{N}"] = {"us": us, "GB/s": nbytes / (us * 1e-6) / 1e9}
+    res["decode_linear_M32"] = per
+    del dec, qm
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(budget_s: float = 10.0):
     """The oracle's dequantize-then-fp32-matmul over the GEMV workload on the host."""
     import torch
@@ -319,7 +388,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode", "decode_xl", "copy"], default=None,
                     help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
                          "used to calibrate the HBM byte counters")
     args = ap.parse_args()
@@ -352,6 +421,9 @@ def main() -> int:
     if args.only == "decode":
         print(json.dumps(decode_section(dev)))
         return 0
+    if args.only == "decode_xl":
+        print(json.dumps(decode_xl_section(dev)))
+        return 0
 
     head = gemv_section(1, SMALL_KN, 12, 6, args.steps, args.warmup, dev, seed=0)
     print(f"# headline gemv M=1: {head['GB/s']:.1f} GB/s, {head['ms_per_step']:.4f} ms/step", file=sys.stderr,
@@ -370,6 +442,8 @@ def main() -> int:
         detail["quantize_xl"] = quantize_section(dev)
         detail["decode_gpt2_small_int8"] = decode_section(dev)
         print("# decode done", file=sys.stderr, flush=True)
+        detail["decode_gpt2_xl_int8_b32"] = decode_xl_section(dev)
+        print("# xl decode done", file=sys.stderr, flush=True)
         cpu = cpu_baseline()
 
     traffic = None
