@@ -3,15 +3,27 @@
 //     y[m, n] = scale[n] * sum_k q[n, k] * x[m, k] + bias[n]
 //
 // The op is bound by the weight stream: N*K bytes of int8 (N*K/2 of int4)
-// per call against 2-4*M*K bytes of activations. Design:
+// per call against 2-4*M*K bytes of activations; at decode sizes (0.6-10 MB)
+// one launch is about one trip to HBM plus the launch itself. Two kernels:
+//
+// gemv_direct_kernel (up to 4 rows, no LayerNorm; the default): one
+// wavefront per weight row, every load of the workgroup issued before any is
+// used -- the row's 16-byte chunks (nontemporal), the activations they
+// multiply (straight into registers) and the epilogue operands -- then one
+// FMA pass, a wavefront reduction and the store. Rows are dealt to the eight
+// XCDs in contiguous blocks.
+//
+// gemv_kernel (LayerNorm prologue, group-wise int4, rows longer than the
+// direct kernel's registers):
 //   * a workgroup stages its MT activation rows in LDS once, as fp32 and in
 //     "planes" (float4 p of every 16-byte weight chunk stored contiguously
 //     over chunks), so lane l's reads of chunk l are consecutive 16-byte LDS
 //     words: no bank conflicts;
 //   * each wavefront owns R weight rows; lane l streams 16-byte chunks
-//     l, l+64, ... of each row (global_load_dwordx4, fully coalesced: a
-//     wavefront instruction covers 1 KB of one row), four chunks per row in
-//     flight, the first ones issued before the activations are staged;
+//     l, l+64, ... of each row (nontemporal global_load_dwordx4, fully
+//     coalesced: a wavefront instruction covers 1 KB of one row), four chunks
+//     per row in flight, the first ones issued before the activations are
+//     staged;
 //   * the chunk is dequantized in registers (sign-extended bytes or biased
 //     nibbles -> fp32, one v_cvt_f32_i32_sdwa per int8 code) once and reused
 //     for all MT activation rows;
@@ -124,6 +136,15 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Bijective map of a workgroup index so that XCD b % 8 (where the hardware
+// places workgroup b) owns a contiguous range of the G workgroups.
+__device__ __forceinline__ int xcd_block(int b, int G) {
+    const int q = G >> 3, r = G & 7, xcd = b & 7, idx = b >> 3;
+    return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + idx;
+}
+
 // Sum of v over the workgroup, for MT rows at once. red holds MT * 8 floats.
 template <int MT>
 __device__ __forceinline__ void block_sum(float (&v)[MT], float* red) {
@@ -158,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     const int NC = K / KC;
     const int m0 = blockIdx.y * MT;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n0 = (blockIdx.x * kWavesPerBlock + wave) * R;
+    const int n0 = (xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + wave) * R;
     const bool active = n0 < N;  // wave-uniform
 
     const uint8_t* wrow[R];
@@ -173,12 +194,33 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
             const int c = c0 + 64 * u;
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                wv[u][r] = (c < NC) ? *reinterpret_cast<const uint4*>(wrow[r] + 16 * (int64_t)c) : make_uint4(0, 0, 0, 0);
+            {
+                // nontemporal: the weights are read once
+                const u32x4 t = (c < NC) ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + 16 * (int64_t)c))
+                                         : u32x4{0u, 0u, 0u, 0u};
+                wv[u][r] = make_uint4(t.x, t.y, t.z, t.w);
+            }
         }
     };
     // The first weight block goes out before the activations are staged, so
     // its HBM latency overlaps the staging and the barrier.
     if (active) load_block(lane);
+
+    // The epilogue operands of the output this lane stores (lane r * MT + m
+    // stores row n0 + r of activation row m0 + m) are loaded now as well:
+    // loaded after the reduction they would cost a second, serial trip to
+    // HBM. A residual that aliases y is read here by the lane that later
+    // writes the same element, so the early read is safe.
+    float ep_scale = 1.f, ep_bias = 0.f, ep_res = 0.f;
+    {
+        const int r = lane / MT, m = lane - (lane / MT) * MT;
+        const int n = n0 + r;
+        if (active && r < R && n < N && m0 + m < M) {
+            if (FMT == kW8 || FMT == kW4) ep_scale = scale[n];
+            if (bias) ep_bias = bias[n];
+            if (fz.res) ep_res = fz.res[(int64_t)(m0 + m) * fz.ldr + n];
+        }
+    }
 
     // stage MT activation rows as fp32 planes: xs[m][p][c]
     float rsum[MT];
@@ -296,12 +338,128 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
         for (int m = 0; m < MT; ++m) {
             if (lane == r * MT + m && n < N && m0 + m < M) {
                 float v = acc[r][m];
-                if (FMT == kW8 || FMT == kW4) v *= scale[n];
-                if (bias) v += bias[n];
+                if (FMT == kW8 || FMT == kW4) v *= ep_scale;
+                if (bias) v += ep_bias;
                 if (fz.act == 1) v = gelu_tanh(v);
-                if (fz.res) v += fz.res[(int64_t)(m0 + m) * fz.ldr + n];
+                if (fz.res) v += ep_res;
                 store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
             }
+        }
+    }
+}
+
+// Direct decode GEMV (no LayerNorm prologue, int8 / int4 / fp32 weights).
+// At decode sizes (0.6-10 MB per matrix) a launch costs about one trip to
+// HBM plus the launch itself, so this kernel is built to make that trip once:
+//   * one wavefront per workgroup, one weight row per wavefront; lane l holds
+//     16-byte chunks l, l + 64, ... of the row (UM of them at most);
+//   * every load is issued before any is used: the row's chunks
+//     (nontemporal: the stream is read once and must not evict what is
+//     reused), the activations those chunks multiply (16-32 bytes per chunk
+//     and row, straight into registers, no LDS staging and no barrier), and
+//     the lane's epilogue operands (scale, bias, residual);
+//   * rows are handed to the eight XCDs in contiguous blocks (the hardware
+//     deals workgroups round-robin over XCDs), so a 128-byte line of scales or
+//     biases is fetched into one XCD's L2 rather than into all eight;
+//   * the lane partial sums are reduced across the wavefront; lane m stores
+//     output (m0 + m, n).
+template <typename TX>
+__device__ __forceinline__ float4 x4_of(const u32x4& u, int half);
+
+template <>
+__device__ __forceinline__ float4 x4_of<uint16_t>(const u32x4& u, int half) {
+    const uint32_t a = half ? u.z : u.x, b = half ? u.w : u.y;
+    return make_float4(__uint_as_float(a << 16), __uint_as_float(a & 0xffff0000u), __uint_as_float(b << 16),
+                       __uint_as_float(b & 0xffff0000u));
+}
+
+template <>
+__device__ __forceinline__ float4 x4_of<float>(const u32x4& u, int) {
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
+
+template <int MT, int UM, int FMT, typename TX, typename TY>
+__global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ x, int64_t ldx, int M,
+                                                         const uint8_t* __restrict__ w, int64_t ldw,
+                                                         const float* __restrict__ scale,
+                                                         const float* __restrict__ bias, TY* y, int64_t ldy, int N,
+                                                         int K, Fusion fz) {
+    constexpr int KC = Fmt<FMT>::KC;
+    constexpr int P = KC / 4;                          // float4 of activations per chunk
+    constexpr int XB = KC * (int)sizeof(TX);           // activation bytes per chunk and row
+    constexpr int XQ = XB >= 16 ? XB / 16 : 1;         // 16-byte registers holding them
+    const int lane = threadIdx.x;
+    const int n = xcd_block(blockIdx.x, gridDim.x);
+    const int m0 = blockIdx.y * MT;
+    const int NC = K / KC;
+    const uint8_t* wr = w + (int64_t)n * ldw;
+
+    u32x4 wv[UM];
+#pragma unroll
+    for (int u = 0; u < UM; ++u) {
+        const int c = lane + 64 * u;
+        wv[u] = c < NC ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * (int64_t)c))
+                       : u32x4{0u, 0u, 0u, 0u};
+    }
+    // activations of the same K range: rows past M repeat row M - 1 (their
+    // outputs are not stored)
+    u32x4 xv[UM][MT][XQ];
+#pragma unroll
+    for (int u = 0; u < UM; ++u) {
+        const int c = lane + 64 * u;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const TX* xr = x + (int64_t)min(m0 + m, M - 1) * ldx + (int64_t)KC * c;
+#pragma unroll
+            for (int q = 0; q < XQ; ++q) {
+                if (c >= NC) {
+                    xv[u][m][q] = u32x4{0u, 0u, 0u, 0u};
+                } else if constexpr (XB >= 16) {
+                    xv[u][m][q] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(xr) + 16 * q);
+                } else {  // fp32 weights with bf16 activations: 8 bytes
+                    const uint2 h = *reinterpret_cast<const uint2*>(xr);
+                    xv[u][m][q] = u32x4{h.x, h.y, 0u, 0u};
+                }
+            }
+        }
+    }
+    float ep_scale = 1.f, ep_bias = 0.f, ep_res = 0.f;
+    if (lane < MT && m0 + lane < M) {
+        if (FMT == kW8 || FMT == kW4) ep_scale = scale[n];
+        if (bias) ep_bias = bias[n];
+        // a residual aliasing y is read by the lane that writes the element
+        if (fz.res) ep_res = fz.res[(int64_t)(m0 + lane) * fz.ldr + n];
+    }
+
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < UM; ++u) {
+        if (lane + 64 * u < NC) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float4 xf[P];
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    if constexpr (sizeof(TX) == 2) xf[p] = x4_of<TX>(xv[u][m][p / 2], p % 2);
+                    else xf[p] = x4_of<TX>(xv[u][m][p], 0);
+                }
+                acc[m] += dot_chunk<FMT>(make_uint4(wv[u].x, wv[u].y, wv[u].z, wv[u].w), xf);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = wave_sum(acc[m]);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (lane == m && m0 + m < M) {
+            float v = acc[m];
+            if (FMT == kW8 || FMT == kW4) v *= ep_scale;
+            v += ep_bias;
+            if (fz.act == 1) v = gelu_tanh(v);
+            if (fz.res) v += ep_res;
+            store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
         }
     }
 }
@@ -359,6 +517,54 @@ int run_gemv(const LinearArgs& a) {
     return launch_status();
 }
 
+// Activation registers of the direct kernel: UM chunks x MT rows x XQ x 4
+// VGPRs, kept within 128 so that weights, activations and sums all fit.
+template <int MT, int UM, int FMT, typename TX>
+constexpr bool direct_fits() {
+    constexpr int XB = Fmt<FMT>::KC * (int)sizeof(TX);
+    return UM * MT * (XB >= 16 ? XB / 16 : 1) * 4 <= 128;
+}
+
+template <int MT, int UM, int FMT, typename TX, typename TY>
+bool run_direct(const LinearArgs& a, int& rc) {
+    if constexpr (direct_fits<MT, UM, FMT, TX>()) {
+        const dim3 grid((unsigned)a.N, (unsigned)((a.M + MT - 1) / MT));
+        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, FMT, TX, TY>), grid, dim3(64), 0, a.stream,
+                           static_cast<const TX*>(a.x), a.ldx, (int)a.M, a.w, a.ldw, a.scale, a.bias,
+                           static_cast<TY*>(a.y), a.ldy, (int)a.N, (int)a.K, a.fuse);
+        rc = launch_status();
+        return true;
+    }
+    return false;
+}
+
+template <int UM, int FMT, typename TX, typename TY>
+bool run_direct_mt(const LinearArgs& a, int& rc) {
+    if (a.M == 1) return run_direct<1, UM, FMT, TX, TY>(a, rc);
+    if (a.M == 2) return run_direct<2, UM, FMT, TX, TY>(a, rc);
+    return run_direct<4, UM, FMT, TX, TY>(a, rc);
+}
+
+// The direct kernel, when it takes the arguments (no LayerNorm, int8 / int4 /
+// fp32 weights, a row of at most 8 chunks per lane, 16-byte activation rows).
+template <int FMT, typename TX, typename TY>
+bool try_direct(const LinearArgs& a, int& rc) {
+    if constexpr (FMT == kW4G) {
+        return false;
+    } else {
+        constexpr int KC = Fmt<FMT>::KC;
+        constexpr size_t XB = KC * sizeof(TX);
+        if (a.fuse.ln_w) return false;
+        const size_t xa = XB >= 16 ? 16 : XB;
+        if (!aligned(a.x, xa) || ((size_t)a.ldx * sizeof(TX)) % xa != 0) return false;
+        const int64_t um = (a.K / KC + 63) / 64;
+        if (um <= 2) return run_direct_mt<2, FMT, TX, TY>(a, rc);
+        if (um <= 4) return run_direct_mt<4, FMT, TX, TY>(a, rc);
+        if (um <= 8) return run_direct_mt<8, FMT, TX, TY>(a, rc);
+        return false;
+    }
+}
+
 template <int FMT, typename TX, typename TY>
 int run_generic(const LinearArgs& a) {
     const int64_t outs = a.M * a.N;
@@ -381,6 +587,8 @@ int dispatch_fmt(const LinearArgs& a) {
         if (fused) return TIQ_EUNSUPPORTED;
         return run_generic<FMT, TX, TY>(a);
     }
+    int rc = TIQ_OK;
+    if (a.M <= 4 && try_direct<FMT, TX, TY>(a, rc)) return rc;
     const size_t row_lds = (size_t)a.K * sizeof(float);
     int mt = 4;
     while (mt > 1 && (size_t)mt * row_lds > kMaxLds) mt >>= 1;

@@ -157,16 +157,25 @@ __global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__
 }
 
 // WF: kW8 (int8 codes, per-row scale) or kF32 (fp32 weights, no scale).
-// PL: activations arrive as the three bf16 planes of ln_split_kernel (x is
-// then a uint16_t pointer with row stride 3 K and LayerNorm already applied)
-// instead of fp32 rows split here.
-template <int WF, bool PL, typename TY>
+// XM: how the activations arrive.
+//   kXRows   fp32 rows, LayerNorm'd (optionally) and split here;
+//   kXPlanes the three bf16 planes of ln_split_kernel (x is then a uint16_t
+//            pointer to the operand-ordered blocks, LayerNorm already applied);
+//   kXBf16   bf16 rows (int8 weights only, no LayerNorm): one plane, each
+//            int8 x bf16 product exact, one MFMA per 16 K.
+enum XMode : int { kXRows = 0, kXPlanes = 1, kXBf16 = 2 };
+// bf16 rows: units a wavefront holds, every one in flight at once
+// (K <= 8 * 12 * 32 = 3072)
+constexpr int kXbUnits = 12;
+
+template <int WF, int XM, typename TY>
 __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int K, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, int N, TY* __restrict__ y, int64_t ldy,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps, int act,
     const float* __restrict__ res, int64_t ldr) {
     constexpr int WB = (WF == kW8) ? 16 : 64;  // weight bytes a lane loads per unit
+    constexpr bool PL = XM == kXPlanes;
     constexpr int kXp = ring_units<WF>();
     __shared__ float red[kWaves][32][33];      // partial output tiles, rows padded
     __shared__ float stat[kWaves][32];
@@ -180,12 +189,13 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const int u0 = wave * U / kWaves, u1 = (wave + 1) * U / kWaves;
     const bool xrow_ok = m0 + r < M;
     const float* xr = x + (int64_t)(xrow_ok ? m0 + r : 0) * ldx + 16 * h;  // + 32 u
+    const uint16_t* xbr = reinterpret_cast<const uint16_t*>(x) + (int64_t)(xrow_ok ? m0 + r : 0) * ldx + 16 * h;
     // plane input: this row tile's operand blocks, lane-contiguous
     const uint16_t* x3t = reinterpret_cast<const uint16_t*>(x) + (int64_t)blockIdx.y * (K / 32) * 6 * 64 * 8 + lane * 8;
     const uint8_t* wr = w + (int64_t)min(n0 + r, N - 1) * ldw + WB * h;    // + 2 WB u
 
     const int cnt = u1 - u0;  // <= kUnits (the host checks K)
-    constexpr int kUnits = max_units<WF>();
+    constexpr int kUnits = XM == kXBf16 ? kXbUnits : max_units<WF>();
     // every weight slice of the wavefront is requested first, so the whole
     // matrix is in flight at once (behind the LayerNorm statistics);
     // activations (L2 hits) follow through a ring of kXp unit registers
@@ -196,11 +206,27 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
 #pragma unroll
             for (int q = 0; q < WB / 16; ++q)
                 wreg[c][q] = *reinterpret_cast<const u32x4*>(wr + 2 * WB * (u0 + c) + 16 * q);
+    // Epilogue operands of this thread's two outputs (column n0 + t % 32,
+    // rows m0 + t / 32 and 16 below it), requested with the weights rather
+    // than after the reduction, where they would cost another serial trip to
+    // HBM. A residual aliasing y is read by the thread that writes the same
+    // element.
+    const int ep_n = n0 + (threadIdx.x & 31), ep_m = m0 + (threadIdx.x >> 5);
+    float ep_scale = 1.f, ep_bias = 0.f, ep_res[2] = {0.f, 0.f};
+    if (ep_n < N) {
+        if (WF == kW8) ep_scale = scale[ep_n];
+        if (bias) ep_bias = bias[ep_n];
+        if (res) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                if (ep_m + 16 * t < M) ep_res[t] = res[(int64_t)(ep_m + 16 * t) * ldr + ep_n];
+        }
+    }
     // LayerNorm statistics of the 32 activation rows (two-pass); its weight
     // and bias go to LDS (read there, they add no global loads to the unit
     // loop, whose in-order waits would otherwise include the prefetches)
     float mu = 0.f, rs = 1.f;
-    if (!PL && ln_w) {
+    if (XM == kXRows && ln_w) {
         for (int i = threadIdx.x; i < K / 4; i += kWaves * 64) {
             reinterpret_cast<float4*>(gb_s[0])[i] = reinterpret_cast<const float4*>(ln_w)[i];
             reinterpret_cast<float4*>(gb_s[1])[i] = reinterpret_cast<const float4*>(ln_b)[i];
@@ -353,7 +379,35 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
         }
     };
 
-    if (PL && WF == kW8 && cnt <= kPlUnits) {
+    // bf16 rows: the 16 K of a lane are two operand registers
+    auto xload_bf = [&](int u, u32x4 (&xv)[2]) {
+        xv[0] = *reinterpret_cast<const u32x4*>(xbr + 32 * u);
+        xv[1] = *reinterpret_cast<const u32x4*>(xbr + 32 * u + 8);
+    };
+    auto unit_bf = [&](const u32x4 (&xv)[2], const u32x4 (&wv)[WB / 16]) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const u32x4 t = xrow_ok ? xv[e] : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 d = wv[0];
+            const uint32_t s0 = e == 0 ? d.x : d.z, s1 = e == 0 ? d.y : d.w;
+            const u32x4 wq = {bf16x2_of_bytes(s0, 0), bf16x2_of_bytes(s0, 16), bf16x2_of_bytes(s1, 0),
+                              bf16x2_of_bytes(s1, 16)};
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wq),
+                                                          __builtin_bit_cast(bf16x8, t), acc, 0, 0, 0);
+        }
+    };
+
+    if constexpr (XM == kXBf16) {
+        static_assert(WF == kW8, "bf16 rows are taken with int8 weights");
+        // every activation unit in flight (the host checks cnt <= kXbUnits)
+        u32x4 ball[kXbUnits][2];
+#pragma unroll
+        for (int c = 0; c < kXbUnits; ++c)
+            if (c < cnt) xload_bf(u0 + c, ball[c]);
+#pragma unroll
+        for (int c = 0; c < kXbUnits; ++c)
+            if (c < cnt) unit_bf(ball[c], wreg[c]);
+    } else if (PL && WF == kW8 && cnt <= kPlUnits) {
         // every activation unit in flight too
         u32x4 pall[kPlUnits][3][2];
 #pragma unroll
@@ -411,10 +465,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
         const int gm = m0 + m, gn = n0 + nn;
         float v = vsum[t];
         if (gm < M && gn < N) {
-            if (WF == kW8) v *= scale[gn];
-            if (bias) v += bias[gn];
+            if (WF == kW8) v *= ep_scale;
+            if (bias) v += ep_bias;
             if (act == 1) v = gelu_tanh_f(v);
-            if (res) v += res[(int64_t)gm * ldr + gn];
+            if (res) v += ep_res[t];
             store_out<TY>(y + (int64_t)gm * ldy + gn, v);
         }
     }
@@ -428,7 +482,7 @@ size_t planes_bytes(int64_t M, int64_t K) { return round256((size_t)((M + 31) / 
 template <int WF, typename TY>
 int run_skinny(const LinearArgs& a) {
     const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 31) / 32));
-    if (a.ws && a.ws_bytes >= planes_bytes(a.M, a.K)) {
+    if (a.x_dtype == TIQ_F32 && a.ws && a.ws_bytes >= planes_bytes(a.M, a.K)) {
         // LayerNorm + split once, then the products on the planes
         uint16_t* x3 = static_cast<uint16_t*>(a.ws);
         if (a.fuse.ln_w)
@@ -440,13 +494,22 @@ int run_skinny(const LinearArgs& a) {
                                static_cast<const float*>(a.x), a.ldx, (int)a.K, nullptr, nullptr, 0.f, x3);
         int rc = launch_status();
         if (rc != TIQ_OK) return rc;
-        hipLaunchKernelGGL((skinny_kernel<WF, true, TY>), grid, dim3(kWaves * 64), 0, a.stream,
+        hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                            reinterpret_cast<const float*>(x3), (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
                            a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
                            a.fuse.res, a.fuse.ldr);
         return launch_status();
     }
-    hipLaunchKernelGGL((skinny_kernel<WF, false, TY>), grid, dim3(kWaves * 64), 0, a.stream,
+    if constexpr (WF == kW8) {
+        if (a.x_dtype == TIQ_BF16) {
+            hipLaunchKernelGGL((skinny_kernel<kW8, kXBf16, TY>), grid, dim3(kWaves * 64), 0, a.stream,
+                               static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
+                               a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
+                               a.fuse.res, a.fuse.ldr);
+            return launch_status();
+        }
+    }
+    hipLaunchKernelGGL((skinny_kernel<WF, kXRows, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                        static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias,
                        (int)a.N, static_cast<TY*>(a.y), a.ldy, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, a.fuse.act,
                        a.fuse.res, a.fuse.ldr);
@@ -458,10 +521,14 @@ int run_skinny(const LinearArgs& a) {
 size_t skinny_workspace(int64_t M, int64_t K) { return planes_bytes(M, K); }
 
 bool skinny_supported(const LinearArgs& a) {
-    if (a.x_dtype != TIQ_F32 || (a.fmt != kW8 && a.fmt != kF32)) return false;
+    if (a.fmt != kW8 && a.fmt != kF32) return false;
+    // bf16 rows: int8 weights, no LayerNorm, 16-byte rows
+    const bool xbf = a.x_dtype == TIQ_BF16;
+    if (xbf && (a.fmt != kW8 || a.fuse.ln_w || a.ldx % 8 != 0)) return false;
+    if (!xbf && a.x_dtype != TIQ_F32) return false;
     if (a.M < kSkinnyMinRows || a.M > 64 || a.K % 32 != 0 || a.N > 0x7fffffff) return false;
     const int64_t units = (a.K / 32 + kWaves - 1) / kWaves;
-    if (units > (a.fmt == kW8 ? max_units<kW8>() : max_units<kF32>())) return false;
+    if (units > (xbf ? kXbUnits : a.fmt == kW8 ? max_units<kW8>() : max_units<kF32>())) return false;
     if (!aligned(a.x, 16) || a.ldx % 4 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
     if (a.fuse.ln_w && (a.K > kLnMaxK || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16))) return false;
     // the residual may alias y only element for element

@@ -115,9 +115,9 @@ def test_batched_ln_gelu_linear(dev, c_oracle, M, K, N, use_ws):
 @pytest.mark.parametrize("M", [8, 32])
 @pytest.mark.parametrize("K,N", [(6400, 1600), (3072, 768)])
 def test_batched_residual_in_place(dev, c_oracle, M, K, N, use_ws):
-    """Long K: with a workspace the K range is split over workgroups (the last
-    to finish sums the slices). Two calls in a row on one workspace, the
-    second with fewer rows, check that the tile counters start at zero."""
+    """Long K (activations streamed through a register ring), residual
+    added in place. Two calls in a row on one workspace, the second with
+    fewer rows: nothing of the first call's planes reaches the second."""
     L = _lib.lib()
     gen = torch.Generator().manual_seed(M + K)
     w = torch.randn(N, K, generator=gen) * 0.02
@@ -143,6 +143,38 @@ def test_batched_residual_in_place(dev, c_oracle, M, K, N, use_ws):
         ref = x0 + OL.linear_ref(h, w_hat, b)
         assert (x.cpu() - ref).abs().max() <= 1e-3 * ref.abs().max()
         _f64_check(x, ref, x0.double() + h.double() @ w_hat.double().T + b.double())
+
+
+@pytest.mark.parametrize("M", [5, 16, 64])
+@pytest.mark.parametrize("K,N,act", [(768, 3072, 1), (3072, 768, 0)])
+def test_batched_bf16_rows_gelu_residual(dev, c_oracle, M, K, N, act):
+    """bf16 activation rows on the matrix-core kernel with the GELU epilogue
+    or the residual added in place."""
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(M * 5 + K)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    b = 0.1 * torch.randn(N, generator=gen)
+    r0 = torch.randn(M, N, generator=gen)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    xd, qd, sd, bd = x.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
+    y = r0.to(dev).clone()
+    res = y.data_ptr() if act == 0 else None
+    rc = L.tiq_linear_fused(xd.data_ptr(), 1, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
+                            bd.data_ptr(), N, y.data_ptr(), 0, N, None, None, 1e-5, act, res, N if res else 0,
+                            _st())
+    _lib.check(rc, "fused bf16 rows")
+    torch.cuda.synchronize()
+    w_hat = OL.dequantize(q, s)
+    lin32 = OL.linear_ref(x, w_hat, b)
+    lin64 = x.double() @ w_hat.double().T + b.double()
+    if act == 1:
+        ref32, ref64 = _gelu(lin32), _gelu(lin64)
+    else:
+        ref32, ref64 = r0 + lin32, r0.double() + lin64
+    ok, err, bound = OL.within_tolerance(y, ref32)
+    assert ok, (err, bound)
+    _f64_check(y, ref32, ref64)
 
 
 @pytest.mark.parametrize("use_ws", [False, True])
@@ -183,6 +215,43 @@ def test_fused_residual_in_place_and_int4(dev, c_oracle, M):
     _lib.check(rc, "fused residual")
     ref = x0 + OL.linear_ref(h, OL.dequantize(q, s))
     assert (x.cpu() - ref).abs().max() <= 1e-3 * ref.abs().max()
+
+
+# Up to 4 rows without LayerNorm take the direct GEMV (one wavefront per
+# weight row, every load issued up front); rows too long for its registers
+# (6400 int8 columns at 4 rows) take the LDS-staged kernel. Each weight
+# format, both activation dtypes, the GELU epilogue and the in-place residual.
+@pytest.mark.parametrize("fmt", ["int8", "int4", "f32"])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("K,N", [(1600, 1000), (6400, 700)])
+def test_direct_gemv_formats(dev, c_oracle, fmt, x_dtype, M, K, N):
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(M * 13 + K + len(fmt))
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen).to(x_dtype)
+    b = 0.1 * torch.randn(N, generator=gen)
+    r0 = torch.randn(M, N, generator=gen)
+    if fmt == "f32":
+        wd, sd, wf, w_hat = w.to(dev), None, _lib.WF_F32, w
+    else:
+        q, s = c_oracle.quantize_per_channel(w.numpy(), 8 if fmt == "int8" else 4)
+        wd = torch.from_numpy(q if fmt == "int8" else c_oracle.pack_int4(q)).to(dev)
+        sd = torch.from_numpy(s.reshape(-1)).to(dev)
+        wf, w_hat = (_lib.WF_INT8 if fmt == "int8" else _lib.WF_INT4), OL.dequantize(q, s)
+    act = 1 if K == 1600 else 0       # GELU epilogue, or the residual in place
+    y = r0.to(dev).clone()
+    xd, bd = x.to(dev), b.to(dev)
+    res = None if act else y.data_ptr()
+    rc = L.tiq_linear_fused(xd.data_ptr(), _lib.dtype_code(x_dtype), M, K, K, wd.data_ptr(), wf,
+                            None if sd is None else sd.data_ptr(), None, 0, bd.data_ptr(), N, y.data_ptr(), 0, N,
+                            None, None, 1e-5, act, res, 0 if act else N, _st())
+    _lib.check(rc, f"direct {fmt}")
+    torch.cuda.synchronize()
+    lin = OL.linear_ref(x, w_hat, b)
+    ref = _gelu(lin) if act else r0 + lin
+    ok, err, bound = OL.within_tolerance(y, ref)
+    assert ok, (err, bound)
 
 
 def test_fused_f32_head_with_ln(dev):

@@ -135,6 +135,46 @@ def test_linear_w8_fp32_matrix_cores(dev, c_oracle, K, N, M):
     assert err_gpu <= 8 * max(err_cpu, floor), f"error {err_gpu:.3g} vs fp32 oracle {err_cpu:.3g}"
 
 
+# bf16 activations at 5..64 rows take the matrix-core decode kernel (one bf16
+# plane: every int8 x bf16 product is exact, fp32 accumulation); K beyond its
+# register budget (6400) takes the GEMV. Besides the 1e-3 contract, the fp32
+# result is held to a small multiple of torch fp32's own error against a
+# float64 computation of the same product.
+@pytest.mark.parametrize("KN", SMALL + [(1600, 4800), (6400, 1600)])
+@pytest.mark.parametrize("M", [5, 16, 33, 64])
+def test_linear_w8_bf16_batched(dev, c_oracle, KN, M):
+    K, N = KN
+    _run_w8("tiq_linear_w8", dev, c_oracle, K, N, M, torch.bfloat16, seed=M + K, bias=M != 33)
+    w, x, b = _inputs(K, N, M, M + K, torch.bfloat16, bias=M != 33)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    y = torch.empty(M, N, device=dev)
+    bd = None if b is None else b.to(dev)
+    _call("tiq_linear_w8", x.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), bd, N, y)
+    w_hat = OL.dequantize(q, s)
+    ref32 = OL.linear_ref(x, w_hat, b)
+    ref64 = x.double() @ w_hat.double().T + (0 if b is None else b.double())
+    err = float((y.cpu().double() - ref64).abs().max())
+    err32 = float((ref32.double() - ref64).abs().max())
+    assert err <= 8 * max(err32, 2.0 ** -24 * float(ref64.abs().max())), (err, err32)
+
+
+@pytest.mark.parametrize("pad", [64, 4])
+def test_linear_w8_bf16_strided_rows(dev, c_oracle, pad):
+    """Row stride K + 64 (16-byte rows: matrix-core kernel) and K + 4 (8-byte
+    rows: the GEMV), strided output; nothing written outside the outputs."""
+    K, N, M = 768, 2304, 16
+    w, x, b = _inputs(K, N, M, pad, torch.bfloat16)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    xs = torch.zeros(M, K + pad, device=dev, dtype=torch.bfloat16)
+    xs[:, :K] = x.to(dev)
+    ys = torch.full((M, N + 32), 7.0, device=dev)
+    _call("tiq_linear_w8", xs[:, :K], torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev),
+          b.to(dev), N, ys[:, :N])
+    ok, err, bound = OL.within_tolerance(ys[:, :N], OL.linear_ref(x, OL.dequantize(q, s), b))
+    assert ok, (err, bound)
+    assert torch.all(ys[:, N:] == 7.0), "kernel wrote outside its output rows"
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 256])
 def test_linear_w8_dispatch(dev, c_oracle, M):
     _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.bfloat16, seed=M)
