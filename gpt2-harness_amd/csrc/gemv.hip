@@ -394,27 +394,29 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
     const int NC = K / KC;
     const uint8_t* wr = w + (int64_t)n * ldw;
 
+    // No load sits behind a branch: a lane past the end of the row re-reads
+    // the row's last chunk (its product is dropped below; the repeats
+    // coalesce into one request). Loads under a branch get merged with their
+    // alternative through register moves, which wait for every load issued
+    // before them and so serialize the trips to memory.
     u32x4 wv[UM];
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
-        const int c = lane + 64 * u;
-        wv[u] = c < NC ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * (int64_t)c))
-                       : u32x4{0u, 0u, 0u, 0u};
+        const int c = min(lane + 64 * u, NC - 1);
+        wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * (int64_t)c));
     }
     // activations of the same K range: rows past M repeat row M - 1 (their
     // outputs are not stored)
     u32x4 xv[UM][MT][XQ];
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
-        const int c = lane + 64 * u;
+        const int c = min(lane + 64 * u, NC - 1);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const TX* xr = x + (int64_t)min(m0 + m, M - 1) * ldx + (int64_t)KC * c;
 #pragma unroll
             for (int q = 0; q < XQ; ++q) {
-                if (c >= NC) {
-                    xv[u][m][q] = u32x4{0u, 0u, 0u, 0u};
-                } else if constexpr (XB >= 16) {
+                if constexpr (XB >= 16) {
                     xv[u][m][q] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(xr) + 16 * q);
                 } else {  // fp32 weights with bf16 activations: 8 bytes
                     const uint2 h = *reinterpret_cast<const uint2*>(xr);
@@ -423,30 +425,29 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
             }
         }
     }
-    float ep_scale = 1.f, ep_bias = 0.f, ep_res = 0.f;
-    if (lane < MT && m0 + lane < M) {
-        if (FMT == kW8 || FMT == kW4) ep_scale = scale[n];
-        if (bias) ep_bias = bias[n];
-        // a residual aliasing y is read by the lane that writes the element
-        if (fz.res) ep_res = fz.res[(int64_t)(m0 + lane) * fz.ldr + n];
-    }
+    // epilogue operands, read by every lane (lane m < MT keeps row m0 + m's);
+    // a residual aliasing y is read by the lane that writes the element
+    const float ep_scale = (FMT == kW8 || FMT == kW4) ? scale[n] : 1.f;
+    const float ep_bias = bias ? bias[n] : 0.f;
+    float ep_res = 0.f;
+    if (fz.res) ep_res = fz.res[(int64_t)min(m0 + min(lane, MT - 1), M - 1) * fz.ldr + n];
 
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.f;
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
-        if (lane + 64 * u < NC) {
+        const bool own = lane + 64 * u < NC;
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                float4 xf[P];
+        for (int m = 0; m < MT; ++m) {
+            float4 xf[P];
 #pragma unroll
-                for (int p = 0; p < P; ++p) {
-                    if constexpr (sizeof(TX) == 2) xf[p] = x4_of<TX>(xv[u][m][p / 2], p % 2);
-                    else xf[p] = x4_of<TX>(xv[u][m][p], 0);
-                }
-                acc[m] += dot_chunk<FMT>(make_uint4(wv[u].x, wv[u].y, wv[u].z, wv[u].w), xf);
+            for (int p = 0; p < P; ++p) {
+                if constexpr (sizeof(TX) == 2) xf[p] = x4_of<TX>(xv[u][m][p / 2], p % 2);
+                else xf[p] = x4_of<TX>(xv[u][m][p], 0);
             }
+            const float part = dot_chunk<FMT>(make_uint4(wv[u].x, wv[u].y, wv[u].z, wv[u].w), xf);
+            acc[m] += own ? part : 0.f;
         }
     }
 #pragma unroll
@@ -454,9 +455,7 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         if (lane == m && m0 + m < M) {
-            float v = acc[m];
-            if (FMT == kW8 || FMT == kW4) v *= ep_scale;
-            v += ep_bias;
+            float v = acc[m] * ep_scale + ep_bias;
             if (fz.act == 1) v = gelu_tanh(v);
             if (fz.res) v += ep_res;
             store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
@@ -558,6 +557,7 @@ bool try_direct(const LinearArgs& a, int& rc) {
         const size_t xa = XB >= 16 ? 16 : XB;
         if (!aligned(a.x, xa) || ((size_t)a.ldx * sizeof(TX)) % xa != 0) return false;
         const int64_t um = (a.K / KC + 63) / 64;
+        if (um <= 1) return run_direct_mt<1, FMT, TX, TY>(a, rc);
         if (um <= 2) return run_direct_mt<2, FMT, TX, TY>(a, rc);
         if (um <= 4) return run_direct_mt<4, FMT, TX, TY>(a, rc);
         if (um <= 8) return run_direct_mt<8, FMT, TX, TY>(a, rc);
