@@ -103,72 +103,90 @@ class LinearSet:
                 raise RuntimeError(f"{entry} failed with status {rc}")
 
 
-def timed_graph_steps(ls: LinearSet, steps: int, warmup: int, entry: str = "tiq_linear_w8"):
-    """Capture one HIP graph per weight copy; time `steps` replays (rotating)."""
+def capture_graphs(ls: LinearSet, entry: str = "tiq_linear_w8"):
+    """One HIP graph per weight copy. Copy 0 runs once eagerly first (module
+    load); every other launch of the section is a graph replay."""
     import torch
 
-    copies = len(ls.items)
-    graphs = []
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for c in range(copies):  # warm once eagerly (module load), then capture
-            ls.launch_copy(c, entry)
+        ls.launch_copy(0, entry)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    for c in range(copies):
+    graphs = []
+    for c in range(len(ls.items)):
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
             ls.launch_copy(c, entry)
         graphs.append(gr)
+    return graphs
+
+
+def replay_ms(graphs, steps: int, warmup: int) -> float:
+    """Mean ms per replay over `steps` replays (rotating over the graphs),
+    HIP events on the stream the graphs replay on."""
+    import torch
+
     for i in range(warmup):
-        graphs[i % copies].replay()
+        graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
-        graphs[i % copies].replay()
+        graphs[i % len(graphs)].replay()
     end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
-    return ms / steps
+    return start.elapsed_time(end) / steps
 
 
-def per_launch_times(ls: LinearSet, reps: int, entry: str = "tiq_linear_w8"):
-    """Event pair around every launch (eager), weights rotated: per-shape ms."""
+def per_shape_graph_times(ls: LinearSet, reps: int, entry: str = "tiq_linear_w8"):
+    """Per shape: a graph of that shape's launches over every layer and copy,
+    timed alone (HIP events) after a 512 MiB buffer write has evicted the
+    weights from the 256 MB Infinity Cache; returns ms per launch."""
     import torch
 
-    out: dict[tuple[int, int], list[float]] = {}
-    copies = len(ls.items)
-    for r in range(reps):
-        items = ls.items[r % copies]
-        evs = []
-        st = torch.cuda.current_stream().cuda_stream
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    out = {}
+    for K, N in dict.fromkeys((K, N) for K, N, *_ in ls.items[0]):
         fn = getattr(ls.lib, entry)
-        for K, N, q, s, x, y in items:
+        gr = torch.cuda.CUDAGraph()
+        launches = 0
+        with torch.cuda.graph(gr):
+            st = torch.cuda.current_stream().cuda_stream
+            for items in ls.items:
+                for k, n, q, s, x, y in items:
+                    if (k, n) != (K, N):
+                        continue
+                    rc = fn(x.data_ptr(), ls.xd, ls.M, k, k, q.data_ptr(), s.data_ptr(), None, n, y.data_ptr(),
+                            ls.yd, n, st)
+                    if rc:
+                        raise RuntimeError(f"{entry} failed with status {rc}")
+                    launches += 1
+        total = 0.0
+        for _ in range(reps):
+            flush.fill_(1)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            rc = fn(x.data_ptr(), ls.xd, ls.M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), ls.yd, N, st)
+            gr.replay()
             b.record()
-            if rc:
-                raise RuntimeError(f"{entry} failed with status {rc}")
-            evs.append((K, N, a, b))
-        torch.cuda.synchronize()
-        for K, N, a, b in evs:
-            out.setdefault((K, N), []).append(a.elapsed_time(b))
-    return {kn: statistics.median(v) for kn, v in out.items()}
+            torch.cuda.synchronize()
+            total += a.elapsed_time(b)
+        out[(K, N)] = total / reps / launches
+    del flush
+    return out
 
 
 def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed):
     ls = LinearSet(kn, layers, copies, M, dev, seed)
-    ms = timed_graph_steps(ls, steps, warmup)
+    ms = replay_ms(capture_graphs(ls), steps, warmup)
     gbs = ls.bytes_per_copy / (ms * 1e-3) / 1e9
-    per = per_launch_times(ls, max(2, copies))
+    per = per_shape_graph_times(ls, 5)
     shapes = {f"{K}x{N}": {"us": per[(K, N)] * 1e3,
                            "GB/s": gemv_bytes(M, K, N) / (per[(K, N)] * 1e-3) / 1e9} for K, N in kn}
     res = {"M": M, "ms_per_step": ms, "GB/s": gbs, "launches_per_step": ls.launches_per_copy,
            "bytes_per_step": ls.bytes_per_copy, "avg_launch_us": ms * 1e3 / ls.launches_per_copy,
-           "per_shape_eager": shapes}
+           "per_shape_graph": shapes}
     del ls
     return res
 

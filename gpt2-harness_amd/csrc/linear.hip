@@ -116,7 +116,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 100; }
+extern "C" int tiq_version(void) { return 110; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
