@@ -27,8 +27,8 @@
 //   * the chunk is dequantized in registers (sign-extended bytes or biased
 //     nibbles -> fp32, one v_cvt_f32_i32_sdwa per int8 code) once and reused
 //     for all MT activation rows;
-//   * per-row partial sums are reduced across the wavefront with xor
-//     shuffles; the per-channel scale and the bias are applied once per
+//   * per-row partial sums are reduced across the wavefront with DPP lane
+//     moves; the per-channel scale and the bias are applied once per
 //     output; the group-wise format scales each 32-column chunk's partial sum
 //     by its group's fp16 scale.
 // Optional fusions for the decode step of a GPT-2 block (model.py:410-427):
@@ -151,7 +151,7 @@ __device__ __forceinline__ void block_sum(float (&v)[MT], float* red) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        const float s = wave_sum(v[m]);
+        const float s = wave_sum_dpp(v[m]);
         if (lane == 0) red[m * kWavesPerBlock + wave] = s;
     }
     __syncthreads();
@@ -329,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = wave_sum(acc[r][m]);
+        for (int m = 0; m < MT; ++m) acc[r][m] = wave_sum_dpp(acc[r][m]);
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -361,8 +361,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
 //   * rows are handed to the eight XCDs in contiguous blocks (the hardware
 //     deals workgroups round-robin over XCDs), so a 128-byte line of scales or
 //     biases is fetched into one XCD's L2 rather than into all eight;
-//   * the lane partial sums are reduced across the wavefront; lane m stores
-//     output (m0 + m, n).
+//   * the lane partial sums are reduced across the wavefront with DPP lane
+//     moves; lane m stores output (m0 + m, n).
 template <typename TX>
 __device__ __forceinline__ float4 x4_of(const u32x4& u, int half);
 
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
         }
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = wave_sum(acc[m]);
+    for (int m = 0; m < MT; ++m) acc[m] = wave_sum_dpp(acc[m]);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         if (lane == m && m0 + m < M) {

@@ -1,6 +1,7 @@
 // hbm_read_probe: measures what one kernel launch can read from HBM on this
 // GPU, as a function of bytes per launch, 16-byte loads in flight per lane
-// and grid size, plus the per-launch cost of back-to-back launches. Buffers
+// and grid size, plus the per-launch cost of back-to-back launches (on a
+// stream and inside a HIP graph, with an empty kernel for the floor). Buffers
 // rotate over a 2 GiB region so every launch reads cold (past the 256 MB
 // Infinity Cache). It calibrates the attainable bandwidth the GEMV and
 // quantize kernels are judged against; it is not part of libtiq_hip.so.
@@ -31,6 +32,8 @@ __global__ __launch_bounds__(256) void read_kernel(const uint4* __restrict__ p, 
     for (long c = tid + U * nthr; c < nchunks; c += nthr) { uint4 t = p[c]; s ^= t.x ^ t.y ^ t.z ^ t.w; }
     if (s == 0x12345678u) out[tid % 1024] = (float)s;  // practically never taken
 }
+
+__global__ void empty_kernel(float*) {}
 
 int main() {
     const size_t region = 2ull << 30;  // 2 GiB
@@ -101,6 +104,45 @@ int main() {
         CK(hipEventElapsedTime(&ms, a, b));
         printf("back-to-back bytes=%zu: %.2f us per launch (%.1f GB/s)\n", bytes, ms * 1e3 / 200, bytes * 200 / (ms * 1e-3) / 1e9);
     }
+    // The same inside a HIP graph, as the decode step runs: 240 launches
+    // captured back to back, the graph replayed; an empty kernel (the launch
+    // floor) and one 16-byte load per thread of 1.8 / 10.2 MB (cold).
+    hipStream_t st;
+    CK(hipStreamCreate(&st));
+    for (size_t bytes : {0ul, 1800000ul, 10200000ul}) {
+        const long nchunks = (long)(bytes / 16);
+        const unsigned blocks = bytes ? (unsigned)((nchunks + 255) / 256) : 1u;
+        const size_t stride = ((bytes + (1 << 20)) >> 20) << 20;
+        const int slots = (int)(region / stride) - 1;
+        const int L = 240;
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        CK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+        for (int r = 0; r < L; ++r) {
+            if (bytes == 0) hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, st, out);
+            else hipLaunchKernelGGL(read_kernel<1>, dim3(blocks), dim3(256), 0, st, buf + (size_t)(r % slots) * (stride / 16), nchunks, out);
+        }
+        CK(hipStreamEndCapture(st, &g));
+        CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        CK(hipGraphLaunch(ge, st));
+        CK(hipStreamSynchronize(st));
+        float best = 1e30f;
+        for (int rep = 0; rep < 5; ++rep) {
+            CK(hipEventRecord(a, st));
+            CK(hipGraphLaunch(ge, st));
+            CK(hipEventRecord(b, st));
+            CK(hipEventSynchronize(b));
+            float ms;
+            CK(hipEventElapsedTime(&ms, a, b));
+            best = ms < best ? ms : best;
+        }
+        printf("graph back-to-back bytes=%zu: %.3f us per launch (%.1f GB/s)\n", bytes, best * 1e3 / L,
+               bytes / (best * 1e-3 / L) / 1e9);
+        fflush(stdout);
+        CK(hipGraphExecDestroy(ge));
+        CK(hipGraphDestroy(g));
+    }
+    CK(hipStreamDestroy(st));
     CK(hipFree(buf));
     CK(hipFree(out));
     printf("done\n");

@@ -53,6 +53,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// x moved across lanes by DPP control CTRL; lanes of rows outside ROW_MASK get 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wavefront with DPP lane moves (VALU operations,
+// no round trips through the LDS crossbar as with shuffles): pairs and quads
+// (quad_perm), 8 and 16 lanes (row_half_mirror, row_mirror), then rows 0 -> 1
+// and 2 -> 3 (row_bcast:15) and rows 0-1 -> 2-3 (row_bcast:31); lane 63 holds
+// the total, which every lane receives. All 64 lanes must be active.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_move<0xB1>(v);        // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);        // quad_perm [2, 3, 0, 1]
+    v += dpp_move<0x141>(v);       // row_half_mirror
+    v += dpp_move<0x140>(v);       // row_mirror
+    v += dpp_move<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_move<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // (amax / qmax).clamp(min=FLT_MIN) with the IEEE correctly rounded division
 // (hipcc keeps fp32 division correctly rounded unless told otherwise; this
 // library is never built with fast-math). NaN passes through the clamp.
