@@ -14,6 +14,8 @@ from .qlinear import QuantLinear
 from .quantization import (
     TARGET_SUFFIXES,
     QuantResult,
+    SyntheticTokenStream,
+    load_packed,
     pack_int4,
     packed_size_bytes,
     perplexity_with_error_bars,
@@ -22,6 +24,7 @@ from .quantization import (
     quantize_linear,
     quantize_model,
     quantize_tensor,
+    save_packed,
     unpack_int4,
 )
 from .sampling import generate
@@ -35,10 +38,12 @@ __all__ = [
     "KVCache",
     "QuantLinear",
     "QuantResult",
+    "SyntheticTokenStream",
     "TARGET_SUFFIXES",
     "generate",
     "generate_graph",
     "gpt2_config",
+    "load_packed",
     "make_decoder",
     "pack_int4",
     "packed_size_bytes",
@@ -48,5 +53,6 @@ __all__ = [
     "quantize_linear",
     "quantize_model",
     "quantize_tensor",
+    "save_packed",
     "unpack_int4",
 ]

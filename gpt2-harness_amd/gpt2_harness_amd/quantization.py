@@ -13,8 +13,12 @@ Same public names, argument meaning and error messages as the reference's
   the codes (int8, or nibble-packed for <= 4 bits), so the forward pass reads
   1 (or 0.5) byte per weight instead of the 4 bytes of the reference's
   simulated fp32 ``W_hat``; the stats dict has the reference's keys;
-* :func:`packed_size_bytes`   (``:219-259``) -- same payload schema;
-* :func:`perplexity_with_error_bars` (``:262-319``) and :class:`QuantResult`.
+* :func:`packed_size_bytes`   (``:219-259``) -- same payload schema, written by
+  :func:`save_packed`; :func:`load_packed` builds the quantized model straight
+  from such a file (codes to :class:`QuantLinear`, no fp32 round trip);
+* :func:`perplexity_with_error_bars` (``:262-319``, forward passes and cross
+  entropy on the GPU) with :class:`SyntheticTokenStream` standing in for the
+  corpus, and :class:`QuantResult`.
 
 Everything runs on the GPU: tensors must live on a ROCm device, and the
 functions raise when the HIP library is missing. Group-wise int4 with fp16
@@ -41,6 +45,7 @@ from .qlinear import FMT_W4, FMT_W4G, FMT_W8, QuantLinear
 __all__ = [
     "TARGET_SUFFIXES",
     "QuantResult",
+    "SyntheticTokenStream",
     "pack_int4",
     "packed_size_bytes",
     "perplexity_with_error_bars",
@@ -49,6 +54,8 @@ __all__ = [
     "quantize_linear",
     "quantize_model",
     "quantize_tensor",
+    "load_packed",
+    "save_packed",
     "unpack_int4",
 ]
 
@@ -218,6 +225,8 @@ def quantize_model(
     granularity: Granularity = "per_channel",
     include_embedding: bool = False,
     group_size: int | None = None,
+    *,
+    save_to: str | Path | None = None,
 ) -> tuple[nn.Module, dict[str, Any]]:
     """Return a copy of the model with its target Linears quantized.
 
@@ -229,6 +238,8 @@ def quantize_model(
             its ``W_hat`` is written back in fp32 as the reference does.
         group_size: Extension: group-wise int4 with fp16 scales for the
             target Linears (``bits`` must be 4).
+        save_to: Extension: also keep the packed checkpoint whose size is
+            ``packed_bytes`` at this path (read back by :func:`load_packed`).
 
     Returns:
         ``(quantized_model, stats)`` with the reference's stats keys.
@@ -273,7 +284,8 @@ def quantize_model(
         "n_quantized_params": n_quant_params,
         "n_total_params": total_params,
         "fraction_quantized": n_quant_params / total_params,
-        "packed_bytes": packed_size_bytes(q_model, codes, bits, group_size=group_size),
+        "packed_bytes": (packed_size_bytes(q_model, codes, bits, group_size=group_size) if save_to is None
+                         else save_packed(q_model, codes, bits, save_to, group_size=group_size)),
         "fp32_bytes": total_params * 4,
     }
     stats["compression_ratio"] = stats["fp32_bytes"] / stats["packed_bytes"]
@@ -282,24 +294,28 @@ def quantize_model(
     return q_model, stats
 
 
-def packed_size_bytes(
+def _packed_payload(
     model: nn.Module,
     codes: dict[str, tuple[torch.Tensor, torch.Tensor]],
     bits: int,
     group_size: int | None = None,
-) -> int:
-    """Serialise a packed checkpoint (reference payload schema) and return its size.
+) -> dict[str, torch.Tensor]:
+    """The reference's packed checkpoint payload (``quantization.py:239-250``).
 
     Keys: ``name.q`` (int8 codes, or ``pack_int4`` bytes at 4 bits),
-    ``name.scale`` (fp32; fp16 for the group-wise format), ``name.shape``
-    (int32), plus every other unique parameter in fp32.
+    ``name.scale`` (fp32), ``name.shape`` (int32 ``[N, K]``), plus every other
+    unique parameter in fp32. The group-wise format (no counterpart in the
+    reference) stores its per-row nibbles, fp16 group scales, the true
+    ``[N, K]`` and ``name.group`` (int32).
     """
     payload: dict[str, torch.Tensor] = {}
     for name, (q, scale) in codes.items():
-        if group_size is not None and q.dtype == torch.uint8:
+        if group_size is not None and q.dtype == torch.uint8 and scale.dtype == torch.float16:
+            K = int(model.get_submodule(name).in_features)
             payload[f"{name}.q"] = q.cpu()
             payload[f"{name}.scale"] = scale.cpu()
-            payload[f"{name}.shape"] = torch.tensor([q.shape[0], 0], dtype=torch.int32)
+            payload[f"{name}.shape"] = torch.tensor([q.shape[0], K], dtype=torch.int32)
+            payload[f"{name}.group"] = torch.tensor(group_size, dtype=torch.int32)
             continue
         payload[f"{name}.q"] = (pack_int4(q) if bits == 4 else q).cpu()
         payload[f"{name}.scale"] = scale.to(torch.float32).cpu()
@@ -312,14 +328,144 @@ def packed_size_bytes(
             continue
         seen.add(id(p))
         payload[name] = p.detach().to(torch.float32).cpu()
+    return payload
 
+
+def save_packed(
+    model: nn.Module,
+    codes: dict[str, tuple[torch.Tensor, torch.Tensor]],
+    bits: int,
+    path: str | Path,
+    group_size: int | None = None,
+) -> int:
+    """Write the packed checkpoint (the reference's payload schema, ``torch.save``)
+    to ``path`` and return its size in bytes. ``codes`` is what
+    :func:`quantize_model` records (``name -> (q, scale)``)."""
+    torch.save(_packed_payload(model, codes, bits, group_size), Path(path))
+    return Path(path).stat().st_size
+
+
+def packed_size_bytes(
+    model: nn.Module,
+    codes: dict[str, tuple[torch.Tensor, torch.Tensor]],
+    bits: int,
+    group_size: int | None = None,
+) -> int:
+    """Serialise a packed checkpoint (reference payload schema) and return its
+    real file size (``quantization.py:219-259``)."""
     with tempfile.NamedTemporaryFile(suffix=".pt", delete=False) as fh:
         tmp = Path(fh.name)
     try:
-        torch.save(payload, tmp)
-        return tmp.stat().st_size
+        return save_packed(model, codes, bits, tmp, group_size)
     finally:
         tmp.unlink(missing_ok=True)
+
+
+def _bits_of_codes(q: torch.Tensor) -> int:
+    """Smallest width in [2, 8] whose symmetric range holds every code."""
+    lo, hi = int(q.min()), int(q.max())
+    b = 2
+    while b < 8 and (lo < -(1 << (b - 1)) or hi > (1 << (b - 1)) - 1):
+        b += 1
+    return b
+
+
+@torch.no_grad()
+def load_packed(model: nn.Module, source: str | Path | dict[str, torch.Tensor]) -> nn.Module:
+    """Fill ``model`` from a packed checkpoint written by :func:`save_packed`.
+
+    Every ``name.q`` entry becomes a :class:`QuantLinear` built straight from
+    the stored codes and scales (no fp32 weight and no requantization on the
+    way); a quantized embedding (``include_embedding``) gets the reference's
+    fp32 ``W_hat``; every other stored parameter is copied in. ``model`` is a
+    model of the same configuration on the GPU (its own weights are
+    overwritten) and is returned. The file is read with ``weights_only=True``.
+    """
+    payload = source if isinstance(source, dict) else torch.load(Path(source), map_location="cpu",
+                                                                 weights_only=True)
+    dev = next(model.parameters()).device
+    _lib.require_gpu(next(model.parameters()), "model parameters")
+    names = [k[: -len(".q")] for k in payload if k.endswith(".q")]
+    for name in names:
+        q = payload[f"{name}.q"].to(dev)
+        scale = payload[f"{name}.scale"].to(dev)
+        N, K = (int(v) for v in payload[f"{name}.shape"].tolist())
+        module = model.get_submodule(name)
+        bias = payload.get(f"{name}.bias")
+        bias = None if bias is None else bias.to(dev)
+        if f"{name}.group" in payload:
+            g = int(payload[f"{name}.group"])
+            new = QuantLinear(q, scale, bias, K, N, 4, f"group{g}", FMT_W4G, g)
+            _set_submodule(model, name, new)
+            continue
+        granularity = "per_tensor" if scale.dim() == 0 else "per_channel"
+        if q.dtype == torch.uint8:  # pack_int4 of the row-major codes
+            bits = 4
+            codes8 = None if K % 2 == 0 else unpack_int4(q, N * K).view(N, K)
+        else:
+            codes8 = q.view(N, K)
+            bits = _bits_of_codes(codes8)
+        if isinstance(module, nn.Embedding):
+            c8 = codes8 if codes8 is not None else unpack_int4(q, N * K).view(N, K)
+            w_hat = torch.empty(N, K, device=dev)
+            rc = _lib.lib().tiq_dequantize_int8(c8.data_ptr(), scale.data_ptr(), int(granularity == "per_channel"),
+                                                N, K, w_hat.data_ptr(), _lib.stream_of(c8))
+            _lib.check(rc, "dequantize")
+            module.weight.data.copy_(w_hat)
+            continue
+        row_scale = scale.reshape(-1).expand(N).contiguous() if granularity == "per_tensor" else scale.reshape(N)
+        # the storage quantize_linear chooses: nibbles for <= 4 bits and even K
+        if codes8 is None:
+            new = QuantLinear(q, row_scale, bias, K, N, bits, granularity, FMT_W4)
+        elif bits <= 4 and K % 2 == 0:
+            new = QuantLinear(pack_int4(codes8), row_scale, bias, K, N, bits, granularity, FMT_W4)
+        else:
+            new = QuantLinear(codes8, row_scale, bias, K, N, bits, granularity, FMT_W8)
+        _set_submodule(model, name, new)
+    quantized = set(names)
+    for pname, p in model.named_parameters():
+        owner = pname.rpartition(".")[0]
+        if owner in quantized or pname not in payload:
+            continue
+        p.data.copy_(payload[pname].to(dev))
+    return model
+
+
+class SyntheticTokenStream:
+    """A seeded uniform token stream with the reference's perplexity windows.
+
+    Stands in for the reference's ``TokenDataset`` (``data.py:123-230``) where
+    the corpus cannot be fetched: ``sequential_batches`` walks the split in
+    non-overlapping windows of ``block_size`` predictions (a window holds
+    ``block_size + 1`` ids, ``x = ids[:-1]``, ``y = ids[1:]``, windows ``w``
+    starting at ``w * block_size``), ``batch_size`` windows per batch, a
+    trailing short window dropped -- the shape of the reference's
+    ``sequential_batches`` (``data.py:192-230``).
+    """
+
+    def __init__(self, vocab_size: int, n_tokens: int, block_size: int = 128, seed: int = 0) -> None:
+        if n_tokens <= block_size + 1:
+            raise ValueError(f"a stream of {n_tokens} tokens is too short for block_size={block_size}")
+        gen = torch.Generator().manual_seed(seed)
+        self.tokens = torch.randint(0, vocab_size, (n_tokens,), generator=gen, dtype=torch.int64)
+        self.block_size = block_size
+
+    def sequential_batches(self, split: str, batch_size: int, limit: int | None = None):
+        if split not in ("train", "val"):
+            raise ValueError(f"unknown split {split!r}")
+        data, T = self.tokens, self.block_size
+        n_windows = (len(data) - 1) // T
+        out = []
+        for start in range(0, n_windows, batch_size):
+            rows = [data[w * T : w * T + T + 1] for w in range(start, min(start + batch_size, n_windows))]
+            rows = [r for r in rows if len(r) == T + 1]
+            if not rows:
+                break
+            block = torch.stack(rows)
+            out.append((block[:, :-1].contiguous(), block[:, 1:].contiguous()))
+            if limit is not None and len(out) >= limit:
+                break
+        return out
 
 
 @torch.no_grad()
@@ -334,7 +480,10 @@ def perplexity_with_error_bars(
     """Held-out perplexity with a spread over disjoint chunks (``quantization.py:262-319``).
 
     ``dataset`` is anything with ``sequential_batches(split, batch_size=, limit=)``
-    returning ``(x, y)`` id tensors, as the reference's ``TokenDataset``.
+    returning ``(x, y)`` id tensors, as the reference's ``TokenDataset`` or
+    :class:`SyntheticTokenStream`. The forward passes (prefill-shaped Linears,
+    ``M = batch_size * block_size``) and the summed cross entropy run on the
+    GPU; only one scalar per batch comes back to the host.
     """
     model = model.to(device).eval()
     batches = dataset.sequential_batches("val", batch_size=batch_size, limit=n_chunks * batches_per_chunk)
@@ -345,8 +494,9 @@ def perplexity_with_error_bars(
             continue
         total, n = 0.0, 0
         for x, y in group:
-            logits = model(x.to(device))["logits"].float().cpu()
-            total += F.cross_entropy(logits.reshape(-1, logits.size(-1)), y.reshape(-1), reduction="sum").item()
+            logits = model(x.to(device))["logits"].float()
+            y = y.to(logits.device)
+            total += float(F.cross_entropy(logits.reshape(-1, logits.size(-1)), y.reshape(-1), reduction="sum"))
             n += y.numel()
         chunk_losses.append(total / n)
     mean = statistics.fmean(chunk_losses)

@@ -124,3 +124,24 @@ def test_kv_cache_length_semantics():
     assert c.seq_len == 3 and c.length(1) == 0
     kk, _ = c.update(0, k[:, :, :1], k[:, :, :1])
     assert kk.shape[-2] == 4
+
+
+def test_synthetic_token_stream_windows():
+    """The perplexity windows: non-overlapping blocks of T predictions that
+    share one id with the next (ids[wT : wT + T + 1]), y = x shifted by one,
+    batch_size windows per batch, the limit honoured, seeded."""
+    T, n = 16, 16 * 10 + 5
+    ds = g.SyntheticTokenStream(50, n, T, seed=3)
+    assert torch.equal(ds.tokens, g.SyntheticTokenStream(50, n, T, seed=3).tokens)
+    assert not torch.equal(ds.tokens, g.SyntheticTokenStream(50, n, T, seed=4).tokens)
+    batches = ds.sequential_batches("val", batch_size=4)
+    assert [tuple(x.shape) for x, _ in batches] == [(4, T), (4, T), (2, T)]   # 10 windows
+    flat_x = torch.cat([x for x, _ in batches]).reshape(-1)
+    flat_y = torch.cat([y for _, y in batches]).reshape(-1)
+    assert torch.equal(flat_x, ds.tokens[: 10 * T]) and torch.equal(flat_y, ds.tokens[1 : 10 * T + 1])
+    assert len(ds.sequential_batches("val", batch_size=4, limit=2)) == 2
+    assert int(ds.tokens.max()) < 50 and int(ds.tokens.min()) >= 0
+    with pytest.raises(ValueError):
+        g.SyntheticTokenStream(50, T + 1, T)
+    with pytest.raises(ValueError):
+        ds.sequential_batches("test", batch_size=4)
