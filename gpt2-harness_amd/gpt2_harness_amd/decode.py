@@ -15,7 +15,8 @@ Two step implementations:
   head): the library's decode kernels only -- an embedding kernel, then per
   block LayerNorm+``c_attn``, attention over the cache, ``c_proj``+residual,
   LayerNorm+``c_fc``+GELU, ``c_proj``+residual (5 launches), then
-  LayerNorm+``lm_head`` and ``argmax`` -- 5 * n_layer + 4 launches per token;
+  LayerNorm+``lm_head`` (fp32, or int8 / int4 codes when the embedding was
+  quantized) and ``argmax`` -- 5 * n_layer + 4 launches per token;
 * :class:`GraphDecoder`: the model's own modules as torch ops with attention
   over all ``T_max`` slots, the slots after the current position masked to
   ``-inf`` (probability exactly 0), for any other model layout.
@@ -206,9 +207,11 @@ def fused_supported(model) -> str | None:
                 return "every target Linear must be quantized"
         if block.attn.head_mask is not None or block.mlp.neuron_mask is not None:
             return "head / neuron masks are not fused"
-    w = model.lm_head.weight
-    if w.dtype != torch.float32 or model.lm_head.bias is not None or model.wte.weight.dtype != torch.float32:
-        return "needs an fp32 bias-free lm_head"
+    head = model.lm_head
+    if model.wte.weight.dtype != torch.float32 or head.bias is not None:
+        return "needs an fp32 embedding and a bias-free lm_head"
+    if not isinstance(head, QuantLinear) and head.weight.dtype != torch.float32:
+        return "needs an fp32 or quantized lm_head"
     return None
 
 
@@ -228,7 +231,10 @@ class FusedDecoder(_DecoderBase):
         self.hid = torch.zeros(B, model.h[0].mlp.c_fc.out_features, device=dev)
         self.logits = torch.zeros(B, cfg.vocab_size, device=dev)
         self.tok_flat = self.tok.view(-1)
-        self.head_w = model.lm_head.weight.detach().contiguous()
+        # the head: int8 / int4 codes when the embedding was quantized
+        # (include_embedding), else the tied fp32 weight
+        self.head_q = model.lm_head if isinstance(model.lm_head, QuantLinear) else None
+        self.head_w = None if self.head_q is not None else model.lm_head.weight.detach().contiguous()
         self.L = _lib.lib()
         self.argmax_ws = torch.empty(int(self.L.tiq_argmax_rows_workspace(B)), dtype=torch.uint8, device=dev)
         # batched steps stage LayerNorm'd, split activations here (0 bytes: the
@@ -237,7 +243,8 @@ class FusedDecoder(_DecoderBase):
         qkv = C + 2 * self.Hkv * self.hd
         ws = max(int(self.L.tiq_linear_fused_workspace(_lib.F32, _lib.WF_INT8, B, k, n))
                  for k, n in ((C, qkv), (C, C), (C, hidden), (hidden, C)))
-        ws = max(ws, int(self.L.tiq_linear_fused_workspace(_lib.F32, _lib.WF_F32, B, C, cfg.vocab_size)))
+        head_fmt = _lib.WF_F32 if self.head_q is None else _WF[self.head_q.fmt]
+        ws = max(ws, int(self.L.tiq_linear_fused_workspace(_lib.F32, head_fmt, B, C, cfg.vocab_size)))
         self.lin_ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
         self.lin_ws_bytes = ws
 
@@ -272,11 +279,14 @@ class FusedDecoder(_DecoderBase):
             self._linear(mlp.c_fc, self.x, self.hid, ln=block.ln_2, act=_lib.ACT_GELU_TANH)
             self._linear(mlp.c_proj, self.hid, self.x, res=self.x)
         ln = m.ln_f
-        rc = L.tiq_linear_fused_ws(self.x.data_ptr(), _lib.F32, B, C, C, self.head_w.data_ptr(), _lib.WF_F32, None,
-                                   None, 0, None, cfg.vocab_size, self.logits.data_ptr(), _lib.F32, cfg.vocab_size,
-                                   ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps), 0, None, 0,
-                                   self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
-        _lib.check(rc, "lm_head")
+        if self.head_q is not None:
+            self._linear(self.head_q, self.x, self.logits, ln=ln)
+        else:
+            rc = L.tiq_linear_fused_ws(self.x.data_ptr(), _lib.F32, B, C, C, self.head_w.data_ptr(), _lib.WF_F32,
+                                       None, None, 0, None, cfg.vocab_size, self.logits.data_ptr(), _lib.F32,
+                                       cfg.vocab_size, ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps), 0,
+                                       None, 0, self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
+            _lib.check(rc, "lm_head")
         # argmax also records the token at slot pos + 1 and advances pos
         _lib.check(L.tiq_argmax_rows(self.logits.data_ptr(), B, cfg.vocab_size, cfg.vocab_size,
                                      self.tok_flat.data_ptr(), self.out.data_ptr(), self.T, self.pos.data_ptr(),

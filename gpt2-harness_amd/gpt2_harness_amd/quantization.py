@@ -205,12 +205,23 @@ def quantize_linear(
         mod = QuantLinear(packed, s16, bias, K, N, bits, f"group{group_size}", FMT_W4G, group_size)
         return mod, (packed, s16)
     q, scale = quantize_tensor(w, bits, granularity)
+    return _quant_linear_from_codes(q, scale, bias, bits, granularity), (q, scale)
+
+
+def _quant_linear_from_codes(q: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None, bits: int,
+                             granularity: str) -> QuantLinear:
+    """The storage :func:`quantize_linear` picks for ``(q, scale)`` of an
+    ``(N, K)`` weight: nibbles for <= 4 bits and even K, int8 codes otherwise."""
+    N, K = q.shape
     row_scale = scale.reshape(-1).expand(N).contiguous() if granularity == "per_tensor" else scale.reshape(N)
     if bits <= 4 and K % 2 == 0:
-        mod = QuantLinear(pack_int4(q), row_scale, bias, K, N, bits, granularity, FMT_W4)
-    else:
-        mod = QuantLinear(q, row_scale, bias, K, N, bits, granularity, FMT_W8)
-    return mod, (q, scale)
+        return QuantLinear(pack_int4(q), row_scale, bias, K, N, bits, granularity, FMT_W4)
+    return QuantLinear(q, row_scale, bias, K, N, bits, granularity, FMT_W8)
+
+
+def _tied_head(model: nn.Module) -> bool:
+    head, wte = getattr(model, "lm_head", None), getattr(model, "wte", None)
+    return isinstance(head, nn.Linear) and isinstance(wte, nn.Embedding) and head.weight is wte.weight
 
 
 def _set_submodule(root: nn.Module, name: str, new: nn.Module) -> None:
@@ -235,7 +246,10 @@ def quantize_model(
         bits: Bit width in ``[2, 8]``.
         granularity: ``per_channel`` or ``per_tensor``.
         include_embedding: Also quantize ``wte`` (and so the tied ``lm_head``):
-            its ``W_hat`` is written back in fp32 as the reference does.
+            its ``W_hat`` is written back in fp32 as the reference does, for
+            the embedding lookup; the tied ``lm_head`` becomes a
+            :class:`QuantLinear` over the same codes, so the head reads 1 (or
+            0.5) byte per weight and computes the same ``x @ W_hat^T``.
         group_size: Extension: group-wise int4 with fp16 scales for the
             target Linears (``bits`` must be 4).
         save_to: Extension: also keep the packed checkpoint whose size is
@@ -268,9 +282,12 @@ def quantize_model(
                 new, code = quantize_linear(module, bits, granularity, group_size)
                 _set_submodule(q_model, name, new)
             else:
+                tied = _tied_head(q_model)
                 q, scale = quantize_tensor(w.float(), bits, granularity)
                 code = (q, scale)
                 module.weight.data = quantize_dequantize(w.float(), bits, granularity).to(w.dtype)
+                if tied:
+                    q_model.lm_head = _quant_linear_from_codes(q, scale, None, bits, granularity)
             codes[name] = code
             quantized.append(name)
             n_quant_params += w.numel()
@@ -401,27 +418,21 @@ def load_packed(model: nn.Module, source: str | Path | dict[str, torch.Tensor]) 
         granularity = "per_tensor" if scale.dim() == 0 else "per_channel"
         if q.dtype == torch.uint8:  # pack_int4 of the row-major codes
             bits = 4
-            codes8 = None if K % 2 == 0 else unpack_int4(q, N * K).view(N, K)
+            c8 = unpack_int4(q, N * K).view(N, K)
         else:
-            codes8 = q.view(N, K)
-            bits = _bits_of_codes(codes8)
+            c8 = q.view(N, K)
+            bits = _bits_of_codes(c8)
         if isinstance(module, nn.Embedding):
-            c8 = codes8 if codes8 is not None else unpack_int4(q, N * K).view(N, K)
+            tied = _tied_head(model)
             w_hat = torch.empty(N, K, device=dev)
             rc = _lib.lib().tiq_dequantize_int8(c8.data_ptr(), scale.data_ptr(), int(granularity == "per_channel"),
                                                 N, K, w_hat.data_ptr(), _lib.stream_of(c8))
             _lib.check(rc, "dequantize")
             module.weight.data.copy_(w_hat)
+            if tied:  # as quantize_model: the head over the same codes
+                model.lm_head = _quant_linear_from_codes(c8, scale, None, bits, granularity)
             continue
-        row_scale = scale.reshape(-1).expand(N).contiguous() if granularity == "per_tensor" else scale.reshape(N)
-        # the storage quantize_linear chooses: nibbles for <= 4 bits and even K
-        if codes8 is None:
-            new = QuantLinear(q, row_scale, bias, K, N, bits, granularity, FMT_W4)
-        elif bits <= 4 and K % 2 == 0:
-            new = QuantLinear(pack_int4(codes8), row_scale, bias, K, N, bits, granularity, FMT_W4)
-        else:
-            new = QuantLinear(codes8, row_scale, bias, K, N, bits, granularity, FMT_W8)
-        _set_submodule(model, name, new)
+        _set_submodule(model, name, _quant_linear_from_codes(c8, scale, bias, bits, granularity))
     quantized = set(names)
     for pname, p in model.named_parameters():
         owner = pname.rpartition(".")[0]

@@ -104,8 +104,11 @@ def init_params(cfg: Shape, seed: int | None = 0) -> dict[str, torch.Tensor]:
     return p
 
 
-def quantize_params(p: dict[str, torch.Tensor], bits: int = 8, granularity: str = "per_channel"):
-    """Simulated quantization of the target weights (``quantization.py:188-197``).
+def quantize_params(p: dict[str, torch.Tensor], bits: int = 8, granularity: str = "per_channel",
+                    include_embedding: bool = False):
+    """Simulated quantization of the target weights (``quantization.py:186-197``);
+    with ``include_embedding`` also ``wte`` (``:189-192``), whose ``W_hat`` the
+    tied head then uses (``forward`` reads ``wte.weight`` for both).
 
     Returns ``(params_with_W_hat, codes)`` where ``codes[name] = (q, scale)``.
     """
@@ -113,7 +116,8 @@ def quantize_params(p: dict[str, torch.Tensor], bits: int = 8, granularity: str 
     codes = {}
     for key, w in p.items():
         name = key[: -len(".weight")] if key.endswith(".weight") else None
-        if name is None or not name.endswith(TARGET_SUFFIXES):
+        is_emb = include_embedding and name == "wte"
+        if name is None or not (name.endswith(TARGET_SUFFIXES) or is_emb):
             continue
         q, s = Q.quantize_tensor(w.numpy(), bits, granularity)
         codes[name] = (q, s)

@@ -118,7 +118,10 @@ def test_include_embedding_writes_w_hat(reference_decode, dev):
     from oracle import quant as OQ
 
     assert np.array_equal(qm.wte.weight.detach().cpu().numpy(), OQ.quantize_dequantize(w, 8))
-    assert qm.lm_head.weight is qm.wte.weight
+    # the tied head now reads the same codes: its W_hat is the embedding's
+    assert isinstance(qm.lm_head, g.QuantLinear)
+    assert torch.equal(qm.lm_head.weight, qm.wte.weight)
+    assert model.lm_head.weight is model.wte.weight   # the source model keeps its tie
 
 
 def test_groupwise_model_decodes(reference_decode, dev):
@@ -176,4 +179,46 @@ def test_batched_fused_decode_matches_oracle(reference_decode, dev, batch):
     dec = g.make_decoder(qm, batch, 36)
     assert isinstance(dec, g.FusedDecoder)
     got = g.generate_graph(qm, prompt.to(dev), 20, decoder=dec)
+    assert got.cpu().tolist() == want.tolist(), f"min margin {min(margins):.3g}"
+
+
+MINI = dict(vocab_size=97, n_positions=96, n_layer=2, n_head=2, n_embd=128)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("batch", [1, 8])
+def test_quantized_head_matches_oracle(dev, bits, batch):
+    """include_embedding (the reference's SCHEMES row 5): wte holds the fp32
+    W_hat for the lookup and the tied head runs on the same codes; eager
+    generate and the captured fused decode give the oracle's tokens, whose
+    head is the fp32 W_hat (quantization.py:189-197)."""
+    shp = OM.Shape(MINI["vocab_size"], MINI["n_positions"], MINI["n_layer"], MINI["n_head"], MINI["n_embd"])
+    qp, _ = OM.quantize_params(OM.init_params(shp, 0), bits, include_embedding=True)
+    prompt = OM.benchmark_prompt(shp.vocab_size, batch, 16)
+    want, margins = OM.generate_greedy(qp, shp, prompt, 20)
+    qm, stats = g.quantize_model(_model(MINI, dev), bits, include_embedding=True)
+    assert stats["n_quantized_tensors"] == 4 * MINI["n_layer"] + 1
+    assert isinstance(qm.lm_head, g.QuantLinear)
+    assert torch.equal(qm.lm_head.weight, qm.wte.weight)        # one W_hat, two storages
+    assert torch.equal(qm.wte.weight.cpu(), qp["wte.weight"])    # the oracle's W_hat, bit for bit
+    eager = g.generate(qm, prompt.to(dev), 20)
+    assert eager.cpu().tolist() == want.tolist(), f"min margin {min(margins):.3g}"
+    dec = g.make_decoder(qm, batch, 36)
+    assert isinstance(dec, g.FusedDecoder)
+    got = g.generate_graph(qm, prompt.to(dev), 20, decoder=dec)
+    assert got.cpu().tolist() == want.tolist(), f"min margin {min(margins):.3g}"
+
+
+def test_quantized_head_gpt2_small_matches_oracle(dev):
+    """GPT-2 small int8 per-channel + embedding, 64-token prompt, 64 greedy
+    tokens through the captured fused decode (int8 head GEMV over 50257
+    rows) against the oracle's fp32 CPU generation."""
+    shp = OM.GPT2_SMALL
+    qp, _ = OM.quantize_params(OM.init_params(shp, 0), 8, include_embedding=True)
+    prompt = OM.benchmark_prompt(shp.vocab_size, 1, 64)
+    want, margins = OM.generate_greedy(qp, shp, prompt, 64)
+    cfg = dict(vocab_size=shp.vocab_size, n_positions=shp.n_positions, n_layer=shp.n_layer, n_head=shp.n_head,
+               n_embd=shp.n_embd)
+    qm, _ = g.quantize_model(_model(cfg, dev), 8, include_embedding=True)
+    got = g.generate_graph(qm, prompt.to(dev), 64)
     assert got.cpu().tolist() == want.tolist(), f"min margin {min(margins):.3g}"
