@@ -290,6 +290,70 @@ def decode_section(dev, repeats=3):
             ts.append(time.perf_counter() - t0)
         med = statistics.median(ts)
         res[label] = {"tokens_per_s": 64 / med, "ms_per_token": 1e3 * med / 64, "tokens_match_reference": match}
+    del dec_t, dec_f, qm
+    # the reference's fifth scheme: int8 per-channel + embedding; the tied
+    # head (50257 x 768) runs on int8 codes (token parity: the GPU tests
+    # against the oracle, no reference fixture holds these tokens)
+    torch.manual_seed(0)
+    model = g.GPT(g.GPTConfig()).to(dev).eval()
+    qe, _ = g.quantize_model(model, 8, include_embedding=True)
+    del model
+    dec_e = g.FusedDecoder(qe, 1, 128)
+    g.generate_graph(qe, prompt, 64, decoder=dec_e)
+    ts = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.generate_graph(qe, prompt, 64, decoder=dec_e)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    res["graph_fused_int8_embedding"] = {"tokens_per_s": 64 / med, "ms_per_token": 1e3 * med / 64}
+    return res
+
+
+def eval_section(dev):
+    """GPT-2 small seed 0 int8 per-channel: the packed checkpoint written by
+    quantize_model(save_to=) and read back into a fresh model by load_packed,
+    then the reference's held-out evaluation shape (8 chunks x 2 batches x 4
+    windows of 128 tokens: 16 forward passes with M = 512 prefill Linears)
+    over synthetic tokens on the GPU."""
+    import tempfile
+
+    import torch
+
+    import gpt2_harness_amd as g
+
+    torch.manual_seed(0)
+    model = g.GPT(g.GPTConfig()).to(dev).eval()
+    res = {"model": "gpt2 (124M) seed 0, int8 per-channel"}
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "gpt2_int8.pt"
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        qm, stats = g.quantize_model(model, 8, save_to=path)
+        torch.cuda.synchronize()
+        t_quant = time.perf_counter() - t0
+        del qm
+        skeleton = g.GPT(g.GPTConfig()).to(dev).eval()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loaded = g.load_packed(skeleton, path)
+        torch.cuda.synchronize()
+        t_load = time.perf_counter() - t0
+    del model
+    res["packed_checkpoint"] = {"bytes": stats["packed_bytes"], "compression_ratio": stats["compression_ratio"],
+                                "quantize_model_and_save_s": t_quant, "load_packed_s": t_load}
+    ds = g.SyntheticTokenStream(50257, 8 * 2 * 4 * 128 + 1, 128, seed=0)
+    g.perplexity_with_error_bars(loaded, ds, n_chunks=1, batches_per_chunk=1, device=dev)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ppl = g.perplexity_with_error_bars(loaded, ds, device=dev)
+    torch.cuda.synchronize()
+    t = time.perf_counter() - t0
+    res["perplexity"] = {"forward_passes": 16, "tokens": 8 * 2 * 4 * 128, "seconds": t,
+                         "tokens_per_s": 8 * 2 * 4 * 128 / t, "loss_mean": ppl["loss_mean"],
+                         "loss_std": ppl["loss_std"], "ppl_of_mean_loss": ppl["ppl_of_mean_loss"]}
     return res
 
 
@@ -406,7 +470,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode", "decode_xl", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode", "decode_xl", "eval", "copy"],
+                    default=None,
                     help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
                          "used to calibrate the HBM byte counters")
     args = ap.parse_args()
@@ -442,6 +507,9 @@ def main() -> int:
     if args.only == "decode_xl":
         print(json.dumps(decode_xl_section(dev)))
         return 0
+    if args.only == "eval":
+        print(json.dumps(eval_section(dev)))
+        return 0
 
     head = gemv_section(1, SMALL_KN, 12, 6, args.steps, args.warmup, dev, seed=0)
     print(f"# headline gemv M=1: {head['GB/s']:.1f} GB/s, {head['ms_per_step']:.4f} ms/step", file=sys.stderr,
@@ -462,6 +530,8 @@ def main() -> int:
         print("# decode done", file=sys.stderr, flush=True)
         detail["decode_gpt2_xl_int8_b32"] = decode_xl_section(dev)
         print("# xl decode done", file=sys.stderr, flush=True)
+        detail["eval_gpt2_small_int8"] = eval_section(dev)
+        print("# eval done", file=sys.stderr, flush=True)
         cpu = cpu_baseline()
 
     traffic = None

@@ -38,43 +38,48 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     const int b = blockIdx.x / H, h = blockIdx.x % H;
     const int group = H / Hkv, hk = h / group;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int64_t pos = *pos_p;
-    if (pos < 0 || pos >= t_max) {  // position outside the cache: flag the output, touch nothing else
-        if (tid < kHeadDim) y[(int64_t)b * ldy + h * kHeadDim + tid] = NAN;
-        return;
-    }
     const float* row = qkv + (int64_t)b * ld_qkv;
     const int C = H * kHeadDim, KV = Hkv * kHeadDim;
     float* kb = kc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
     float* vb = vc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
 
     // ---- issue every load of the first kPreKeys slots ----
+    // No address depends on pos (a device scalar) and no load sits behind a
+    // branch: slots are clamped into the cache and the values of slots >= pos
+    // are dropped where they are used, so all loads are in flight together.
+    const int64_t last = t_max - 1;
     // keys: slot t = (tid / 4) + 64 j, this lane's 16 dims at qd
     const int qd = (lane & 3) * 16;
     const int kslot = (wave * 16) + (lane >> 2);  // 0..63
     float4 kr[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int64_t t = kslot + 64 * j;
-        const bool ld = t < pos;  // slot pos comes from qkv, not the cache
+        const int64_t t = min((int64_t)(kslot + 64 * j), last);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            kr[j][q] = ld ? reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < 4; ++q) kr[j][q] = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q];
     }
     // values: slot t = wave + 4 i, this lane's dim
     float vr[kPreKeys / 4];
 #pragma unroll
-    for (int i = 0; i < kPreKeys / 4; ++i) {
-        const int64_t t = wave + 4 * i;
-        vr[i] = (t < pos) ? vb[t * kHeadDim + lane] : 0.f;
+    for (int i = 0; i < kPreKeys / 4; ++i) vr[i] = vb[min((int64_t)(wave + 4 * i), last) * kHeadDim + lane];
+    float q_new = 0.f, k_new = 0.f, v_new = 0.f;
+    if (tid < kHeadDim) {
+        q_new = row[h * kHeadDim + tid];
+        k_new = row[C + hk * kHeadDim + tid];
+        v_new = row[C + KV + hk * kHeadDim + tid];
+    }
+    const int64_t pos = *pos_p;
+    if (pos < 0 || pos >= t_max) {  // position outside the cache: flag the output, write nothing else
+        if (tid < kHeadDim) y[(int64_t)b * ldy + h * kHeadDim + tid] = NAN;
+        return;
     }
     if (tid < kHeadDim) {
-        qs[tid] = row[h * kHeadDim + tid];
-        kn[tid] = row[C + hk * kHeadDim + tid];
-        vn[tid] = row[C + KV + hk * kHeadDim + tid];
+        qs[tid] = q_new;
+        kn[tid] = k_new;
+        vn[tid] = v_new;
         if (h % group == 0) {  // one writer per kv head
-            kb[pos * kHeadDim + tid] = kn[tid];
-            vb[pos * kHeadDim + tid] = vn[tid];
+            kb[pos * kHeadDim + tid] = k_new;
+            vb[pos * kHeadDim + tid] = v_new;
         }
     }
     __syncthreads();

@@ -222,6 +222,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
         }
     }
 
+    // LayerNorm weight and bias of the columns this thread normalizes
+    // (k4 = tid, tid + kThreads; rows up to 8 * kThreads columns), requested
+    // with the weights so the normalize pass does not wait on them
+    constexpr int kLnPre = 2;
+    const bool ln_pre = fz.ln_w && K4 <= kLnPre * kThreads;
+    float4 gpre[kLnPre], bpre[kLnPre];
+    if (ln_pre) {
+#pragma unroll
+        for (int j = 0; j < kLnPre; ++j) {
+            const int k4 = min((int)threadIdx.x + kThreads * j, K4 - 1);
+            gpre[j] = reinterpret_cast<const float4*>(fz.ln_w)[k4];
+            bpre[j] = reinterpret_cast<const float4*>(fz.ln_b)[k4];
+        }
+    }
+
     // stage MT activation rows as fp32 planes: xs[m][p][c]
     float rsum[MT];
 #pragma unroll
@@ -262,7 +277,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
         float rstd[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) rstd[m] = 1.0f / sqrtf(dev[m] / (float)K + fz.ln_eps);
-        for (int t = threadIdx.x; t < MT * K4; t += blockDim.x) {
+        if (ln_pre) {
+#pragma unroll
+            for (int j = 0; j < kLnPre; ++j) {
+                const int k4 = (int)threadIdx.x + kThreads * j;
+                if (k4 >= K4) break;
+                const int c = k4 / P, p = k4 - c * P;
+                const float4 g = gpre[j], b = bpre[j];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float4 v = xs[m * K4 + p * NC + c];
+                    v.x = (v.x - mean[m]) * rstd[m] * g.x + b.x;
+                    v.y = (v.y - mean[m]) * rstd[m] * g.y + b.y;
+                    v.z = (v.z - mean[m]) * rstd[m] * g.z + b.z;
+                    v.w = (v.w - mean[m]) * rstd[m] * g.w + b.w;
+                    if (m0 + m >= M) v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    xs[m * K4 + p * NC + c] = v;
+                }
+            }
+        }
+        for (int t = ln_pre ? MT * K4 : threadIdx.x; t < MT * K4; t += blockDim.x) {
             const int m = t / K4, k4 = t - m * K4;
             const int c = k4 / P, p = k4 - c * P;
             float4 v = xs[m * K4 + p * NC + c];
@@ -378,7 +412,7 @@ __device__ __forceinline__ float4 x4_of<float>(const u32x4& u, int) {
     return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
-template <int MT, int UM, int FMT, typename TX, typename TY>
+template <int MT, int UM, int FMT, typename TX, typename TY, bool LNF>
 __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ x, int64_t ldx, int M,
                                                          const uint8_t* __restrict__ w, int64_t ldw,
                                                          const float* __restrict__ scale,
@@ -425,12 +459,64 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
             }
         }
     }
+    // LayerNorm weight and bias of the lane's columns
+    float4 gv[LNF ? UM : 1][P], bv[LNF ? UM : 1][P];
+    if constexpr (LNF) {
+#pragma unroll
+        for (int u = 0; u < UM; ++u) {
+            const int c = min(lane + 64 * u, NC - 1);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                gv[u][p] = reinterpret_cast<const float4*>(fz.ln_w + (int64_t)KC * c)[p];
+                bv[u][p] = reinterpret_cast<const float4*>(fz.ln_b + (int64_t)KC * c)[p];
+            }
+        }
+    }
     // epilogue operands, read by every lane (lane m < MT keeps row m0 + m's);
     // a residual aliasing y is read by the lane that writes the element
     const float ep_scale = (FMT == kW8 || FMT == kW4) ? scale[n] : 1.f;
     const float ep_bias = bias ? bias[n] : 0.f;
     float ep_res = 0.f;
     if (fz.res) ep_res = fz.res[(int64_t)min(m0 + min(lane, MT - 1), M - 1) * fz.ldr + n];
+
+    auto x_of = [&](int u, int m, int p) -> float4 {
+        if constexpr (sizeof(TX) == 2) return x4_of<TX>(xv[u][m][p / 2], p % 2);
+        else return x4_of<TX>(xv[u][m][p], 0);
+    };
+    // LayerNorm statistics: between them the lanes hold the whole row, so the
+    // mean and then the mean squared deviation (biased, as torch) are two
+    // wavefront sums over the lanes' own chunks
+    float mean[MT], rstd[MT];
+    if constexpr (LNF) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float t = 0.f;
+#pragma unroll
+            for (int u = 0; u < UM; ++u) {
+                float cs = 0.f;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const float4 v = x_of(u, m, p);
+                    cs += (v.x + v.y) + (v.z + v.w);
+                }
+                t += lane + 64 * u < NC ? cs : 0.f;
+            }
+            mean[m] = wave_sum_dpp(t) / (float)K;
+            float d = 0.f;
+#pragma unroll
+            for (int u = 0; u < UM; ++u) {
+                float cs = 0.f;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const float4 v = x_of(u, m, p);
+                    const float a = v.x - mean[m], b = v.y - mean[m], c = v.z - mean[m], e = v.w - mean[m];
+                    cs += (a * a + b * b) + (c * c + e * e);
+                }
+                d += lane + 64 * u < NC ? cs : 0.f;
+            }
+            rstd[m] = 1.0f / sqrtf(wave_sum_dpp(d) / (float)K + fz.ln_eps);
+        }
+    }
 
     float acc[MT];
 #pragma unroll
@@ -443,8 +529,14 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
             float4 xf[P];
 #pragma unroll
             for (int p = 0; p < P; ++p) {
-                if constexpr (sizeof(TX) == 2) xf[p] = x4_of<TX>(xv[u][m][p / 2], p % 2);
-                else xf[p] = x4_of<TX>(xv[u][m][p], 0);
+                xf[p] = x_of(u, m, p);
+                if constexpr (LNF) {
+                    const float4 g = gv[u][p], b = bv[u][p];
+                    xf[p].x = (xf[p].x - mean[m]) * rstd[m] * g.x + b.x;
+                    xf[p].y = (xf[p].y - mean[m]) * rstd[m] * g.y + b.y;
+                    xf[p].z = (xf[p].z - mean[m]) * rstd[m] * g.z + b.z;
+                    xf[p].w = (xf[p].w - mean[m]) * rstd[m] * g.w + b.w;
+                }
             }
             const float part = dot_chunk<FMT>(make_uint4(wv[u].x, wv[u].y, wv[u].z, wv[u].w), xf);
             acc[m] += own ? part : 0.f;
@@ -518,17 +610,23 @@ int run_gemv(const LinearArgs& a) {
 
 // Activation registers of the direct kernel: UM chunks x MT rows x XQ x 4
 // VGPRs, kept within 128 so that weights, activations and sums all fit.
-template <int MT, int UM, int FMT, typename TX>
+template <int MT, int UM, int FMT, typename TX, bool LNF>
 constexpr bool direct_fits() {
     constexpr int XB = Fmt<FMT>::KC * (int)sizeof(TX);
+    // with LayerNorm: fp32 activations and int8 / int4 codes only, plus the
+    // LayerNorm weight and bias of the lane's columns (2 x KC VGPRs a chunk)
+    if constexpr (LNF) {
+        if (sizeof(TX) != 4 || FMT == kF32) return false;
+        return UM * (MT * (XB / 16) * 4 + 2 * Fmt<FMT>::KC) <= 160;
+    }
     return UM * MT * (XB >= 16 ? XB / 16 : 1) * 4 <= 128;
 }
 
-template <int MT, int UM, int FMT, typename TX, typename TY>
+template <int MT, int UM, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct(const LinearArgs& a, int& rc) {
-    if constexpr (direct_fits<MT, UM, FMT, TX>()) {
+    if constexpr (direct_fits<MT, UM, FMT, TX, LNF>()) {
         const dim3 grid((unsigned)a.N, (unsigned)((a.M + MT - 1) / MT));
-        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, FMT, TX, TY>), grid, dim3(64), 0, a.stream,
+        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, FMT, TX, TY, LNF>), grid, dim3(64), 0, a.stream,
                            static_cast<const TX*>(a.x), a.ldx, (int)a.M, a.w, a.ldw, a.scale, a.bias,
                            static_cast<TY*>(a.y), a.ldy, (int)a.N, (int)a.K, a.fuse);
         rc = launch_status();
@@ -537,12 +635,24 @@ bool run_direct(const LinearArgs& a, int& rc) {
     return false;
 }
 
-template <int UM, int FMT, typename TX, typename TY>
+template <int UM, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct_mt(const LinearArgs& a, int& rc) {
-    if (a.M == 1) return run_direct<1, UM, FMT, TX, TY>(a, rc);
-    if (a.M == 2) return run_direct<2, UM, FMT, TX, TY>(a, rc);
-    return run_direct<4, UM, FMT, TX, TY>(a, rc);
+    if (a.M == 1) return run_direct<1, UM, FMT, TX, TY, LNF>(a, rc);
+    if (a.M == 2) return run_direct<2, UM, FMT, TX, TY, LNF>(a, rc);
+    return run_direct<4, UM, FMT, TX, TY, LNF>(a, rc);
 }
+
+template <int FMT, typename TX, typename TY, bool LNF>
+bool run_direct_um(const LinearArgs& a, int& rc) {
+    const int64_t um = (a.K / Fmt<FMT>::KC + 63) / 64;
+    if (um <= 1) return run_direct_mt<1, FMT, TX, TY, LNF>(a, rc);
+    if (um <= 2) return run_direct_mt<2, FMT, TX, TY, LNF>(a, rc);
+    if (um <= 4) return run_direct_mt<4, FMT, TX, TY, LNF>(a, rc);
+    if (um <= 8) return run_direct_mt<8, FMT, TX, TY, LNF>(a, rc);
+    return false;
+}
+
+constexpr int64_t kDirectLnMaxRows = 8192;
 
 // The direct kernel, when it takes the arguments (no LayerNorm, int8 / int4 /
 // fp32 weights, a row of at most 8 chunks per lane, 16-byte activation rows).
@@ -553,15 +663,17 @@ bool try_direct(const LinearArgs& a, int& rc) {
     } else {
         constexpr int KC = Fmt<FMT>::KC;
         constexpr size_t XB = KC * sizeof(TX);
-        if (a.fuse.ln_w) return false;
         const size_t xa = XB >= 16 ? 16 : XB;
         if (!aligned(a.x, xa) || ((size_t)a.ldx * sizeof(TX)) % xa != 0) return false;
-        const int64_t um = (a.K / KC + 63) / 64;
-        if (um <= 1) return run_direct_mt<1, FMT, TX, TY>(a, rc);
-        if (um <= 2) return run_direct_mt<2, FMT, TX, TY>(a, rc);
-        if (um <= 4) return run_direct_mt<4, FMT, TX, TY>(a, rc);
-        if (um <= 8) return run_direct_mt<8, FMT, TX, TY>(a, rc);
-        return false;
+        if (a.fuse.ln_w) {
+            // every wavefront reads the whole row and its LayerNorm weight and
+            // bias (12 bytes a column) from L2: worth it while a launch is
+            // latency-bound, not for a head of 50257 rows, where that traffic
+            // is twelve times the weights' and the LDS-staged kernel shares it
+            if (a.N > kDirectLnMaxRows || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16)) return false;
+            return run_direct_um<FMT, TX, TY, true>(a, rc);
+        }
+        return run_direct_um<FMT, TX, TY, false>(a, rc);
     }
 }
 
