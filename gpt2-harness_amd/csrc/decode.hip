@@ -110,8 +110,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
                 s = fmaf(qs[qd + 4 * q + 3], k4[q].w, s);
             }
         }
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
+        s += dpp_move<0xB1>(s);  // quad_perm [1, 0, 3, 2]: the lane xor 1
+        s += dpp_move<0x4E>(s);  // quad_perm [2, 3, 0, 1]: the lane xor 2
         if ((lane & 3) == 0 && t <= pos) sc[t] = s * inv_div;
     }
     __syncthreads();
@@ -119,8 +119,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     // ---- softmax over slots 0..pos ----
     float mx = -INFINITY;
     for (int64_t t = tid; t <= pos; t += 256) mx = fmaxf(mx, sc[t]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max_dpp(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -131,7 +130,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
         sc[t] = p;
         sum += p;
     }
-    sum = wave_sum(sum);
+    sum = wave_sum_dpp(sum);
     if (lane == 0) red[wave] = sum;
     __syncthreads();
     sum = (red[0] + red[1]) + (red[2] + red[3]);

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__
             const float4 v = *reinterpret_cast<const float4*>(xr + k);
             s += (v.x + v.y) + (v.z + v.w);
         }
-        s = wave_sum(s);
+        s = wave_sum_dpp(s);
         if ((tid & 63) == 0) part[tid >> 6] = s;
         __syncthreads();
         mu = ((part[0] + part[1]) + (part[2] + part[3])) / (float)K;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__
             const float a = v.x - mu, b = v.y - mu, c = v.z - mu, e = v.w - mu;
             d += (a * a + b * b) + (c * c + e * e);
         }
-        d = wave_sum(d);
+        d = wave_sum_dpp(d);
         if ((tid & 63) == 0) part[tid >> 6] = d;
         __syncthreads();
         rs = 1.0f / sqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)K + ln_eps);

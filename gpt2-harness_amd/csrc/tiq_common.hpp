@@ -53,10 +53,12 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// x moved across lanes by DPP control CTRL; lanes of rows outside ROW_MASK get 0.
+// x moved across lanes by DPP control CTRL; lanes of rows outside ROW_MASK
+// get `keep` (0 by default).
 template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ float dpp_move(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+__device__ __forceinline__ float dpp_move(float x, float keep = 0.f) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(keep), __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
 }
 
 // Sum over the 64 lanes of a wavefront with DPP lane moves (VALU operations,
@@ -71,6 +73,18 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += dpp_move<0x140>(v);       // row_mirror
     v += dpp_move<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
     v += dpp_move<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Maximum over the 64 lanes, the same moves as wave_sum_dpp (lanes outside a
+// broadcast's rows keep their own value). All 64 lanes must be active.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    v = fmaxf(v, dpp_move<0x142, 0xa>(v, v));
+    v = fmaxf(v, dpp_move<0x143, 0xc>(v, v));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
