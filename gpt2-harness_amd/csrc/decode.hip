@@ -26,15 +26,33 @@ constexpr int kMaxSlots = 1024;  // n_positions of GPT-2
 // waits for HBM once; longer histories stream the rest in a second pass.
 constexpr int kPreKeys = 128;  // slots whose key rows / values are prefetched
 
+// Columns k .. k + 7 of activation row m as the exact three bf16 planes, in
+// the operand order of the batched decode linear for K = Kc columns: for row
+// tile t = m / 32, unit u = k / 32, plane q and half e = (k / 8) % 2, a 1 KB
+// block holds the 16 bytes of lane 32 ((k / 16) % 2) + m % 32.
+__device__ __forceinline__ void store_planes(uint16_t* x3, int64_t m, int64_t Kc, int64_t k, const float (&v)[8]) {
+    uint32_t pl[3][4];
+    split3_words(v, pl);
+    const int64_t U = Kc / 32, t = m >> 5, u = k >> 5;
+    const int r = (int)(m & 31), hh = (int)((k >> 4) & 1), e = (int)((k >> 3) & 1);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const int64_t blk = ((t * U + u) * 3 + q) * 2 + e;
+        *reinterpret_cast<uint4*>(x3 + (blk * 64 + 32 * hh + r) * 8) = make_uint4(pl[q][0], pl[q][1], pl[q][2], pl[q][3]);
+    }
+}
+
 __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __restrict__ qkv, int64_t ld_qkv, int H,
                                                                int Hkv, float* __restrict__ kc,
                                                                float* __restrict__ vc, int64_t t_max,
                                                                const int64_t* __restrict__ pos_p,
-                                                               float* __restrict__ y, int64_t ldy) {
+                                                               float* __restrict__ y, int64_t ldy,
+                                                               uint16_t* __restrict__ x3) {
     __shared__ float qs[kHeadDim], kn[kHeadDim], vn[kHeadDim];
     __shared__ float sc[kMaxSlots];
     __shared__ float red[4];
     __shared__ float part[4][kHeadDim];
+    __shared__ float ov[kHeadDim];
     const int b = blockIdx.x / H, h = blockIdx.x % H;
     const int group = H / Hkv, hk = h / group;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -71,6 +89,12 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     const int64_t pos = *pos_p;
     if (pos < 0 || pos >= t_max) {  // position outside the cache: flag the output, write nothing else
         if (tid < kHeadDim) y[(int64_t)b * ldy + h * kHeadDim + tid] = NAN;
+        if (x3 && tid < kHeadDim / 8) {
+            float nan8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nan8[i] = NAN;
+            store_planes(x3, b, H * kHeadDim, h * kHeadDim + 8 * tid, nan8);
+        }
         return;
     }
     if (tid < kHeadDim) {
@@ -86,33 +110,45 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
 
     // ---- scores ----
     const float inv_div = 1.0f / sqrtf((float)kHeadDim);  // exactly 1/8
-    for (int64_t t0 = 0; t0 <= pos; t0 += 64) {
-        const int64_t t = t0 + kslot;
-        const int j = (int)(t0 >> 6);
-        float s = 0.f;
-        if (t == pos) {
+    // chunks of kPreKeys slots, this thread's two 64-slot rows each: the first
+    // chunk's keys were loaded at the start, a later chunk's are all requested
+    // before any is used (one trip to memory per chunk, slots clamped into the
+    // cache; only slots < pos count, slot pos is the new key)
+    for (int64_t base = 0; base <= pos; base += kPreKeys) {
+        float4 kk[2][4];
+        if (base == 0) {
 #pragma unroll
-            for (int d = 0; d < 16; ++d) s = fmaf(qs[qd + d], kn[qd + d], s);
-        } else if (t < pos) {
-            float4 k4[4];
-            if (j < 2) {
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) k4[q] = (j == 0) ? kr[0][q] : kr[1][q];
-            } else {
+                for (int q = 0; q < 4; ++q) kk[j][q] = kr[j][q];
+        } else {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) k4[q] = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q];
-            }
+            for (int j = 0; j < 2; ++j) {
+                const int64_t t = min(base + kslot + 64 * j, last);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                s = fmaf(qs[qd + 4 * q], k4[q].x, s);
-                s = fmaf(qs[qd + 4 * q + 1], k4[q].y, s);
-                s = fmaf(qs[qd + 4 * q + 2], k4[q].z, s);
-                s = fmaf(qs[qd + 4 * q + 3], k4[q].w, s);
+                for (int q = 0; q < 4; ++q) kk[j][q] = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q];
             }
         }
-        s += dpp_move<0xB1>(s);  // quad_perm [1, 0, 3, 2]: the lane xor 1
-        s += dpp_move<0x4E>(s);  // quad_perm [2, 3, 0, 1]: the lane xor 2
-        if ((lane & 3) == 0 && t <= pos) sc[t] = s * inv_div;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t t = base + kslot + 64 * j;
+            float s = 0.f;
+            if (t == pos) {
+#pragma unroll
+                for (int d = 0; d < 16; ++d) s = fmaf(qs[qd + d], kn[qd + d], s);
+            } else if (t < pos) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    s = fmaf(qs[qd + 4 * q], kk[j][q].x, s);
+                    s = fmaf(qs[qd + 4 * q + 1], kk[j][q].y, s);
+                    s = fmaf(qs[qd + 4 * q + 2], kk[j][q].z, s);
+                    s = fmaf(qs[qd + 4 * q + 3], kk[j][q].w, s);
+                }
+            }
+            s += dpp_move<0xB1>(s);  // quad_perm [1, 0, 3, 2]: the lane xor 1
+            s += dpp_move<0x4E>(s);  // quad_perm [2, 3, 0, 1]: the lane xor 2
+            if ((lane & 3) == 0 && t <= pos) sc[t] = s * inv_div;
+        }
     }
     __syncthreads();
 
@@ -136,19 +172,40 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     sum = (red[0] + red[1]) + (red[2] + red[3]);
 
     // ---- weighted sum of values: wavefront w takes slots t = w mod 4, lane = dim ----
+    // (in chunks of kPreKeys slots as the scores: the first prefetched, a
+    // later chunk's values all requested before any is used)
     float acc = 0.f;
+    for (int64_t base = 0; base < pos; base += kPreKeys) {
+        float vv[kPreKeys / 4];
+        if (base == 0) {
 #pragma unroll
-    for (int i = 0; i < kPreKeys / 4; ++i) {
-        const int64_t t = wave + 4 * i;
-        if (t < pos) acc = fmaf(sc[t], vr[i], acc);
+            for (int i = 0; i < kPreKeys / 4; ++i) vv[i] = vr[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPreKeys / 4; ++i) vv[i] = vb[min(base + wave + 4 * i, last) * kHeadDim + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < kPreKeys / 4; ++i) {
+            const int64_t t = base + wave + 4 * i;
+            if (t < pos) acc = fmaf(sc[t], vv[i], acc);
+        }
     }
-    for (int64_t t = wave + kPreKeys; t < pos; t += 4) acc = fmaf(sc[t], vb[t * kHeadDim + lane], acc);
     if ((pos & 3) == wave) acc = fmaf(sc[pos], vn[lane], acc);
     part[wave][lane] = acc;
     __syncthreads();
     if (tid < kHeadDim) {
         const float o = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
         y[(int64_t)b * ldy + h * kHeadDim + tid] = o / sum;
+        ov[tid] = o / sum;
+    }
+    if (x3) {  // the head's 64 outputs as the operand planes of the output projection
+        __syncthreads();
+        if (tid < kHeadDim / 8) {
+            float o8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o8[i] = ov[8 * tid + i];
+            store_planes(x3, b, H * kHeadDim, h * kHeadDim + 8 * tid, o8);
+        }
     }
 }
 
@@ -235,18 +292,34 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 
 using namespace tiq;
 
-extern "C" int tiq_decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head,
-                                    int64_t n_kv_head, int64_t head_dim, float* k_cache, float* v_cache,
-                                    int64_t t_max, const int64_t* pos, float* y, int64_t ldy, void* stream) {
+static int decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head, int64_t n_kv_head,
+                            int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
+                            float* y, int64_t ldy, uint16_t* planes_out, void* stream) {
     if (batch < 0 || n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head) return TIQ_EINVAL;
     if (batch == 0) return TIQ_OK;
     if (!qkv || !k_cache || !v_cache || !pos || !y) return TIQ_EINVAL;
     if (head_dim != kHeadDim || t_max <= 0 || t_max > kMaxSlots) return TIQ_EUNSUPPORTED;
     if (ld_qkv < (n_head + 2 * n_kv_head) * head_dim || ldy < n_head * head_dim) return TIQ_EINVAL;
-    if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return TIQ_EALIGN;
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || (planes_out && !aligned(planes_out, 16))) return TIQ_EALIGN;
     hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)(batch * n_head)), dim3(256), 0, as_stream(stream), qkv,
-                       ld_qkv, (int)n_head, (int)n_kv_head, k_cache, v_cache, t_max, pos, y, ldy);
+                       ld_qkv, (int)n_head, (int)n_kv_head, k_cache, v_cache, t_max, pos, y, ldy, planes_out);
     return launch_status();
+}
+
+extern "C" int tiq_decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head,
+                                    int64_t n_kv_head, int64_t head_dim, float* k_cache, float* v_cache,
+                                    int64_t t_max, const int64_t* pos, float* y, int64_t ldy, void* stream) {
+    return decode_attention(qkv, ld_qkv, batch, n_head, n_kv_head, head_dim, k_cache, v_cache, t_max, pos, y, ldy,
+                            nullptr, stream);
+}
+
+extern "C" int tiq_decode_attention_planes(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head,
+                                           int64_t n_kv_head, int64_t head_dim, float* k_cache, float* v_cache,
+                                           int64_t t_max, const int64_t* pos, float* y, int64_t ldy,
+                                           uint16_t* planes_out, void* stream) {
+    if (!planes_out) return TIQ_EINVAL;
+    return decode_attention(qkv, ld_qkv, batch, n_head, n_kv_head, head_dim, k_cache, v_cache, t_max, pos, y, ldy,
+                            planes_out, stream);
 }
 
 extern "C" int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte, int64_t vocab,

@@ -85,6 +85,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     constexpr int PASSES = (BM * BN * (int)sizeof(TY) + 2 * STAGE - 1) / (2 * STAGE);
     static_assert(PASSES == 1 || PASSES == 2, "output tile passes");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) float sb_s[2][BN];  // the tile's scale and bias
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
@@ -157,6 +158,14 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     for (int q = 0; q < NL; ++q) gload(0, 0, q);
 #pragma unroll
     for (int q = 0; q < NL; ++q) gload(min(1, nk - 1) * BK, 1, q);
+    // the epilogue's per-column scale and bias, read once here, behind the
+    // first tiles' loads (after the last k step they would cost another trip
+    // to memory); columns past N repeat the last one
+    for (int c = tid; c < BN; c += NT) {
+        const int n = min(n_blk + c, N - 1);
+        sb_s[0][c] = scale[n];
+        sb_s[1][c] = bias ? bias[n] : 0.f;
+    }
 #pragma unroll
     for (int q = 0; q < NL; ++q) lstore(smem, 0, q);
     __syncthreads();
@@ -216,10 +225,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int nl = wn + 32 * i + 8 * g + 4 * h;  // 4 consecutive outputs
-                    const int n0 = n_blk + nl < N ? n_blk + nl : N - 4;
-                    const float4 sc = *reinterpret_cast<const float4*>(scale + n0);
-                    float4 bi = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (bias) bi = *reinterpret_cast<const float4*>(bias + n0);
+                    const float4 sc = *reinterpret_cast<const float4*>(&sb_s[0][nl]);
+                    const float4 bi = *reinterpret_cast<const float4*>(&sb_s[1][nl]);
 #pragma unroll
                     for (int j = 0; j < TMm; ++j) {
                         const int ml = wm + 32 * j + r - pass * ROWS;
@@ -249,7 +256,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
             const int ml = idx / UNITS, u = idx % UNITS;
             const int m = m_blk + pass * ROWS + ml, n = n_blk + u * UNIT;
             const u32x4 v = *reinterpret_cast<const u32x4*>(smem + ml * ROW_BYTES + ((u ^ (ml & (UNITS - 1))) * 16));
-            if (m < M && n < N) *reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n) = v;
+            // nontemporal: the output is written once and read by a later kernel
+            if (m < M && n < N) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n));
         }
         if (pass + 1 < PASSES) __syncthreads();
     }

@@ -244,3 +244,45 @@ extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, 
     return run_linear(make_args(x, x_dtype, M, K, ldx, packed, (K + 1) / 2, nullptr, scale_f16, group, bias, N, y,
                                 y_dtype, ldy, stream, kW4G));
 }
+
+extern "C" size_t tiq_decode_linear_workspace(int w_format, int64_t M, int64_t K, int64_t N) {
+    if ((w_format != TIQ_WF_INT8 && w_format != TIQ_WF_F32) || M < kSkinnyMinRows || M > 64 || K <= 0 ||
+        K % 32 != 0 || N <= 0)
+        return 0;
+    return decode_linear_workspace(M, K, N);
+}
+
+extern "C" size_t tiq_decode_planes_bytes(int64_t M, int64_t K) {
+    if (M <= 0 || K <= 0 || K % 32 != 0) return 0;
+    return decode_planes_bytes(M, K);
+}
+
+extern "C" int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M, int64_t K,
+                                 const void* w, int w_format, const float* scale, const float* bias, int64_t N,
+                                 float* y, int64_t ldy, const float* ln_weight, const float* ln_bias, float ln_eps,
+                                 int activation, const float* residual, int64_t ld_residual,
+                                 const float* next_ln_weight, const float* next_ln_bias, float next_ln_eps,
+                                 uint16_t* planes_out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_F32) return TIQ_EUNSUPPORTED;
+    if (activation != TIQ_ACT_NONE && activation != TIQ_ACT_GELU_TANH) return TIQ_EINVAL;
+    if ((ln_weight == nullptr) != (ln_bias == nullptr)) return TIQ_EINVAL;
+    if (M < 0 || K < 0 || N < 0) return TIQ_EINVAL;
+    if (M == 0 || N == 0) return TIQ_OK;
+    if (!w || (w_format == TIQ_WF_INT8 && !scale)) return TIQ_EINVAL;
+    if (x_planes && ln_weight) return TIQ_EINVAL;  // planes already carry their LayerNorm
+    if (!x_planes && (!x || ldx < K)) return TIQ_EINVAL;
+    if (y && ldy < N) return TIQ_EINVAL;
+    if (residual && (!y || ld_residual < N)) return TIQ_EINVAL;
+    const WFormat fmt = (WFormat)w_format;
+    LinearArgs a = make_args(x, TIQ_F32, M, K, ldx, static_cast<const uint8_t*>(w), fmt == kW8 ? K : 4 * K, scale,
+                             nullptr, 0, bias, N, y, TIQ_F32, ldy, stream, fmt);
+    a.fuse.ln_w = ln_weight;
+    a.fuse.ln_b = ln_bias;
+    a.fuse.ln_eps = ln_eps;
+    a.fuse.act = activation;
+    a.fuse.res = residual;
+    a.fuse.ldr = ld_residual;
+    a.ws = workspace;
+    a.ws_bytes = workspace_bytes;
+    return run_decode_linear(a, x_planes, next_ln_weight, next_ln_bias, next_ln_eps, planes_out);
+}

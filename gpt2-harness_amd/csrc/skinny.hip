@@ -22,6 +22,8 @@
 //   * LayerNorm statistics (two-pass mean and biased variance, as torch) are
 //     computed over the workgroup's activation rows, which needs K covered by
 //     one workgroup (at most 2048 with 8 wavefronts of 8 units).
+#include <algorithm>
+
 #include "tiq_internal.hpp"
 
 namespace tiq {
@@ -47,12 +49,6 @@ constexpr int ring_units() { return WF == kW8 ? 4 : 3; }
 constexpr int kPlUnits = 7;
 constexpr int kLnMaxK = kWaves * 8 * 32;
 
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-    const bf16x2 v = __builtin_convertvector(floatx2{a, b}, bf16x2);
-    return __builtin_bit_cast(uint32_t, v);
-}
-__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
 // 8 fp32 values -> three bf16x8 planes with hi + lo + lo2 == v.
 __device__ __forceinline__ void split3(const float (&v)[8], bf16x8& p0, bf16x8& p1, bf16x8& p2) {
@@ -156,6 +152,140 @@ __global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__
     }
 }
 
+// The end of a split-K decode linear, one workgroup of 1024 threads per
+// activation row m, thread t owning the 8 consecutive columns 8 t .. 8 t + 7:
+// the S partial rows (row m of slice s at part + (s M + m) ldp) are summed in
+// a fixed order (the result does not depend on timing), then scale, bias,
+// GELU(tanh) and the residual (which may alias y: every element is read and
+// written by one thread) give the output row, stored to y when y is given.
+// With PLANES the row is also written as the next linear's operand planes
+// (ln_split_kernel's layout, K' = N), after LayerNorm when LN. With S = 1,
+// no epilogue and part = fp32 rows, the kernel is a LayerNorm + split pass.
+// Every load is issued before any is used and none sits behind a branch
+// (the optional operands are compile-time flags).
+constexpr int kRedThreads = 1024;
+constexpr int kRedMaxCols = kRedThreads * 8;
+template <bool LN, bool PLANES, bool SC, bool BI, bool RS>
+__global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* __restrict__ part, int64_t ldp,
+                                                                  int S, int M, int N,
+                                                                  const float* __restrict__ scale,
+                                                                  const float* __restrict__ bias, int act,
+                                                                  const float* res, int64_t ldr, float* y,
+                                                                  int64_t ldy, const float* __restrict__ ln_w,
+                                                                  const float* __restrict__ ln_b, float ln_eps,
+                                                                  uint16_t* __restrict__ x3) {
+    __shared__ float red[kRedThreads / 64];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const int NC8 = N / 8;
+    const bool own = tid < NC8;
+    const int n = 8 * min(tid, NC8 - 1);  // a thread past the row repeats its last chunk, unused
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int si = 0; si < S; ++si) {
+        const float* pr = part + ((int64_t)si * M + m) * ldp + n;
+        const float4 p0 = reinterpret_cast<const float4*>(pr)[0], p1 = reinterpret_cast<const float4*>(pr)[1];
+        a[0] += p0.x; a[1] += p0.y; a[2] += p0.z; a[3] += p0.w;
+        a[4] += p1.x; a[5] += p1.y; a[6] += p1.z; a[7] += p1.w;
+    }
+    float4 sc[2], bi[2], rs[2], gw[2], gb[2];
+    if constexpr (SC) sc[0] = reinterpret_cast<const float4*>(scale + n)[0], sc[1] = reinterpret_cast<const float4*>(scale + n)[1];
+    if constexpr (BI) bi[0] = reinterpret_cast<const float4*>(bias + n)[0], bi[1] = reinterpret_cast<const float4*>(bias + n)[1];
+    if constexpr (RS) {
+        rs[0] = reinterpret_cast<const float4*>(res + (int64_t)m * ldr + n)[0];
+        rs[1] = reinterpret_cast<const float4*>(res + (int64_t)m * ldr + n)[1];
+    }
+    if constexpr (LN) gw[0] = reinterpret_cast<const float4*>(ln_w + n)[0], gw[1] = reinterpret_cast<const float4*>(ln_w + n)[1];
+    if constexpr (LN) gb[0] = reinterpret_cast<const float4*>(ln_b + n)[0], gb[1] = reinterpret_cast<const float4*>(ln_b + n)[1];
+    auto lane8 = [](const float4 (&f)[2], int i) { const float4 q = f[i >> 2]; return (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w; };
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float t = a[i];
+        if constexpr (SC) t *= lane8(sc, i);
+        if constexpr (BI) t += lane8(bi, i);
+        if (act == 1) t = gelu_tanh_f(t);
+        if constexpr (RS) t += lane8(rs, i);
+        v[i] = t;
+    }
+    if (y && own) {
+        float* yr = y + (int64_t)m * ldy + n;
+        reinterpret_cast<float4*>(yr)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(yr)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if constexpr (!PLANES) return;
+    float mu = 0.f, rstd = 1.f;
+    if constexpr (LN) {  // two-pass mean and biased variance over the row, as torch
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += v[i];
+        sum = wave_sum_dpp(own ? sum : 0.f);
+        if ((tid & 63) == 0) red[tid >> 6] = sum;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRedThreads / 64; ++w) tot += red[w];
+        mu = tot / (float)N;
+        __syncthreads();
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d += (v[i] - mu) * (v[i] - mu);
+        d = wave_sum_dpp(own ? d : 0.f);
+        if ((tid & 63) == 0) red[tid >> 6] = d;
+        __syncthreads();
+        tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRedThreads / 64; ++w) tot += red[w];
+        rstd = 1.0f / sqrtf(tot / (float)N + ln_eps);
+    }
+    if (!own) return;
+    const int U = N / 32, t = m >> 5, r = m & 31;
+    const int u = n >> 5, h = (n >> 4) & 1, e = (n >> 3) & 1;
+    float x8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if constexpr (LN) x8[i] = (v[i] - mu) * rstd * lane8(gw, i) + lane8(gb, i);
+        else x8[i] = v[i];
+    }
+    u32x4 pl[3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x0 = x8[2 * i], x1 = x8[2 * i + 1];
+        const uint32_t hh = pk_bf16(x0, x1);
+        const float r0 = x0 - bf_lo(hh), r1 = x1 - bf_hi(hh);
+        const uint32_t l = pk_bf16(r0, r1);
+        pl[0][i] = hh;
+        pl[1][i] = l;
+        pl[2][i] = pk_bf16(r0 - bf_lo(l), r1 - bf_hi(l));
+    }
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const int64_t blk = (((int64_t)t * U + u) * 3 + q) * 2 + e;
+        *reinterpret_cast<u32x4*>(x3 + (blk * 64 + 32 * h + r) * 8) = pl[q];
+    }
+}
+
+// The reduction kernel instance for these operands.
+using ReduceFn = void (*)(const float*, int64_t, int, int, int, const float*, const float*, int, const float*,
+                          int64_t, float*, int64_t, const float*, const float*, float, uint16_t*);
+template <bool LN, bool PLANES>
+ReduceFn reduce_fn(bool sc, bool bi, bool rs) {
+    const int k = (sc ? 4 : 0) | (bi ? 2 : 0) | (rs ? 1 : 0);
+    switch (k) {
+        case 0: return reduce_rows_kernel<LN, PLANES, false, false, false>;
+        case 1: return reduce_rows_kernel<LN, PLANES, false, false, true>;
+        case 2: return reduce_rows_kernel<LN, PLANES, false, true, false>;
+        case 3: return reduce_rows_kernel<LN, PLANES, false, true, true>;
+        case 4: return reduce_rows_kernel<LN, PLANES, true, false, false>;
+        case 5: return reduce_rows_kernel<LN, PLANES, true, false, true>;
+        case 6: return reduce_rows_kernel<LN, PLANES, true, true, false>;
+        default: return reduce_rows_kernel<LN, PLANES, true, true, true>;
+    }
+}
+
+ReduceFn pick_reduce(bool ln, bool planes, bool sc, bool bi, bool rs) {
+    if (!planes) return reduce_fn<false, false>(sc, bi, rs);
+    return ln ? reduce_fn<true, true>(sc, bi, rs) : reduce_fn<false, true>(sc, bi, rs);
+}
+
 // WF: kW8 (int8 codes, per-row scale) or kF32 (fp32 weights, no scale).
 // XM: how the activations arrive.
 //   kXRows   fp32 rows, LayerNorm'd (optionally) and split here;
@@ -173,7 +303,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int K, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, int N, TY* __restrict__ y, int64_t ldy,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps, int act,
-    const float* __restrict__ res, int64_t ldr) {
+    const float* __restrict__ res, int64_t ldr, float* __restrict__ part) {
     constexpr int WB = (WF == kW8) ? 16 : 64;  // weight bytes a lane loads per unit
     constexpr bool PL = XM == kXPlanes;
     constexpr int kXp = ring_units<WF>();
@@ -186,7 +316,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const int r = lane & 31, h = lane >> 5;
     const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
     const int U = K / 32;
-    const int u0 = wave * U / kWaves, u1 = (wave + 1) * U / kWaves;
+    // split-K: workgroup z takes units [z U / S, (z + 1) U / S) of the row,
+    // shared out over its wavefronts (S = 1: the whole row)
+    const int ub = blockIdx.z * U / gridDim.z, Us = (blockIdx.z + 1) * U / gridDim.z - ub;
+    const int u0 = ub + wave * Us / kWaves, u1 = ub + (wave + 1) * Us / kWaves;
     const bool xrow_ok = m0 + r < M;
     const float* xr = x + (int64_t)(xrow_ok ? m0 + r : 0) * ldx + 16 * h;  // + 32 u
     const uint16_t* xbr = reinterpret_cast<const uint16_t*>(x) + (int64_t)(xrow_ok ? m0 + r : 0) * ldx + 16 * h;
@@ -464,6 +597,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
         const int m = o >> 5, nn = o & 31;
         const int gm = m0 + m, gn = n0 + nn;
         float v = vsum[t];
+        if (part) {  // split-K: the raw partial sum; the epilogue runs after the reduction
+            if (gm < M && gn < N) part[((int64_t)blockIdx.z * M + gm) * N + gn] = v;
+            continue;
+        }
         if (gm < M && gn < N) {
             if (WF == kW8) v *= ep_scale;
             if (bias) v += ep_bias;
@@ -497,7 +634,7 @@ int run_skinny(const LinearArgs& a) {
         hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                            reinterpret_cast<const float*>(x3), (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
                            a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
-                           a.fuse.res, a.fuse.ldr);
+                           a.fuse.res, a.fuse.ldr, nullptr);
         return launch_status();
     }
     if constexpr (WF == kW8) {
@@ -505,20 +642,129 @@ int run_skinny(const LinearArgs& a) {
             hipLaunchKernelGGL((skinny_kernel<kW8, kXBf16, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                                static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
                                a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
-                               a.fuse.res, a.fuse.ldr);
+                               a.fuse.res, a.fuse.ldr, nullptr);
             return launch_status();
         }
     }
     hipLaunchKernelGGL((skinny_kernel<WF, kXRows, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                        static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias,
                        (int)a.N, static_cast<TY*>(a.y), a.ldy, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, a.fuse.act,
-                       a.fuse.res, a.fuse.ldr);
+                       a.fuse.res, a.fuse.ldr, nullptr);
+    return launch_status();
+}
+
+// Splits of a batched decode linear's K range: about 512 workgroups in all,
+// at least one 32-column unit per wavefront of a split.
+int64_t decode_splits(int64_t M, int64_t K, int64_t N) {
+    // about six 32-column units per wavefront: a split pays for its partial
+    // sums and the reduction only on long rows (6400 columns: four splits)
+    (void)M;
+    (void)N;
+    int64_t S = (K / 32) / (kWaves * 6);
+    // TIQ_DECODE_SPLITS (read on every call, far cheaper than a launch) fixes
+    // the count, so that one process can measure each
+    if (const char* e = getenv("TIQ_DECODE_SPLITS")) S = std::max(1, atoi(e));
+    S = std::min<int64_t>(S, (K / 32) / kWaves);
+    return std::max<int64_t>(1, std::min<int64_t>(S, 32));
+}
+
+size_t partials_bytes(int64_t M, int64_t K, int64_t N) {
+    return round256((size_t)(decode_splits(M, K, N) * M * N) * 4);
+}
+
+template <int WF>
+int run_decode_t(const LinearArgs& a, const uint16_t* x3, const float* next_ln_w, const float* next_ln_b,
+                 float next_eps, uint16_t* planes_out, float* part, int64_t S) {
+    const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 31) / 32), (unsigned)S);
+    const float* xp = reinterpret_cast<const float*>(x3);
+    if (!part) {  // one split and no planes: the product kernel's own epilogue writes y
+        hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, float>), grid, dim3(kWaves * 64), 0, a.stream, xp,
+                           (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N,
+                           static_cast<float*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act, a.fuse.res,
+                           a.fuse.ldr, nullptr);
+        return launch_status();
+    }
+    hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, float>), grid, dim3(kWaves * 64), 0, a.stream, xp, (int64_t)0,
+                       (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N, static_cast<float*>(nullptr),
+                       (int64_t)0, nullptr, nullptr, 0.f, 0, nullptr, (int64_t)0, part);
+    int rc = launch_status();
+    if (rc != TIQ_OK) return rc;
+    const float* sc = WF == kW8 ? a.scale : nullptr;
+    ReduceFn red = pick_reduce(next_ln_w != nullptr, planes_out != nullptr, sc != nullptr, a.bias != nullptr,
+                               a.fuse.res != nullptr);
+    hipLaunchKernelGGL(red, dim3((unsigned)a.M), dim3(kRedThreads), 0, a.stream, part, (int64_t)a.N, (int)S,
+                       (int)a.M, (int)a.N, sc, a.bias, a.fuse.act, a.fuse.res, a.fuse.ldr, static_cast<float*>(a.y),
+                       a.ldy, next_ln_w, next_ln_b, next_eps, planes_out);
     return launch_status();
 }
 
 }  // namespace
 
 size_t skinny_workspace(int64_t M, int64_t K) { return planes_bytes(M, K); }
+
+size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N) {
+    return planes_bytes(M, K) + partials_bytes(M, K, N);
+}
+
+size_t decode_planes_bytes(int64_t M, int64_t K) { return planes_bytes(M, K); }
+
+int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float* next_ln_w,
+                      const float* next_ln_b, float next_eps, uint16_t* planes_out) {
+    if (a.fmt != kW8 && a.fmt != kF32) return TIQ_EUNSUPPORTED;
+    if (a.M < kSkinnyMinRows || a.M > 64 || a.K <= 0 || a.K % 32 != 0 || a.N <= 0 || a.N > 0x7fffffff)
+        return TIQ_EUNSUPPORTED;
+    if ((next_ln_w == nullptr) != (next_ln_b == nullptr) || (next_ln_w && !planes_out)) return TIQ_EINVAL;
+    if (!a.y && !planes_out) return TIQ_EINVAL;
+    // a row the reduction cannot take (N % 8, N > 8192) without planes out:
+    // one split, the product kernel's own epilogue
+    const bool red_ok = a.N % 8 == 0 && a.N <= kRedMaxCols;
+    const int64_t S = (red_ok || planes_out) ? decode_splits(a.M, a.K, a.N) : 1;
+    const bool reduce = S > 1 || planes_out;
+    // every wavefront's share of K fits its weight registers
+    const int64_t units = ((a.K / 32 + S - 1) / S + kWaves - 1) / kWaves;
+    if (units > (a.fmt == kW8 ? max_units<kW8>() : max_units<kF32>())) return TIQ_EUNSUPPORTED;
+    if (!aligned(a.w, 16) || a.ldw % 16 != 0) return TIQ_EALIGN;
+    if (x_planes ? !aligned(x_planes, 16)
+                 : (!a.x || !aligned(a.x, 16) || a.ldx % 4 != 0 ||
+                    (a.fuse.ln_w && (!aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16)))))
+        return x_planes || a.x ? TIQ_EALIGN : TIQ_EINVAL;
+    if (reduce) {  // the reduction's 16-byte row accesses and its 8192-column reach
+        if (a.N % 8 != 0 || a.N > kRedMaxCols) return TIQ_EUNSUPPORTED;
+        if ((a.y && (!aligned(a.y, 16) || a.ldy % 4 != 0)) ||
+            (a.fuse.res && (!aligned(a.fuse.res, 16) || a.fuse.ldr % 4 != 0)))
+            return TIQ_EALIGN;
+        if ((a.fmt == kW8 && !aligned(a.scale, 16)) || (a.bias && !aligned(a.bias, 16))) return TIQ_EALIGN;
+        if (planes_out && (!aligned(planes_out, 16) || a.N % 32 != 0)) return TIQ_EUNSUPPORTED;
+    }
+    if (a.fuse.res && a.fuse.res != a.y && a.fuse.ldr < a.N) return TIQ_EINVAL;
+    const size_t need = (x_planes ? 0 : planes_bytes(a.M, a.K)) + (reduce ? partials_bytes(a.M, a.K, a.N) : 0);
+    if (need && (!a.ws || a.ws_bytes < need || !aligned(a.ws, 16))) return TIQ_EWORKSPACE;
+    uint8_t* ws = static_cast<uint8_t*>(a.ws);
+    const uint16_t* x3 = x_planes;
+    if (!x3) {
+        uint16_t* xs = reinterpret_cast<uint16_t*>(ws);
+        if (a.K <= kRedMaxCols) {  // LayerNorm + split: the reduction kernel with one slice, no epilogue
+            ReduceFn f = pick_reduce(a.fuse.ln_w != nullptr, true, false, false, false);
+            hipLaunchKernelGGL(f, dim3((unsigned)a.M), dim3(kRedThreads), 0, a.stream,
+                               static_cast<const float*>(a.x), a.ldx, 1, (int)a.M, (int)a.K, nullptr, nullptr, 0,
+                               nullptr, (int64_t)0, nullptr, (int64_t)0, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, xs);
+        } else if (a.fuse.ln_w) {
+            hipLaunchKernelGGL(ln_split_kernel<true>, dim3((unsigned)a.M), dim3(256), 0, a.stream,
+                               static_cast<const float*>(a.x), a.ldx, (int)a.K, a.fuse.ln_w, a.fuse.ln_b,
+                               a.fuse.ln_eps, xs);
+        } else {
+            hipLaunchKernelGGL(ln_split_kernel<false>, dim3((unsigned)a.M), dim3(256), 0, a.stream,
+                               static_cast<const float*>(a.x), a.ldx, (int)a.K, nullptr, nullptr, 0.f, xs);
+        }
+        int rc = launch_status();
+        if (rc != TIQ_OK) return rc;
+        x3 = xs;
+        ws += planes_bytes(a.M, a.K);
+    }
+    float* part = reduce ? reinterpret_cast<float*>(ws) : nullptr;
+    if (a.fmt == kW8) return run_decode_t<kW8>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, S);
+    return run_decode_t<kF32>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, S);
+}
 
 bool skinny_supported(const LinearArgs& a) {
     if (a.fmt != kW8 && a.fmt != kF32) return false;

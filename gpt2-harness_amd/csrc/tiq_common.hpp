@@ -124,6 +124,31 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// bf16 packing for the exact three-plane split of fp32 activations:
+// x = hi + lo + lo2 with hi = bf16(x), lo = bf16(x - hi), lo2 = bf16(x - hi - lo)
+// (round to nearest even; the residues are exact in fp32).
+typedef __bf16 tiq_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float tiq_floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    const tiq_bf16x2 v = __builtin_convertvector(tiq_floatx2{a, b}, tiq_bf16x2);
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+// The three planes of 8 consecutive values, each as 4 packed bf16 pairs.
+__device__ __forceinline__ void split3_words(const float (&x)[8], uint32_t (&pl)[3][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x0 = x[2 * i], x1 = x[2 * i + 1];
+        const uint32_t h = pk_bf16(x0, x1);
+        const float r0 = x0 - bf_lo(h), r1 = x1 - bf_hi(h);
+        const uint32_t l = pk_bf16(r0, r1);
+        pl[0][i] = h;
+        pl[1][i] = l;
+        pl[2][i] = pk_bf16(r0 - bf_lo(l), r1 - bf_hi(l));
+    }
+}
+
 // Sign-extended byte `i` of a dword, as float.
 template <int I>
 __device__ __forceinline__ float sbyte_f32(uint32_t d) {

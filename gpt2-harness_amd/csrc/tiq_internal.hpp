@@ -67,6 +67,16 @@ int launch_skinny(const LinearArgs& a);
 // Workspace bytes with which it splits the activations once per call.
 size_t skinny_workspace(int64_t M, int64_t K);
 
+// Batched decode linear with its K range split over workgroups (skinny.hip):
+// the products write fp32 partials, one more kernel sums them, applies the
+// epilogue and optionally writes the next linear's LayerNorm'd operand planes
+// (planes_out, K' = N). The input is fp32 rows (a.x, with a.fuse.ln_w) or the
+// planes of a previous call (x_planes).
+int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float* next_ln_w,
+                      const float* next_ln_b, float next_eps, uint16_t* planes_out);
+size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N);
+size_t decode_planes_bytes(int64_t M, int64_t K);
+
 // The register-staged int8 GEMM (gemm_staged.hip): whether it takes these
 // arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128) and
 // its launch.

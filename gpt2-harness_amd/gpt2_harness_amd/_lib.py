@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 F32, BF16 = 0, 1
 
-_i64, _i32, _vp, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+_i64, _i32, _vp, _sz, _f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
 
 #: (name, argtypes, restype) of every exported symbol
 SIGNATURES: dict[str, tuple[list, object]] = {
@@ -44,10 +44,15 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_linear_w4g": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_linear_fused": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
                           _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp], _i32),
+    "tiq_decode_linear_workspace": ([_i32, _i64, _i64, _i64], _sz),
+    "tiq_decode_planes_bytes": ([_i64, _i64], _sz),
+    "tiq_decode_linear": ([_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _f32, _i32,
+                           _vp, _i64, _vp, _vp, _f32, _vp, _vp, _sz, _vp], _i32),
     "tiq_linear_fused_workspace": ([_i32, _i32, _i64, _i64, _i64], _sz),
     "tiq_linear_fused_ws": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
                              _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp, _sz, _vp], _i32),
     "tiq_decode_attention": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _i32),
+    "tiq_decode_attention_planes": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),
     "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _vp], _i32),

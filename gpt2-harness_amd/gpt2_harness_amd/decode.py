@@ -247,6 +247,25 @@ class FusedDecoder(_DecoderBase):
         ws = max(ws, int(self.L.tiq_linear_fused_workspace(_lib.F32, head_fmt, B, C, cfg.vocab_size)))
         self.lin_ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
         self.lin_ws_bytes = ws
+        # Batched rows (5..64) with int8 block Linears: each Linear splits its K
+        # range over workgroups and hands the next one its LayerNorm'd operand
+        # planes (tiq_decode_linear), so no separate LayerNorm / split launches
+        lins = [l for b in model.h for l in (b.attn.c_attn, b.attn.c_proj, b.mlp.c_fc, b.mlp.c_proj)]
+        head_ok = self.head_q is None or self.head_q.fmt == FMT_W8
+        self.chain = 5 <= B <= 64 and head_ok and all(l.fmt == FMT_W8 for l in lins)
+        if self.chain:
+            L = self.L
+            head_wf = _lib.WF_F32 if self.head_q is None else _lib.WF_INT8
+            cws = max(int(L.tiq_decode_linear_workspace(_lib.WF_INT8, B, k, n))
+                      for k, n in ((C, qkv), (C, C), (C, hidden), (hidden, C)))
+            cws = max(cws, int(L.tiq_decode_linear_workspace(head_wf, B, C, cfg.vocab_size)))
+            self.chain_ws = torch.empty(max(cws, 1), dtype=torch.uint8, device=dev)
+            self.chain_ws_bytes = cws
+            pc, ph = int(L.tiq_decode_planes_bytes(B, C)), int(L.tiq_decode_planes_bytes(B, hidden))
+            self.p_ln1 = torch.empty(pc, dtype=torch.uint8, device=dev)   # LayerNorm 1 (or ln_f) planes
+            self.p_ln2 = torch.empty(pc, dtype=torch.uint8, device=dev)   # LayerNorm 2 planes
+            self.p_hid = torch.empty(ph, dtype=torch.uint8, device=dev)   # GELU(c_fc) planes
+            self.p_att = torch.empty(pc, dtype=torch.uint8, device=dev)   # attention output planes
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
@@ -261,7 +280,59 @@ class FusedDecoder(_DecoderBase):
             0 if res is None else res.stride(0), self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
         _lib.check(rc, "fused decode linear")
 
+    def _dl(self, lin, wf, y=None, x=None, planes_in=None, ln=None, act: int = 0, res=None, next_ln=None,
+            planes_out=None) -> None:
+        """One tiq_decode_linear: fp32 rows x (optionally LayerNorm'd) or the
+        planes of the previous call in; y and / or the planes of next_ln(y) out."""
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        K = lin.in_features if hasattr(lin, "in_features") else self.cfg.n_embd
+        N = lin.out_features if hasattr(lin, "out_features") else self.cfg.vocab_size
+        w = lin.codes if isinstance(lin, QuantLinear) else self.head_w
+        scale = lin.scale.data_ptr() if isinstance(lin, QuantLinear) else None
+        bias = _lib.ptr(lin.bias) if isinstance(lin, QuantLinear) else None
+        rc = self.L.tiq_decode_linear(
+            _lib.ptr(x), 0 if x is None else x.stride(0), _lib.ptr(planes_in), self.B, K, w.data_ptr(), wf, scale,
+            bias, N, _lib.ptr(y), 0 if y is None else y.stride(0), None if ln is None else ln.weight.data_ptr(),
+            None if ln is None else ln.bias.data_ptr(), float(ln.eps) if ln is not None else 1e-5, act,
+            _lib.ptr(res), 0 if res is None else res.stride(0), None if next_ln is None else next_ln.weight.data_ptr(),
+            None if next_ln is None else next_ln.bias.data_ptr(), float(next_ln.eps) if next_ln is not None else 1e-5,
+            _lib.ptr(planes_out), self.chain_ws.data_ptr(), self.chain_ws_bytes, st)
+        _lib.check(rc, "decode linear")
+
+    def _step_chain(self) -> None:
+        m, cfg, L = self.model, self.cfg, self.L
+        B, C = self.B, cfg.n_embd
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        W8 = _lib.WF_INT8
+        _lib.check(L.tiq_embed_tokens(self.tok_flat.data_ptr(), self.pos.data_ptr(), m.wte.weight.data_ptr(),
+                                      cfg.vocab_size, m.wpe.weight.data_ptr(), cfg.n_positions, B, C,
+                                      self.x.data_ptr(), st), "embed")
+        n = len(m.h)
+        for i, block in enumerate(m.h):
+            attn, mlp = block.attn, block.mlp
+            if i == 0:  # the embedding rows: LayerNorm 1 here
+                self._dl(attn.c_attn, W8, y=self.qkv, x=self.x, ln=block.ln_1)
+            else:       # the previous block left LayerNorm 1's planes
+                self._dl(attn.c_attn, W8, y=self.qkv, planes_in=self.p_ln1)
+            _lib.check(L.tiq_decode_attention_planes(self.qkv.data_ptr(), self.qkv.stride(0), B, self.H, self.Hkv,
+                                                     self.hd, self.k[i].data_ptr(), self.v[i].data_ptr(), self.T,
+                                                     self.pos.data_ptr(), self.att.data_ptr(), self.att.stride(0),
+                                                     self.p_att.data_ptr(), st), "decode attention")
+            self._dl(attn.c_proj, W8, y=self.x, planes_in=self.p_att, res=self.x, next_ln=block.ln_2,
+                     planes_out=self.p_ln2)
+            self._dl(mlp.c_fc, W8, planes_in=self.p_ln2, act=_lib.ACT_GELU_TANH, planes_out=self.p_hid)
+            nxt = m.h[i + 1].ln_1 if i + 1 < n else m.ln_f
+            self._dl(mlp.c_proj, W8, y=self.x, planes_in=self.p_hid, res=self.x, next_ln=nxt, planes_out=self.p_ln1)
+        head = self.head_q if self.head_q is not None else m.lm_head
+        self._dl(head, W8 if self.head_q is not None else _lib.WF_F32, y=self.logits, planes_in=self.p_ln1)
+        _lib.check(L.tiq_argmax_rows(self.logits.data_ptr(), B, cfg.vocab_size, cfg.vocab_size,
+                                     self.tok_flat.data_ptr(), self.out.data_ptr(), self.T, self.pos.data_ptr(),
+                                     self.argmax_ws.data_ptr(), self.argmax_ws.numel(), st), "argmax")
+
     def _step(self) -> None:
+        if self.chain:
+            self._step_chain()
+            return
         m, cfg, L = self.model, self.cfg, self.L
         B, C = self.B, cfg.n_embd
         st = torch.cuda.current_stream(self.dev).cuda_stream

@@ -217,6 +217,34 @@ int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_
                         const float* residual, int64_t ld_residual, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Batched decode-step linear (5 <= M <= 64 fp32 activation rows; int8
+ * weights with per-row scale, or fp32 weights) whose K range is split over
+ * workgroups: the matrix-core products write fp32 partial sums to the
+ * workspace, a second kernel sums them in a fixed order and applies
+ *     y = act(LayerNorm(x) @ W^T * scale + bias) + residual
+ * (the reference's Linear at model.py:254,319,352,355 with its neighbours at
+ * model.py:413-427, as tiq_linear_fused), so that a small matrix still
+ * occupies the whole GPU.
+ *   Input: fp32 rows x (leading dimension ldx, optional LayerNorm ln_*), or,
+ *   when x_planes is not NULL, operand planes written by planes_out of a
+ *   previous call with N = this K (x and ln_* are then unused; ln_* must be
+ *   NULL).
+ *   Output: y (fp32, may be NULL when only planes are wanted; residual may
+ *   alias it) and, when planes_out is not NULL, the operand planes of
+ *   next_ln(y) (or of y without next_ln_*) for a following call:
+ *   tiq_decode_planes_bytes(M, N) bytes, 16-byte aligned, N % 32 == 0.
+ *   workspace: at least tiq_decode_linear_workspace(w_format, M, K, N)
+ *   bytes, 16-byte aligned; clobbered.
+ * No counterpart in the reference (its decode runs one torch op per step). */
+size_t tiq_decode_linear_workspace(int w_format, int64_t M, int64_t K, int64_t N);
+size_t tiq_decode_planes_bytes(int64_t M, int64_t K);
+int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M, int64_t K, const void* w,
+                      int w_format, const float* scale, const float* bias, int64_t N, float* y, int64_t ldy,
+                      const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                      const float* residual, int64_t ld_residual, const float* next_ln_weight,
+                      const float* next_ln_bias, float next_ln_eps, uint16_t* planes_out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 /* Self-attention of one new token per sequence (model.py:248-318 at T = 1,
  * KVCache.update model.py:153-172): qkv is the (batch, (n_head + 2 n_kv_head)
  * * head_dim) output of c_attn (leading dim ld_qkv); its k and v are written
@@ -227,6 +255,15 @@ int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_
 int tiq_decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head, int64_t n_kv_head,
                          int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
                          float* y, int64_t ldy, void* stream);
+
+/* tiq_decode_attention that also writes its output rows as the operand
+ * planes of the following batched decode linear (tiq_decode_linear's
+ * x_planes, K = n_head * head_dim; tiq_decode_planes_bytes(batch, K) bytes,
+ * 16-byte aligned), saving that linear a split pass. No counterpart in the
+ * reference. */
+int tiq_decode_attention_planes(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head, int64_t n_kv_head,
+                                int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
+                                float* y, int64_t ldy, uint16_t* planes_out, void* stream);
 
 /* x[b] = wte[tokens[b]] + wpe[*pos]  (model.py:561-564 for one position). */
 int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte, int64_t vocab,

@@ -393,3 +393,149 @@ def test_graph_replays_with_different_prompts(reference_decode, dev):
         torch.cuda.synchronize()
         assert torch.equal(got, want), seed
     assert len(dec.prefill_graphs) == 1
+
+
+# ---- tiq_decode_linear: batched decode linears with the K range split over
+# workgroups, chained through operand planes ---------------------------------
+
+def _dl(x, xp, M, K, wd, wf, sd, bd, N, y, ln=None, act=0, res=None, nln=None, planes=None, ws=None):
+    L = _lib.lib()
+    n_ws = int(L.tiq_decode_linear_workspace(wf, M, K, N))
+    if ws is None:
+        ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device="cuda")
+    p = lambda t: None if t is None else t.data_ptr()
+    rc = L.tiq_decode_linear(p(x), 0 if x is None else x.stride(0), p(xp), M, K, wd.data_ptr(), wf, p(sd), p(bd), N,
+                             p(y), 0 if y is None else y.stride(0), p(None if ln is None else ln[0]),
+                             p(None if ln is None else ln[1]), 1e-5, act, p(res), 0 if res is None else res.stride(0),
+                             p(None if nln is None else nln[0]), p(None if nln is None else nln[1]), 1e-5, p(planes),
+                             ws.data_ptr(), n_ws, _st())
+    torch.cuda.synchronize()
+    return rc
+
+
+def _w8(c_oracle, N, K, gen, dev):
+    w = torch.randn(N, K, generator=gen) * 0.02
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    return torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), OL.dequantize(q, s)
+
+
+@pytest.mark.parametrize("M", [5, 32, 64])
+@pytest.mark.parametrize("K,N", [(1600, 4800), (1600, 1600), (6400, 1600), (768, 2304)])
+def test_decode_linear_ln_gelu(dev, c_oracle, M, K, N):
+    """fp32 rows in, LayerNorm + GELU epilogue, fp32 out: split-K products and
+    the fixed-order reduction, held to the float64 bar."""
+    gen = torch.Generator().manual_seed(M * 3 + K + N)
+    qd, sd, w_hat = _w8(c_oracle, N, K, gen, dev)
+    x = torch.randn(M, K, generator=gen) * 2 + 0.5
+    lw, lb = 1 + 0.1 * torch.randn(K, generator=gen), 0.1 * torch.randn(K, generator=gen)
+    b = 0.1 * torch.randn(N, generator=gen)
+    y = torch.empty(M, N, device=dev)
+    rc = _dl(x.to(dev), None, M, K, qd, _lib.WF_INT8, sd, b.to(dev), N, y, ln=(lw.to(dev), lb.to(dev)),
+             act=_lib.ACT_GELU_TANH)
+    _lib.check(rc, "decode linear")
+    ref = _gelu(OL.linear_ref(F.layer_norm(x, (K,), lw, lb, 1e-5), w_hat, b))
+    xn64 = F.layer_norm(x.double(), (K,), lw.double(), lb.double(), 1e-5)
+    _f64_check(y, ref, _gelu(xn64 @ w_hat.double().T + b.double()))
+
+
+@pytest.mark.parametrize("M", [8, 32])
+def test_decode_linear_chain_through_planes(dev, c_oracle, M):
+    """The decode block's chain: (1) fp32 rows + LayerNorm -> y1 and the
+    planes of LayerNorm2(y1); (2) those planes -> GELU, planes only (no fp32
+    output); (3) those planes -> + bias + residual in place. Each stage is
+    checked against float64 from the GPU's previous fp32 result."""
+    C, H = 1600, 6400
+    gen = torch.Generator().manual_seed(M)
+    q1, s1, w1 = _w8(c_oracle, C, C, gen, dev)
+    q2, s2, w2 = _w8(c_oracle, H, C, gen, dev)
+    q3, s3, w3 = _w8(c_oracle, C, H, gen, dev)
+    b1, b2, b3 = (0.1 * torch.randn(n, generator=gen) for n in (C, H, C))
+    g1, e1, g2, e2 = (1 + 0.1 * torch.randn(C, generator=gen), 0.1 * torch.randn(C, generator=gen),
+                      1 + 0.1 * torch.randn(C, generator=gen), 0.1 * torch.randn(C, generator=gen))
+    x = torch.randn(M, C, generator=gen)
+    r0 = torch.randn(M, C, generator=gen)
+    L = _lib.lib()
+    pa = torch.empty(int(L.tiq_decode_planes_bytes(M, C)), dtype=torch.uint8, device=dev)
+    pb = torch.empty(int(L.tiq_decode_planes_bytes(M, H)), dtype=torch.uint8, device=dev)
+    y1 = torch.empty(M, C, device=dev)
+    _lib.check(_dl(x.to(dev), None, M, C, q1, _lib.WF_INT8, s1, b1.to(dev), C, y1, ln=(g1.to(dev), e1.to(dev)),
+                   nln=(g2.to(dev), e2.to(dev)), planes=pa), "stage 1")
+    ref = OL.linear_ref(F.layer_norm(x, (C,), g1, e1, 1e-5), w1, b1)
+    _f64_check(y1, ref, F.layer_norm(x.double(), (C,), g1.double(), e1.double(), 1e-5) @ w1.double().T + b1.double())
+    _lib.check(_dl(None, pa, M, C, q2, _lib.WF_INT8, s2, b2.to(dev), H, None, act=_lib.ACT_GELU_TANH, planes=pb),
+               "stage 2")
+    y3 = r0.to(dev).clone()
+    _lib.check(_dl(None, pb, M, H, q3, _lib.WF_INT8, s3, b3.to(dev), C, y3, res=y3), "stage 3")
+    h64 = _gelu(F.layer_norm(y1.cpu().double(), (C,), g2.double(), e2.double(), 1e-5) @ w2.double().T + b2.double())
+    h32 = _gelu(OL.linear_ref(F.layer_norm(y1.cpu(), (C,), g2, e2, 1e-5), w2, b2))
+    _f64_check(y3, r0 + OL.linear_ref(h32, w3, b3), r0.double() + h64 @ w3.double().T + b3.double())
+
+
+@pytest.mark.parametrize("M", [6, 32])
+def test_decode_linear_fp32_weights_and_errors(dev, M):
+    """fp32 weights (the head) from planes, N not a multiple of 8 (one split,
+    no reduction); argument errors; a second call with fewer rows on the same
+    workspace."""
+    K, N = 768, 5003
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(M + 1)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen)
+    lw, lb = 1 + 0.1 * torch.randn(K, generator=gen), 0.1 * torch.randn(K, generator=gen)
+    wd = w.to(dev)
+    y = torch.empty(M, N, device=dev)
+    _lib.check(_dl(x.to(dev), None, M, K, wd, _lib.WF_F32, None, None, N, y, ln=(lw.to(dev), lb.to(dev))), "head")
+    ref = F.layer_norm(x, (K,), lw, lb, 1e-5) @ w.T
+    _f64_check(y, ref, F.layer_norm(x.double(), (K,), lw.double(), lb.double(), 1e-5) @ w.double().T)
+    # planes carry their LayerNorm: LayerNorm with planes input is an error
+    pl = torch.zeros(int(L.tiq_decode_planes_bytes(M, K)), dtype=torch.uint8, device=dev)
+    assert _dl(None, pl, M, K, wd, _lib.WF_F32, None, None, N, y, ln=(lw.to(dev), lb.to(dev))) == -1
+    # a workspace too small for the input planes
+    assert int(L.tiq_decode_planes_bytes(M, K)) > 256
+    small = torch.empty(256, dtype=torch.uint8, device=dev)
+    rc = L.tiq_decode_linear(x.to(dev).data_ptr(), K, None, M, K, wd.data_ptr(), _lib.WF_F32, None, None, N,
+                             y.data_ptr(), N, None, None, 1e-5, 0, None, 0, None, None, 1e-5, None, small.data_ptr(),
+                             small.numel(), _st())
+    assert rc == -5
+    # two calls in a row on one workspace, the second with fewer rows
+    gen2 = torch.Generator().manual_seed(9)
+    C, N2 = 1600, 4800
+    w2 = torch.randn(N2, C, generator=gen2) * 0.02
+    w2d = w2.to(dev)
+    ws = torch.empty(int(L.tiq_decode_linear_workspace(_lib.WF_F32, 32, C, N2)), dtype=torch.uint8, device=dev)
+    for rows in (32, 32 - 7):
+        xx = torch.randn(rows, C, generator=gen2)
+        yy = torch.empty(rows, N2, device=dev)
+        _lib.check(_dl(xx.to(dev), None, rows, C, w2d, _lib.WF_F32, None, None, N2, yy, ws=ws), "reuse")
+        _f64_check(yy, xx @ w2.T, xx.double() @ w2.double().T)
+
+
+@pytest.mark.parametrize("B,H,pos", [(8, 25, 130), (32, 2, 20)])
+def test_decode_attention_planes_feed_the_projection(dev, c_oracle, B, H, pos):
+    """tiq_decode_attention_planes writes the same rows as tiq_decode_attention
+    and, as planes, the input of tiq_decode_linear: the projection from them
+    equals the projection from the fp32 rows bit for bit."""
+    L = _lib.lib()
+    hd, T = 64, 256
+    C = H * hd
+    gen = torch.Generator().manual_seed(B + H + pos)
+    qkv = torch.randn(B, 3 * C, generator=gen).to(dev)
+    kc = torch.randn(B, H, T, hd, generator=gen).to(dev)
+    vc = torch.randn(B, H, T, hd, generator=gen).to(dev)
+    kc2, vc2 = kc.clone(), vc.clone()
+    p = torch.tensor([pos], device=dev)
+    y1 = torch.empty(B, C, device=dev)
+    y2 = torch.empty(B, C, device=dev)
+    planes = torch.empty(int(L.tiq_decode_planes_bytes(B, C)), dtype=torch.uint8, device=dev)
+    _lib.check(L.tiq_decode_attention(qkv.data_ptr(), 3 * C, B, H, H, hd, kc.data_ptr(), vc.data_ptr(), T,
+                                      p.data_ptr(), y1.data_ptr(), C, _st()), "attention")
+    _lib.check(L.tiq_decode_attention_planes(qkv.data_ptr(), 3 * C, B, H, H, hd, kc2.data_ptr(), vc2.data_ptr(), T,
+                                             p.data_ptr(), y2.data_ptr(), C, planes.data_ptr(), _st()), "planes")
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    qd, sd, _ = _w8(c_oracle, C, C, gen, dev)
+    a = torch.empty(B, C, device=dev)
+    b = torch.empty(B, C, device=dev)
+    _lib.check(_dl(y1, None, B, C, qd, _lib.WF_INT8, sd, None, C, a), "from rows")
+    _lib.check(_dl(None, planes, B, C, qd, _lib.WF_INT8, sd, None, C, b), "from planes")
+    assert torch.equal(a, b)
