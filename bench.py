@@ -360,7 +360,9 @@ def eval_section(dev):
 def decode_xl_section(dev, new_tokens=128):
     """GPT-2-XL (48 layers, d 1600, 25 heads) seed 0, int8 per-channel, batch
     32, 128-token random prompts, greedy +new_tokens: end-to-end tokens/s
-    (prefill + decode) and the per-Linear decode GB/s at M = 32."""
+    (prefill + decode) and the per-Linear decode time / GB/s at M = 32.
+    The step is the fused decoder's batched chain (tiq_decode_linear,
+    tiq_decode_attention_planes), captured once and replayed per token."""
     import torch
 
     import gpt2_harness_amd as g
@@ -391,35 +393,41 @@ def decode_xl_section(dev, new_tokens=128):
            "prefill_ms": t_pre * 1e3, "decode_ms_per_step": t_dec * 1e3 / (new_tokens - 1),
            "tokens_per_s": B * new_tokens / (t_pre + t_dec),
            "decode_tokens_per_s": B * (new_tokens - 1) / t_dec}
-    # per-Linear decode GB/s of layer 0 at M = 32 (HIP events, 20 calls each)
-    L = _lib.lib()
-    st = torch.cuda.current_stream().cuda_stream
-    blk = qm.h[0]
-    x = torch.randn(B, 4 * cfg.n_embd, device=dev)
+    # per-Linear decode time of layer 0 at M = 32, each called as the decode
+    # step calls it (tiq_decode_linear from the previous op's operand planes),
+    # 20 calls captured in a HIP graph, the graph replayed 5 times (HIP
+    # events); GB/s by the decode GEMV formula N K + 4 N + 2 M K + 2 M N
     per = {}
-    for name, lin in (("c_attn", blk.attn.c_attn), ("attn.c_proj", blk.attn.c_proj), ("c_fc", blk.mlp.c_fc),
-                      ("mlp.c_proj", blk.mlp.c_proj)):
+    blk = qm.h[0]
+    W8, gelu = _lib.WF_INT8, _lib.ACT_GELU_TANH
+    calls = (("c_attn", blk.attn.c_attn, lambda l: dec._dl(l, W8, y=dec.qkv, planes_in=dec.p_ln1)),
+             ("attn.c_proj", blk.attn.c_proj, lambda l: dec._dl(l, W8, y=dec.x, planes_in=dec.p_att, res=dec.x,
+                                                               next_ln=blk.ln_2, planes_out=dec.p_ln2)),
+             ("c_fc", blk.mlp.c_fc, lambda l: dec._dl(l, W8, planes_in=dec.p_ln2, act=gelu, planes_out=dec.p_hid)),
+             ("mlp.c_proj", blk.mlp.c_proj, lambda l: dec._dl(l, W8, y=dec.x, planes_in=dec.p_hid, res=dec.x,
+                                                             next_ln=qm.h[1].ln_1, planes_out=dec.p_ln1)))
+    s_cap = torch.cuda.Stream()
+    for name, lin, fn in calls:
         K, N = lin.in_features, lin.out_features
-        y = torch.empty(B, N, device=dev)
-
-        def call():
-            rc = L.tiq_linear_fused_ws(x.data_ptr(), _lib.F32, B, K, x.stride(0), lin.codes.data_ptr(), _lib.WF_INT8,
-                                       lin.scale.data_ptr(), None, 0, _lib.ptr(lin.bias), N, y.data_ptr(), _lib.F32,
-                                       N, None, None, 1e-5, 0, None, 0, dec.lin_ws.data_ptr(), dec.lin_ws_bytes, st)
-            if rc:
-                raise RuntimeError(f"tiq_linear_fused_ws status {rc}")
-
-        call()
+        with torch.cuda.stream(s_cap):
+            fn(lin)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s_cap):
+                for _ in range(20):
+                    fn(lin)
+        gr.replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        for _ in range(20):
-            call()
+        for _ in range(5):
+            gr.replay()
         b.record()
         torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / 20
-        nbytes = N * K + 4 * N + 4 * B * K + 4 * B * N
-        per[f"{K}x{N}"] = {"us": us, "GB/s": nbytes / (us * 1e-6) / 1e9}
+        us = a.elapsed_time(b) * 1e3 / 100
+        nbytes = N * K + 4 * N + 2 * B * K + 2 * B * N
+        per[f"{K}x{N}"] = {"linear": name, "us": us, "GB/s": nbytes / (us * 1e-6) / 1e9}
+        del gr
     res["decode_linear_M32"] = per
     del dec, qm
     torch.cuda.empty_cache()
