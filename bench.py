@@ -192,7 +192,7 @@ def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed):
 
 
 def gemm_section(M, kn, dev, reps=20):
-    """int8 -> bf16 prefill GEMM (tiq_gemm_w8) per shape: `reps` launches back
+    """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws) per shape: `reps` launches back
     to back between one HIP event pair. Beside it, as the measured-achievable
     reference (not this library's path), the platform's bf16 GEMM
     (torch.matmul -> hipBLASLt) on bf16 weights of the same shape."""
@@ -225,10 +225,14 @@ def gemm_section(M, kn, dev, reps=20):
         y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
         st = torch.cuda.current_stream().cuda_stream
 
+        n_ws = int(L.tiq_gemm_w8_workspace(1, M, K, N))  # split-K partials when the tiles are few
+        ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=dev)
+
         def run():
-            rc = L.tiq_gemm_w8(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1, N, st)
+            rc = L.tiq_gemm_w8_ws(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1, N,
+                                  ws.data_ptr(), n_ws, st)
             if rc:
-                raise RuntimeError(f"tiq_gemm_w8 status {rc}")
+                raise RuntimeError(f"tiq_gemm_w8_ws status {rc}")
 
         us = timed(run)
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12

@@ -4,6 +4,8 @@
 //     y[m, n] = scale[n] * sum_k x[m, k] * q[n, k] + bias[n]
 // Built without -amdgpu-mfma-vgpr-form: its 128 x 128 accumulator blocks live
 // in AGPRs.
+#include <algorithm>
+
 #include "tiq_internal.hpp"
 
 namespace tiq {
@@ -153,18 +155,24 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FW[set][i], FX[set][j], acc[i][j], 0, 0, 0);
     };
 
-    const int nk = K / BK;
+    // split-K (gridDim.z > 1): workgroup z takes k64 steps [z NK / S, (z + 1) NK / S)
+    // and writes raw fp32 partial sums (unit scale, no bias) to slice z of y
+    const int NK = K / BK;
+    const int s0 = (int)blockIdx.z * NK / (int)gridDim.z;
+    const int nk = ((int)blockIdx.z + 1) * NK / (int)gridDim.z - s0;
+    const int kbase = s0 * BK;
+    const bool split = gridDim.z > 1;
 #pragma unroll
-    for (int q = 0; q < NL; ++q) gload(0, 0, q);
+    for (int q = 0; q < NL; ++q) gload(kbase, 0, q);
 #pragma unroll
-    for (int q = 0; q < NL; ++q) gload(min(1, nk - 1) * BK, 1, q);
+    for (int q = 0; q < NL; ++q) gload(kbase + min(1, nk - 1) * BK, 1, q);
     // the epilogue's per-column scale and bias, read once here, behind the
     // first tiles' loads (after the last k step they would cost another trip
     // to memory); columns past N repeat the last one
     for (int c = tid; c < BN; c += NT) {
         const int n = min(n_blk + c, N - 1);
-        sb_s[0][c] = scale[n];
-        sb_s[1][c] = bias ? bias[n] : 0.f;
+        sb_s[0][c] = split ? 1.f : scale[n];
+        sb_s[1][c] = (bias && !split) ? bias[n] : 0.f;
     }
 #pragma unroll
     for (int q = 0; q < NL; ++q) lstore(smem, 0, q);
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     auto step = [&](int s, int p) {
         uint8_t* cur = smem + (s & 1) * STAGE;
         uint8_t* nxt = smem + ((s + 1) & 1) * STAGE;
-        const int k2 = min(s + 2, nk - 1) * BK;
+        const int k2 = kbase + min(s + 2, nk - 1) * BK;
 #pragma unroll
         for (int kk = 0; kk < 3; ++kk) {
             const int set = kk & 1;
@@ -257,7 +265,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
             const int m = m_blk + pass * ROWS + ml, n = n_blk + u * UNIT;
             const u32x4 v = *reinterpret_cast<const u32x4*>(smem + ml * ROW_BYTES + ((u ^ (ml & (UNITS - 1))) * 16));
             // nontemporal: the output is written once and read by a later kernel
-            if (m < M && n < N) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(y + (int64_t)m * ldy + n));
+            if (m < M && n < N)
+                __builtin_nontemporal_store(
+                    v, reinterpret_cast<u32x4*>(y + ((int64_t)blockIdx.z * M + m) * ldy + n));
         }
         if (pass + 1 < PASSES) __syncthreads();
     }
@@ -307,7 +317,55 @@ int staged_choice(int64_t M, int64_t N, int64_t K) {
     return best;
 }
 
+// The end of a split-K product: y[m][n] = scale[n] * sum_z part[z][m][n] +
+// bias[n], the S slices summed in a fixed order; 4 consecutive outputs a thread.
+template <typename TY>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ bias, TY* __restrict__ y,
+                                                            int64_t ldy) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= (int64_t)M * N) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    const int64_t slice = (int64_t)M * N;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < S; ++z) {
+        const float4 v = *reinterpret_cast<const float4*>(part + z * slice + i);
+        a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+    }
+    const float4 sc = *reinterpret_cast<const float4*>(scale + n);
+    float4 bi = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bias) bi = *reinterpret_cast<const float4*>(bias + n);
+    const float o0 = fmaf(a.x, sc.x, bi.x), o1 = fmaf(a.y, sc.y, bi.y);
+    const float o2 = fmaf(a.z, sc.z, bi.z), o3 = fmaf(a.w, sc.w, bi.w);
+    TY* yr = y + (int64_t)m * ldy + n;
+    if constexpr (sizeof(TY) == 4) {
+        *reinterpret_cast<float4*>(yr) = make_float4(o0, o1, o2, o3);
+    } else {
+        uint2 o;
+        o.x = (uint32_t)f32_to_bf16_bits(o0) | ((uint32_t)f32_to_bf16_bits(o1) << 16);
+        o.y = (uint32_t)f32_to_bf16_bits(o2) | ((uint32_t)f32_to_bf16_bits(o3) << 16);
+        *reinterpret_cast<uint2*>(yr) = o;
+    }
+}
+
 }  // namespace
+
+// Split-K plan for products with too few output tiles to fill the GPU:
+// 128 x 128 tiles (two workgroups per CU, 512 slots); when they fill less
+// than half of the slots, K is split S ways (each split at least four k64
+// steps, at most 8 splits). 1: no split.
+int64_t staged_splits(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles * 2 >= 512) return 1;
+    const int64_t S = std::min<int64_t>(std::min<int64_t>(512 / tiles, (K / BK) / 4), 8);
+    return std::max<int64_t>(S, 1);
+}
+
+size_t staged_split_workspace(int64_t M, int64_t N, int64_t K) {
+    const int64_t S = staged_splits(M, N, K);
+    return S > 1 ? (size_t)((S * M * N * 4 + 255) / 256 * 256) : 0;
+}
 
 template <typename TY>
 int dispatch_staged_t(const LinearArgs& a, int choice) {
@@ -327,6 +385,30 @@ int launch_staged_gemm(const LinearArgs& a, int choice) {
     if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
     if (a.y_dtype == TIQ_F32) return dispatch_staged_t<float>(a, choice);
     return dispatch_staged_t<uint16_t>(a, choice);
+}
+
+int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
+    if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
+    const int64_t S = staged_splits(a.M, a.N, a.K);
+    const size_t need = staged_split_workspace(a.M, a.N, a.K);
+    if (S <= 1 || !ws || ws_bytes < need || !aligned(ws, 16)) return TIQ_EUNSUPPORTED;
+    float* part = static_cast<float*>(ws);
+    const int64_t tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+    // the products: raw fp32 slices [S][M][N] (unit scale, no bias in the kernel)
+    hipLaunchKernelGGL((gemm_w8_staged<128, 128, float>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
+                       a.stream, static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
+                       a.scale, a.bias, part, (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
+    int rc = launch_status();
+    if (rc != TIQ_OK) return rc;
+    const int64_t quads = a.M * a.N / 4;
+    const dim3 grid((unsigned)((quads + 255) / 256));
+    if (a.y_dtype == TIQ_F32)
+        hipLaunchKernelGGL(splitk_reduce_kernel<float>, grid, dim3(256), 0, a.stream, part, (int)S, (int)a.M,
+                           (int)a.N, a.scale, a.bias, static_cast<float*>(a.y), a.ldy);
+    else
+        hipLaunchKernelGGL(splitk_reduce_kernel<uint16_t>, grid, dim3(256), 0, a.stream, part, (int)S, (int)a.M,
+                           (int)a.N, a.scale, a.bias, static_cast<uint16_t*>(a.y), a.ldy);
+    return launch_status();
 }
 
 }  // namespace tiq

@@ -100,6 +100,10 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
                        static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, static_cast<uint16_t*>(ws));
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
+    // a workspace sized by tiq_gemm_w8_workspace also holds split-K partials
+    const size_t planes = split_workspace(a.M, a.K);
+    rc = launch_staged_gemm_split(g, static_cast<uint8_t*>(ws) + planes, ws_bytes - planes);
+    if (rc != TIQ_EUNSUPPORTED) return rc;
     return launch_staged_gemm(g, staged_gemm_choice(g.M, g.N, g.K));
 }
 
@@ -153,7 +157,36 @@ extern "C" int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K
     if (rc != TIQ_OK || M == 0 || N == 0) return rc;
     rc = run_linear_split(a, workspace, workspace_bytes);
     if (rc != TIQ_EUNSUPPORTED) return rc;
+    if (a.x_dtype == TIQ_BF16 && M >= kGemmMinRows) {  // bf16 rows: split-K when planned
+        rc = launch_staged_gemm_split(a, workspace, workspace_bytes);
+        if (rc != TIQ_EUNSUPPORTED) return rc;
+    }
     return run_linear(a);
+}
+
+extern "C" size_t tiq_gemm_w8_workspace(int x_dtype, int64_t M, int64_t K, int64_t N) {
+    if ((x_dtype != TIQ_F32 && x_dtype != TIQ_BF16) || M < kGemmMinRows || K <= 0 || K % 64 != 0 || N <= 0)
+        return 0;
+    if (x_dtype == TIQ_F32) return split_workspace(M, K) + staged_split_workspace(M, N, 3 * K);
+    return staged_split_workspace(M, N, K);
+}
+
+extern "C" int tiq_gemm_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,
+                              const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0, bias,
+                             N, y, y_dtype, ldy, stream, kW8);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    if (workspace && !aligned(workspace, 16)) return TIQ_EALIGN;
+    if (x_dtype == TIQ_F32) {
+        rc = run_linear_split(a, workspace, workspace_bytes);
+        if (rc != TIQ_EUNSUPPORTED) return rc;
+    } else {
+        rc = launch_staged_gemm_split(a, workspace, workspace_bytes);
+        if (rc != TIQ_EUNSUPPORTED) return rc;
+    }
+    return launch_gemm(a);
 }
 
 extern "C" int tiq_gemv_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,

@@ -83,5 +83,12 @@ size_t decode_planes_bytes(int64_t M, int64_t K);
 bool staged_gemm_supported(const LinearArgs& a);
 int staged_gemm_choice(int64_t M, int64_t N, int64_t K);
 int launch_staged_gemm(const LinearArgs& a, int choice);
+// Split-K for products with few output tiles: S (1 = none), the workspace
+// bytes of its fp32 partial slices, and the launch (TIQ_EUNSUPPORTED when no
+// split is planned or the workspace is short: the caller then launches the
+// plain kernel).
+int64_t staged_splits(int64_t M, int64_t N, int64_t K);
+size_t staged_split_workspace(int64_t M, int64_t N, int64_t K);
+int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes);
 
 }  // namespace tiq

@@ -108,8 +108,9 @@ def linear_into(m: QuantLinear, x2: torch.Tensor, y: torch.Tensor) -> None:
     b = _lib.ptr(m.bias)
     if m.fmt == FMT_W8:
         # fp32 activations over many rows (a prefill) take the matrix cores as
-        # three exact bf16 planes; the library sizes the workspace (0: none)
-        ws_bytes = int(L.tiq_linear_w8_workspace(xd, M, K))
+        # three exact bf16 planes, and a product with few output tiles is split
+        # over K; the library sizes the workspace (0: none)
+        ws_bytes = max(int(L.tiq_linear_w8_workspace(xd, M, K)), int(L.tiq_gemm_w8_workspace(xd, M, K, N)))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
         rc = L.tiq_linear_w8_ws(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b, N,
                                 y.data_ptr(), yd, y.stride(0), None if ws is None else ws.data_ptr(), ws_bytes, st)

@@ -141,6 +141,18 @@ int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
                      void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* Workspace bytes with which tiq_gemm_w8_ws (and tiq_linear_w8_ws) run a
+ * product with few output tiles split over K (fp32 partial slices, summed
+ * in a fixed order by a second kernel), plus, for fp32 activations, their
+ * bf16 planes. 0 when none is needed. */
+size_t tiq_gemm_w8_workspace(int x_dtype, int64_t M, int64_t K, int64_t N);
+/* tiq_gemm_w8 with a caller workspace (see tiq_gemm_w8_workspace): the
+ * prefill product of the reference's Linears (model.py:254,319,352,355 at
+ * M = B * T) on the matrix cores; without enough workspace it runs unsplit. */
+int tiq_gemm_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q, const float* scale,
+                   const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /* Decode GEMV on the vector ALUs: coalesced 128-bit weight loads, dequant in
  * registers, wavefront reductions. Any M (processed in slices of up to 4
  * rows); needs K % 16 == 0 and 16-byte aligned weight rows. */

@@ -175,6 +175,44 @@ def test_linear_w8_bf16_strided_rows(dev, c_oracle, pad):
     assert torch.all(ys[:, N:] == 7.0), "kernel wrote outside its output rows"
 
 
+# Products with few output tiles split K over workgroups (fp32 partial slices
+# in the workspace, summed in a fixed order): bf16 rows through tiq_gemm_w8_ws,
+# fp32 rows through tiq_linear_w8_ws with a workspace sized by
+# tiq_gemm_w8_workspace (three bf16 planes, then the split product). Two
+# calls in a row on one workspace, the second with fewer rows.
+@pytest.mark.parametrize("K,N,M", [(6400, 1600, 256), (1600, 1600, 256), (1600, 4800, 300), (6400, 1600, 1024),
+                                   (768, 2304, 128)])
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_gemm_split_k(dev, c_oracle, K, N, M, x_dtype):
+    L = _lib.lib()
+    xd = _lib.dtype_code(x_dtype)
+    n_ws = int(L.tiq_gemm_w8_workspace(xd, M, K, N))
+    assert n_ws > 0
+    ws = torch.empty(n_ws, dtype=torch.uint8, device=dev)
+    entry = "tiq_gemm_w8_ws" if x_dtype == torch.bfloat16 else "tiq_linear_w8_ws"
+    for rows in (M, M - 37):
+        w, x, b = _inputs(K, N, rows, rows + K, x_dtype)
+        q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+        qd, sd, bd, xg = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
+        y32 = torch.empty(rows, N, device=dev)
+        ybf = torch.empty(rows, N, device=dev, dtype=torch.bfloat16)
+        for y in (y32, ybf):
+            rc = getattr(L, entry)(xg.data_ptr(), xd, rows, K, K, qd.data_ptr(), sd.data_ptr(), bd.data_ptr(), N,
+                                   y.data_ptr(), _lib.dtype_code(y.dtype), N, ws.data_ptr(), n_ws,
+                                   torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, entry)
+        torch.cuda.synchronize()
+        w_hat = OL.dequantize(q, s)
+        ok, err, bound = OL.within_tolerance(y32, OL.linear_ref(x, w_hat, b), TOL)
+        assert ok, (rows, err, bound)
+        assert torch.equal(ybf.cpu(), y32.cpu().to(torch.bfloat16))
+        if x_dtype == torch.float32:   # the exact planes: fp32-accurate
+            ref64 = x.double() @ w_hat.double().T + b.double()
+            err = float((y32.cpu().double() - ref64).abs().max())
+            err32 = float((OL.linear_ref(x, w_hat, b).double() - ref64).abs().max())
+            assert err <= 8 * max(err32, 2.0 ** -24 * float(ref64.abs().max())), (err, err32)
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 256])
 def test_linear_w8_dispatch(dev, c_oracle, M):
     _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.bfloat16, seed=M)
