@@ -130,12 +130,6 @@ __device__ __forceinline__ float dot_chunk(const uint4& w, const float4* xv) {
     else return dot_w4(w, xv);
 }
 
-// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
-__device__ __forceinline__ float gelu_tanh(float x) {
-    const float k = 0.7978845608028654f;
-    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
-}
-
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Bijective map of a workgroup index so that XCD b % 8 (where the hardware
@@ -374,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
                 float v = acc[r][m];
                 if (FMT == kW8 || FMT == kW4) v *= ep_scale;
                 if (bias) v += ep_bias;
-                if (fz.act == 1) v = gelu_tanh(v);
+                v = apply_act(v, fz.act);
                 if (fz.res) v += ep_res;
                 store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
             }
@@ -478,6 +472,10 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
     const float ep_bias = bias ? bias[n] : 0.f;
     float ep_res = 0.f;
     if (fz.res) ep_res = fz.res[(int64_t)min(m0 + min(lane, MT - 1), M - 1) * fz.ldr + n];
+    // Keep those loads here, in the shadow of the weight loads: left to itself
+    // the compiler sinks them into the storing lane's branch, one more trip to
+    // memory after the reduction (the FMA pass waits for the weights anyway).
+    asm volatile("" ::"v"(ep_scale), "v"(ep_bias), "v"(ep_res));
 
     auto x_of = [&](int u, int m, int p) -> float4 {
         if constexpr (sizeof(TX) == 2) return x4_of<TX>(xv[u][m][p / 2], p % 2);
@@ -548,7 +546,7 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ 
     for (int m = 0; m < MT; ++m) {
         if (lane == m && m0 + m < M) {
             float v = acc[m] * ep_scale + ep_bias;
-            if (fz.act == 1) v = gelu_tanh(v);
+            v = apply_act(v, fz.act);
             if (fz.res) v += ep_res;
             store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
         }
@@ -644,12 +642,20 @@ bool run_direct_mt(const LinearArgs& a, int& rc) {
 
 template <int FMT, typename TX, typename TY, bool LNF>
 bool run_direct_um(const LinearArgs& a, int& rc) {
-    const int64_t um = (a.K / Fmt<FMT>::KC + 63) / 64;
-    if (um <= 1) return run_direct_mt<1, FMT, TX, TY, LNF>(a, rc);
-    if (um <= 2) return run_direct_mt<2, FMT, TX, TY, LNF>(a, rc);
-    if (um <= 4) return run_direct_mt<4, FMT, TX, TY, LNF>(a, rc);
-    if (um <= 8) return run_direct_mt<8, FMT, TX, TY, LNF>(a, rc);
-    return false;
+    // exactly the chunks a lane needs: a spare round of (clamped, repeated)
+    // loads costs address work and registers, 0.1-0.2 us a launch
+    switch ((a.K / Fmt<FMT>::KC + 63) / 64) {
+        case 0:
+        case 1: return run_direct_mt<1, FMT, TX, TY, LNF>(a, rc);
+        case 2: return run_direct_mt<2, FMT, TX, TY, LNF>(a, rc);
+        case 3: return run_direct_mt<3, FMT, TX, TY, LNF>(a, rc);
+        case 4: return run_direct_mt<4, FMT, TX, TY, LNF>(a, rc);
+        case 5: return run_direct_mt<5, FMT, TX, TY, LNF>(a, rc);
+        case 6: return run_direct_mt<6, FMT, TX, TY, LNF>(a, rc);
+        case 7: return run_direct_mt<7, FMT, TX, TY, LNF>(a, rc);
+        case 8: return run_direct_mt<8, FMT, TX, TY, LNF>(a, rc);
+        default: return false;
+    }
 }
 
 constexpr int64_t kDirectLnMaxRows = 8192;

@@ -75,11 +75,6 @@ __device__ __forceinline__ uint32_t bf16x2_of_bytes(uint32_t d, int sh) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-__device__ __forceinline__ float gelu_tanh_f(float x) {
-    const float k = 0.7978845608028654f;  // sqrt(2 / pi)
-    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
-}
-
 template <typename TY>
 __device__ __forceinline__ void store_out(TY* p, float v) {
     if constexpr (sizeof(TY) == 4) *p = v;
@@ -202,9 +197,12 @@ __global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* _
         float t = a[i];
         if constexpr (SC) t *= lane8(sc, i);
         if constexpr (BI) t += lane8(bi, i);
-        if (act == 1) t = gelu_tanh_f(t);
-        if constexpr (RS) t += lane8(rs, i);
         v[i] = t;
+    }
+    apply_act<8>(v, act);
+    if constexpr (RS) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] += lane8(rs, i);
     }
     if (y && own) {
         float* yr = y + (int64_t)m * ldy + n;
@@ -604,7 +602,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
         if (gm < M && gn < N) {
             if (WF == kW8) v *= ep_scale;
             if (bias) v += ep_bias;
-            if (act == 1) v = gelu_tanh_f(v);
+            v = apply_act(v, act);
             if (res) v += ep_res[t];
             store_out<TY>(y + (int64_t)gm * ldy + gn, v);
         }

@@ -161,4 +161,30 @@ __device__ __forceinline__ float nibble_f32(uint32_t d) {
     return (float)((int32_t)((d >> (4 * I)) & 0xfu) - 8);
 }
 
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k = 0.7978845608028654f;
+    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+// Activation code 1 (GELU) applied to n values behind a real branch. Left to
+// itself the compiler evaluates the GELU unconditionally and selects the
+// result; those ~45 instructions (two transcendentals) then lengthen every
+// wavefront's tail, ~0.2 us per launch of a latency-bound kernel, also when
+// no activation is asked for. The empty volatile asm cannot be speculated,
+// so the block stays behind the branch.
+template <int n>
+__device__ __forceinline__ void apply_act(float (&v)[n], int act) {
+    if (act == 1) {
+        asm volatile("");
+#pragma unroll
+        for (int i = 0; i < n; ++i) v[i] = gelu_tanh(v[i]);
+    }
+}
+__device__ __forceinline__ float apply_act(float v, int act) {
+    float t[1] = {v};
+    apply_act<1>(t, act);
+    return t[0];
+}
+
 }  // namespace tiq
