@@ -407,17 +407,22 @@ __device__ __forceinline__ float4 x4_of<float>(const u32x4& u, int) {
 }
 
 template <int MT, int UM, int FMT, typename TX, typename TY, bool LNF>
-__global__ __launch_bounds__(64) void gemv_direct_kernel(const TX* __restrict__ x, int64_t ldx, int M,
-                                                         const uint8_t* __restrict__ w, int64_t ldw,
-                                                         const float* __restrict__ scale,
-                                                         const float* __restrict__ bias, TY* y, int64_t ldy, int N,
-                                                         int K, Fusion fz) {
+// The arguments up to M fill the 14 dwords the hardware preloads into SGPRs
+// at wave launch (built with kernarg preloading), so the first loads wait on
+// no kernarg fetch; the grid size is passed rather than read from the
+// dispatch's hidden arguments. The rest is fetched while the weights are in
+// flight.
+__global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restrict__ w,
+                                                         const TX* __restrict__ x,
+                                                         const float* __restrict__ scale, TY* y, int ldw, int ldx,
+                                                         int N, int K, int G, int M, int ldy,
+                                                         const float* __restrict__ bias, Fusion fz) {
     constexpr int KC = Fmt<FMT>::KC;
     constexpr int P = KC / 4;                          // float4 of activations per chunk
     constexpr int XB = KC * (int)sizeof(TX);           // activation bytes per chunk and row
     constexpr int XQ = XB >= 16 ? XB / 16 : 1;         // 16-byte registers holding them
     const int lane = threadIdx.x;
-    const int n = xcd_block(blockIdx.x, gridDim.x);
+    const int n = xcd_block(blockIdx.x, G);
     const int m0 = blockIdx.y * MT;
     const int NC = K / KC;
     const uint8_t* wr = w + (int64_t)n * ldw;
@@ -624,9 +629,9 @@ template <int MT, int UM, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct(const LinearArgs& a, int& rc) {
     if constexpr (direct_fits<MT, UM, FMT, TX, LNF>()) {
         const dim3 grid((unsigned)a.N, (unsigned)((a.M + MT - 1) / MT));
-        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, FMT, TX, TY, LNF>), grid, dim3(64), 0, a.stream,
-                           static_cast<const TX*>(a.x), a.ldx, (int)a.M, a.w, a.ldw, a.scale, a.bias,
-                           static_cast<TY*>(a.y), a.ldy, (int)a.N, (int)a.K, a.fuse);
+        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, FMT, TX, TY, LNF>), grid, dim3(64), 0, a.stream, a.w,
+                           static_cast<const TX*>(a.x), a.scale, static_cast<TY*>(a.y), (int)a.ldw, (int)a.ldx,
+                           (int)a.N, (int)a.K, (int)a.N, (int)a.M, (int)a.ldy, a.bias, a.fuse);
         rc = launch_status();
         return true;
     }
@@ -671,6 +676,8 @@ bool try_direct(const LinearArgs& a, int& rc) {
         constexpr size_t XB = KC * sizeof(TX);
         const size_t xa = XB >= 16 ? 16 : XB;
         if (!aligned(a.x, xa) || ((size_t)a.ldx * sizeof(TX)) % xa != 0) return false;
+        // the kernel takes its strides and sizes as 32-bit integers
+        if (a.ldw > INT32_MAX || a.ldx > INT32_MAX || a.ldy > INT32_MAX || a.N > INT32_MAX) return false;
         if (a.fuse.ln_w) {
             // every wavefront reads the whole row and its LayerNorm weight and
             // bias (12 bytes a column) from L2: worth it while a launch is
