@@ -20,11 +20,28 @@ namespace {
 constexpr int kHeadDim = 64;    // every released GPT-2 size
 constexpr int kMaxSlots = 1024;  // n_positions of GPT-2
 
-// One workgroup (4 wavefronts) per (sequence, head). Every global load the
-// kernel needs for the first kPre key / value slots (the whole cache at
-// GPT-2 decode lengths) is issued before the first barrier, so the kernel
-// waits for HBM once; longer histories stream the rest in a second pass.
-constexpr int kPreKeys = 128;  // slots whose key rows / values are prefetched
+// Attention of one query per (sequence, head): a workgroup of kAttWaves
+// wavefronts. The cache rows are read through buffer descriptors sized to the
+// pos slots written so far: a load past them returns zero with no memory
+// access, so no load address depends on pos (one scalar read gates them all,
+// no per-load clamps) and no traffic is spent on the empty tail of the cache.
+// Slot layout: chunk c covers slots 128 c .. 128 c + 127; wave w takes the
+// 16 slots from 128 c + 16 w, four a load instruction (16 lanes x 16 bytes of
+// one slot's row: 1 KB of consecutive cache per instruction). The keys of the
+// first NCH chunks are requested at launch (and the values too when NCH = 1);
+// with two chunks the values are requested as soon as the scores are stored,
+// into the keys' registers, so that second trip to memory overlaps the
+// softmax. Histories past 128 NCH slots stream one chunk per trip.
+constexpr int kAttWaves = 8;
+constexpr int kSlotsPerWave = 128 / kAttWaves;
+constexpr int kLoadsPerChunk = kSlotsPerWave / 4;
+
+typedef float tiq_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 cache_load(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    const tiq_f32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 
 // Columns k .. k + 7 of activation row m as the exact three bf16 planes, in
 // the operand order of the batched decode linear for K = Kc columns: for row
@@ -42,50 +59,25 @@ __device__ __forceinline__ void store_planes(uint16_t* x3, int64_t m, int64_t Kc
     }
 }
 
-__global__ __launch_bounds__(256) void decode_attention_kernel(const float* __restrict__ qkv, int64_t ld_qkv, int H,
-                                                               int Hkv, float* __restrict__ kc,
-                                                               float* __restrict__ vc, int64_t t_max,
-                                                               const int64_t* __restrict__ pos_p,
-                                                               float* __restrict__ y, int64_t ldy,
-                                                               uint16_t* __restrict__ x3) {
-    __shared__ float qs[kHeadDim], kn[kHeadDim], vn[kHeadDim];
+template <int NCH>
+__global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
+    const float* __restrict__ qkv, int64_t ld_qkv, int H, int Hkv, float* __restrict__ kc, float* __restrict__ vc,
+    int t_max, const int64_t* __restrict__ pos_p, float* __restrict__ y, int64_t ldy, uint16_t* __restrict__ x3) {
+    constexpr int W = kAttWaves, NI = kLoadsPerChunk;
+    __shared__ float qn[kHeadDim], kn[kHeadDim], vn[kHeadDim];
     __shared__ float sc[kMaxSlots];
-    __shared__ float red[4];
-    __shared__ float part[4][kHeadDim];
+    __shared__ float red[W];
+    __shared__ float4 part[W][4][16];
     __shared__ float ov[kHeadDim];
     const int b = blockIdx.x / H, h = blockIdx.x % H;
     const int group = H / Hkv, hk = h / group;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const float* row = qkv + (int64_t)b * ld_qkv;
+    const int row = lane >> 4, d4 = (lane & 15) * 4;  // slot within the load, first of 4 dims
+    const float* qr = qkv + (int64_t)b * ld_qkv;
     const int C = H * kHeadDim, KV = Hkv * kHeadDim;
     float* kb = kc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
     float* vb = vc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
 
-    // ---- issue every load of the first kPreKeys slots ----
-    // No address depends on pos (a device scalar) and no load sits behind a
-    // branch: slots are clamped into the cache and the values of slots >= pos
-    // are dropped where they are used, so all loads are in flight together.
-    const int64_t last = t_max - 1;
-    // keys: slot t = (tid / 4) + 64 j, this lane's 16 dims at qd
-    const int qd = (lane & 3) * 16;
-    const int kslot = (wave * 16) + (lane >> 2);  // 0..63
-    float4 kr[2][4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int64_t t = min((int64_t)(kslot + 64 * j), last);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) kr[j][q] = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q];
-    }
-    // values: slot t = wave + 4 i, this lane's dim
-    float vr[kPreKeys / 4];
-#pragma unroll
-    for (int i = 0; i < kPreKeys / 4; ++i) vr[i] = vb[min((int64_t)(wave + 4 * i), last) * kHeadDim + lane];
-    float q_new = 0.f, k_new = 0.f, v_new = 0.f;
-    if (tid < kHeadDim) {
-        q_new = row[h * kHeadDim + tid];
-        k_new = row[C + hk * kHeadDim + tid];
-        v_new = row[C + KV + hk * kHeadDim + tid];
-    }
     const int64_t pos = *pos_p;
     if (pos < 0 || pos >= t_max) {  // position outside the cache: flag the output, write nothing else
         if (tid < kHeadDim) y[(int64_t)b * ldy + h * kHeadDim + tid] = NAN;
@@ -97,71 +89,82 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
         }
         return;
     }
+    const int valid = (int)pos * kHeadDim * 4;  // bytes of slots 0 .. pos - 1
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kb, (short)0, valid, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vb, (short)0, valid, 0x00020000);
+    const int off0 = ((kSlotsPerWave * wave + row) * kHeadDim + d4) * 4;
+    auto slot_off = [&](int base, int i) { return off0 + (base + 4 * i) * kHeadDim * 4; };
+
+    float4 kr[NCH][NI], vr[NCH][NI];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) kr[c][i] = cache_load(rk, slot_off(128 * c, i));
+    if constexpr (NCH == 1) {  // one chunk: its values too, one trip to memory
+#pragma unroll
+        for (int i = 0; i < NI; ++i) vr[0][i] = cache_load(rv, slot_off(0, i));
+    }
+    const float4 q4 = *reinterpret_cast<const float4*>(qr + h * kHeadDim + d4);
     if (tid < kHeadDim) {
-        qs[tid] = q_new;
+        const float q_new = qr[h * kHeadDim + tid];
+        const float k_new = qr[C + hk * kHeadDim + tid];
+        const float v_new = qr[C + KV + hk * kHeadDim + tid];
+        qn[tid] = q_new;
         kn[tid] = k_new;
         vn[tid] = v_new;
-        if (h % group == 0) {  // one writer per kv head
+        if (h % group == 0) {  // one writer per kv head; no workgroup reads slot pos from the cache
             kb[pos * kHeadDim + tid] = k_new;
             vb[pos * kHeadDim + tid] = v_new;
         }
     }
     __syncthreads();
 
-    // ---- scores ----
+    // ---- scores of slots < pos (slot pos is the new key) ----
     const float inv_div = 1.0f / sqrtf((float)kHeadDim);  // exactly 1/8
-    // chunks of kPreKeys slots, this thread's two 64-slot rows each: the first
-    // chunk's keys were loaded at the start, a later chunk's are all requested
-    // before any is used (one trip to memory per chunk, slots clamped into the
-    // cache; only slots < pos count, slot pos is the new key)
-    for (int64_t base = 0; base <= pos; base += kPreKeys) {
-        float4 kk[2][4];
-        if (base == 0) {
+    auto score = [&](int t, const float4& k) {
+        float s = fmaf(q4.x, k.x, fmaf(q4.y, k.y, fmaf(q4.z, k.z, q4.w * k.w)));
+        s += dpp_move<0xB1>(s);   // the 16 lanes of the slot: lane xor 1,
+        s += dpp_move<0x4E>(s);   // xor 2,
+        s += dpp_move<0x141>(s);  // half-row mirror,
+        s += dpp_move<0x140>(s);  // row mirror: every lane of the row holds the sum
+        if ((lane & 15) == 0 && t < pos) sc[t] = s * inv_div;
+    };
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) kk[j][q] = kr[j][q];
-        } else {
+        for (int i = 0; i < NI; ++i) score(128 * c + kSlotsPerWave * wave + 4 * i + row, kr[c][i]);
+    for (int base = 128 * NCH; base < pos; base += 128) {
+        float4 kk[NI];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int64_t t = min(base + kslot + 64 * j, last);
+        for (int i = 0; i < NI; ++i) kk[i] = cache_load(rk, slot_off(base, i));
 #pragma unroll
-                for (int q = 0; q < 4; ++q) kk[j][q] = reinterpret_cast<const float4*>(kb + t * kHeadDim + qd)[q];
-            }
-        }
+        for (int i = 0; i < NI; ++i) score(base + kSlotsPerWave * wave + 4 * i + row, kk[i]);
+    }
+    if constexpr (NCH >= 2) {
+        asm volatile("" ::: "memory");  // the scores are stored: the keys' registers are free
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t t = base + kslot + 64 * j;
-            float s = 0.f;
-            if (t == pos) {
+        for (int c = 0; c < NCH; ++c)
 #pragma unroll
-                for (int d = 0; d < 16; ++d) s = fmaf(qs[qd + d], kn[qd + d], s);
-            } else if (t < pos) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    s = fmaf(qs[qd + 4 * q], kk[j][q].x, s);
-                    s = fmaf(qs[qd + 4 * q + 1], kk[j][q].y, s);
-                    s = fmaf(qs[qd + 4 * q + 2], kk[j][q].z, s);
-                    s = fmaf(qs[qd + 4 * q + 3], kk[j][q].w, s);
-                }
-            }
-            s += dpp_move<0xB1>(s);  // quad_perm [1, 0, 3, 2]: the lane xor 1
-            s += dpp_move<0x4E>(s);  // quad_perm [2, 3, 0, 1]: the lane xor 2
-            if ((lane & 3) == 0 && t <= pos) sc[t] = s * inv_div;
-        }
+            for (int i = 0; i < NI; ++i) vr[c][i] = cache_load(rv, slot_off(128 * c, i));
+    }
+    if (wave == 0) {  // the new key's score
+        const float s = wave_sum_dpp(qn[lane] * kn[lane]);
+        if (lane == 0) sc[pos] = s * inv_div;
     }
     __syncthreads();
 
     // ---- softmax over slots 0..pos ----
     float mx = -INFINITY;
-    for (int64_t t = tid; t <= pos; t += 256) mx = fmaxf(mx, sc[t]);
+    for (int64_t t = tid; t <= pos; t += 64 * W) mx = fmaxf(mx, sc[t]);
     mx = wave_max_dpp(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) mx = fmaxf(mx, red[w]);
     __syncthreads();
     float sum = 0.f;
-    for (int64_t t = tid; t <= pos; t += 256) {
+    for (int64_t t = tid; t <= pos; t += 64 * W) {
         const float p = expf(sc[t] - mx);
         sc[t] = p;
         sum += p;
@@ -169,32 +172,39 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const float* __re
     sum = wave_sum_dpp(sum);
     if (lane == 0) red[wave] = sum;
     __syncthreads();
-    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    sum = red[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[w];
 
-    // ---- weighted sum of values: wavefront w takes slots t = w mod 4, lane = dim ----
-    // (in chunks of kPreKeys slots as the scores: the first prefetched, a
-    // later chunk's values all requested before any is used)
-    float acc = 0.f;
-    for (int64_t base = 0; base < pos; base += kPreKeys) {
-        float vv[kPreKeys / 4];
-        if (base == 0) {
+    // ---- weighted sum of values: this lane's 4 dims over its slots ----
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](int t, const float4& v) {
+        const float p = t < pos ? sc[t] : 0.f;
+        acc.x = fmaf(p, v.x, acc.x);
+        acc.y = fmaf(p, v.y, acc.y);
+        acc.z = fmaf(p, v.z, acc.z);
+        acc.w = fmaf(p, v.w, acc.w);
+    };
 #pragma unroll
-            for (int i = 0; i < kPreKeys / 4; ++i) vv[i] = vr[i];
-        } else {
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
-            for (int i = 0; i < kPreKeys / 4; ++i) vv[i] = vb[min(base + wave + 4 * i, last) * kHeadDim + lane];
-        }
+        for (int i = 0; i < NI; ++i) add(128 * c + kSlotsPerWave * wave + 4 * i + row, vr[c][i]);
+    for (int base = 128 * NCH; base < pos; base += 128) {
+        float4 vv[NI];
 #pragma unroll
-        for (int i = 0; i < kPreKeys / 4; ++i) {
-            const int64_t t = base + wave + 4 * i;
-            if (t < pos) acc = fmaf(sc[t], vv[i], acc);
-        }
+        for (int i = 0; i < NI; ++i) vv[i] = cache_load(rv, slot_off(base, i));
+#pragma unroll
+        for (int i = 0; i < NI; ++i) add(base + kSlotsPerWave * wave + 4 * i + row, vv[i]);
     }
-    if ((pos & 3) == wave) acc = fmaf(sc[pos], vn[lane], acc);
-    part[wave][lane] = acc;
+    part[wave][row][lane & 15] = acc;
     __syncthreads();
-    if (tid < kHeadDim) {
-        const float o = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+    if (tid < kHeadDim) {  // the new value, then the partial sums of every wave and slot row in order
+        const float* pf = reinterpret_cast<const float*>(part);
+        float o = sc[pos] * vn[tid];
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o += pf[(w * 4 + r) * 64 + tid];
         y[(int64_t)b * ldy + h * kHeadDim + tid] = o / sum;
         ov[tid] = o / sum;
     }
@@ -301,8 +311,13 @@ static int decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int
     if (head_dim != kHeadDim || t_max <= 0 || t_max > kMaxSlots) return TIQ_EUNSUPPORTED;
     if (ld_qkv < (n_head + 2 * n_kv_head) * head_dim || ldy < n_head * head_dim) return TIQ_EINVAL;
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || (planes_out && !aligned(planes_out, 16))) return TIQ_EALIGN;
-    hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)(batch * n_head)), dim3(256), 0, as_stream(stream), qkv,
-                       ld_qkv, (int)n_head, (int)n_kv_head, k_cache, v_cache, t_max, pos, y, ldy, planes_out);
+    const dim3 grid((unsigned)(batch * n_head)), block(64 * kAttWaves);
+    if (t_max <= 128)
+        hipLaunchKernelGGL(decode_attention_kernel<1>, grid, block, 0, as_stream(stream), qkv, ld_qkv, (int)n_head,
+                           (int)n_kv_head, k_cache, v_cache, (int)t_max, pos, y, ldy, planes_out);
+    else
+        hipLaunchKernelGGL(decode_attention_kernel<2>, grid, block, 0, as_stream(stream), qkv, ld_qkv, (int)n_head,
+                           (int)n_kv_head, k_cache, v_cache, (int)t_max, pos, y, ldy, planes_out);
     return launch_status();
 }
 

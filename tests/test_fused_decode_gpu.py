@@ -269,9 +269,13 @@ def test_fused_f32_head_with_ln(dev):
     assert (y.cpu() - ref).abs().max() <= 1e-4 * ref.abs().max()
 
 
-@pytest.mark.parametrize("B,H,Hkv,pos", [(1, 12, 12, 0), (1, 12, 12, 127), (3, 25, 25, 200), (2, 8, 2, 63)])
-def test_decode_attention(dev, B, H, Hkv, pos):
-    hd, T = 64, 256
+@pytest.mark.parametrize("B,H,Hkv,pos,T", [(1, 12, 12, 0, 256), (1, 12, 12, 127, 256), (3, 25, 25, 200, 256),
+                                           (2, 8, 2, 63, 256), (1, 12, 12, 127, 128), (2, 4, 4, 99, 100),
+                                           (2, 4, 4, 150, 200), (1, 4, 2, 700, 1024), (1, 3, 3, 1023, 1024)])
+def test_decode_attention(dev, B, H, Hkv, pos, T):
+    """Slots past 128 / 256 (histories streamed chunk by chunk), caches whose
+    length is not a multiple of the 128-slot chunk, grouped kv heads."""
+    hd = 64
     gen = torch.Generator().manual_seed(pos + H)
     qkv = torch.randn(B, (H + 2 * Hkv) * hd, generator=gen)
     kc = torch.randn(B, Hkv, T, hd, generator=gen)
