@@ -17,7 +17,10 @@ GPT-2-XL shapes with M = 4096, the quantize kernels, and GPT-2 small int8
 greedy decode (64-token prompt, 64 new tokens) with its token parity against
 the reference fixture. ``cpu_baseline`` times the oracle's dequantize-then-
 fp32-matmul (the reference's runtime arithmetic) on the host cores over a
-bounded sample of the same GEMV workload.
+bounded sample of the same GEMV workload; ``detail["cpu_oracle"]`` times the
+oracle on bounded samples of the other configurations (greedy decode,
+quantize, prefill F.linear, the GPT-2-XL batch-32 step extrapolated from a
+2-layer model), each with its sample stated.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--quick]
 """
@@ -489,6 +492,94 @@ def cpu_baseline(budget_s: float = 10.0):
             "ms_per_step": med * 1e3}
 
 
+def cpu_configs():
+    """The oracle (the reference's CPU quantized path restated) on bounded
+    samples of the other configurations, on the same host threads."""
+    import numpy as np
+    import torch
+
+    from oracle import linear as OL
+    from oracle import model as OM
+    from oracle import quant as OQ
+
+    torch.set_num_threads(host_cores())
+    out = {}
+
+    def med(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    # GPT-2 small int8 greedy, batch 1, 64-token prompt
+    p, _ = OM.quantize_params(OM.init_params(OM.GPT2_SMALL, 0), 8)
+    idx = OM.benchmark_prompt(OM.GPT2_SMALL.vocab_size, 1, 64)
+    new = 16
+    t0 = time.perf_counter()
+    OM.generate_greedy(p, OM.GPT2_SMALL, idx, new)
+    dt = time.perf_counter() - t0
+    out["gpt2_small_int8_greedy"] = {"tokens_per_s": new / dt, "sample": f"seed-0 GPT-2 small int8, prompt 64, "
+                                     f"{new} new tokens (prefill included, as benchmark_generation counts)"}
+    del p
+
+    # quantize, GPT-2-XL shapes with 0.1% outliers x20
+    gen = np.random.default_rng(0)
+    q_res = {}
+    for K, N in XL_KN:
+        w = (gen.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float32)
+        flat = w.reshape(-1)
+        pick = gen.choice(flat.size, flat.size // 1000, replace=False)
+        flat[pick] *= 20
+        t8 = med(lambda: OQ.quantize_tensor(w, 8), reps=1)
+        t4 = med(lambda: OQ.quantize_groupwise_int4(w, 128), reps=1)
+        q_res[f"int8_per_channel_{K}x{N}"] = {"GB/s": (5 * N * K + 4 * N) / t8 / 1e9}
+        q_res[f"int4_g128_{K}x{N}"] = {"GB/s": (4 * N * K + N * K // 2 + 2 * N * -(-K // 128)) / t4 / 1e9}
+    out["quantize_xl"] = q_res
+
+    # prefill F.linear on W_hat, GPT-2-XL shapes
+    g = torch.Generator().manual_seed(0)
+    lin = {}
+    w_hats = {}
+    for K, N in XL_KN:
+        q, s = OQ.quantize_tensor((torch.randn(N, K, generator=g) * 0.02).numpy(), 8)
+        w_hats[(K, N)] = OL.dequantize(q, s)
+    for M in (256, 1024):
+        for K, N in XL_KN:
+            x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+            t = med(lambda: OL.linear_ref(x, w_hats[(K, N)]), reps=2)
+            lin[f"M{M}_{K}x{N}"] = {"TFLOP/s": 2 * M * N * K / t / 1e12}
+    out["gemm_xl"] = lin
+    del w_hats
+
+    # GPT-2-XL batch 32: a 2-layer model at XL width, decode steps timed and the
+    # per-layer part extrapolated to 48 layers (the head measured on its own)
+    cfg2 = OM.Shape(n_layer=2, n_head=25, n_embd=1600)
+    p2, _ = OM.quantize_params(OM.init_params(cfg2, 0), 8)
+    B, T0, steps = 32, 128, 3
+    idx = torch.randint(0, cfg2.vocab_size, (B, T0), generator=g)
+    cache = OM.Cache(cfg2.n_layer)
+    OM.forward(p2, cfg2, idx, cache)
+    tok = idx[:, -1:]
+    ts = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        logits = OM.forward(p2, cfg2, tok, cache)
+        ts.append(time.perf_counter() - t0)
+        tok = logits[:, -1:, :].argmax(-1)
+    xh = torch.randn(B, 1600, generator=g)
+    t_head = med(lambda: torch.nn.functional.linear(xh, p2["wte.weight"]), reps=3)
+    t_layer = max(statistics.median(ts) - t_head, 0.0) / cfg2.n_layer
+    t_step = 48 * t_layer + t_head
+    out["gpt2_xl_int8_b32_decode"] = {"tokens_per_s": B / t_step, "ms_per_step": t_step * 1e3,
+                                      "sample": f"extrapolated: {steps} decode steps of a 2-layer GPT-2-XL-width "
+                                                f"model (seed 0, int8) at batch {B} after a {T0}-token prefill; "
+                                                f"48 x the per-layer time plus the fp32 head"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -558,6 +649,8 @@ def main() -> int:
         detail["eval_gpt2_small_int8"] = eval_section(dev)
         print("# eval done", file=sys.stderr, flush=True)
         cpu = cpu_baseline()
+        detail["cpu_oracle"] = cpu_configs()
+        print("# cpu oracle done", file=sys.stderr, flush=True)
 
     traffic = None
     tfile = ROOT / "profiles" / "gemv_w8a16_gpt2small_m1.traffic.json"
