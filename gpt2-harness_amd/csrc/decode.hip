@@ -278,13 +278,16 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     }
 }
 
-__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pv, const int64_t* __restrict__ pi,
-                                                          int64_t rows, int64_t* __restrict__ out,
-                                                          int64_t* __restrict__ ids, int64_t ld_ids,
-                                                          int64_t* __restrict__ pos_p) {
-    const int lane = threadIdx.x;
+// One wavefront per row (rows beyond kArgFinalWaves taken in turn), so the
+// rows' partials are read together rather than one dependent trip per row.
+constexpr int kArgFinalWaves = 16;
+
+__global__ __launch_bounds__(64 * kArgFinalWaves) void argmax_final_kernel(
+    const float* __restrict__ pv, const int64_t* __restrict__ pi, int64_t rows, int64_t* __restrict__ out,
+    int64_t* __restrict__ ids, int64_t ld_ids, int64_t* __restrict__ pos_p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t col = pos_p ? *pos_p + 1 : 0;
-    for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t r = wave; r < rows; r += kArgFinalWaves) {
         float v = pv[r * kArgParts + lane];
         int64_t idx = pi[r * kArgParts + lane];
 #pragma unroll
@@ -294,7 +297,10 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
             if (ids && col >= 0 && col < ld_ids) ids[r * ld_ids + col] = idx;
         }
     }
-    if (lane == 0 && pos_p && ids) *pos_p = col;  // every read of the position in this step came before
+    if (pos_p && ids) {
+        __syncthreads();  // every wavefront has read the position of this step
+        if (threadIdx.x == 0) *pos_p = col;
+    }
 }
 
 }  // namespace
@@ -366,6 +372,7 @@ extern "C" int tiq_argmax_rows(const float* x, int64_t rows, int64_t cols, int64
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgParts, (unsigned)rows), dim3(256), 0, st, x, cols, ld, pv, pi);
     int rc = launch_status();
     if (rc) return rc;
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64), 0, st, pv, pi, rows, out, ids, ld_ids, pos);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64 * kArgFinalWaves), 0, st, pv, pi, rows, out, ids, ld_ids,
+                       pos);
     return launch_status();
 }

@@ -406,7 +406,8 @@ __device__ __forceinline__ float4 x4_of<float>(const u32x4& u, int) {
     return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
-template <int MT, int UM, int FMT, typename TX, typename TY, bool LNF>
+// R weight rows per wavefront (1 or 2) share the activation registers.
+template <int MT, int UM, int R, int FMT, typename TX, typename TY, bool LNF>
 // The arguments up to M fill the 14 dwords the hardware preloads into SGPRs
 // at wave launch (built with kernarg preloading), so the first loads wait on
 // no kernarg fetch; the grid size is passed rather than read from the
@@ -422,21 +423,23 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
     constexpr int XB = KC * (int)sizeof(TX);           // activation bytes per chunk and row
     constexpr int XQ = XB >= 16 ? XB / 16 : 1;         // 16-byte registers holding them
     const int lane = threadIdx.x;
-    const int n = xcd_block(blockIdx.x, G);
+    const int n0 = xcd_block(blockIdx.x, G) * R;  // rows n0 .. n0 + R - 1; past N: row N - 1, not stored
     const int m0 = blockIdx.y * MT;
     const int NC = K / KC;
-    const uint8_t* wr = w + (int64_t)n * ldw;
 
     // No load sits behind a branch: a lane past the end of the row re-reads
     // the row's last chunk (its product is dropped below; the repeats
     // coalesce into one request). Loads under a branch get merged with their
     // alternative through register moves, which wait for every load issued
     // before them and so serialize the trips to memory.
-    u32x4 wv[UM];
+    u32x4 wv[UM][R];
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
         const int c = min(lane + 64 * u, NC - 1);
-        wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 16 * (int64_t)c));
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[u][r] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(w + (int64_t)min(n0 + r, N - 1) * ldw + 16 * (int64_t)c));
     }
     // activations of the same K range: rows past M repeat row M - 1 (their
     // outputs are not stored)
@@ -471,12 +474,14 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
             }
         }
     }
-    // epilogue operands, read by every lane (lane m < MT keeps row m0 + m's);
-    // a residual aliasing y is read by the lane that writes the element
-    const float ep_scale = (FMT == kW8 || FMT == kW4) ? scale[n] : 1.f;
-    const float ep_bias = bias ? bias[n] : 0.f;
+    // epilogue operands, read by every lane (lane r MT + m keeps those of
+    // weight row n0 + r and activation row m0 + m); a residual aliasing y is
+    // read by the lane that writes the element
+    const int en = min(n0 + min(lane / MT, R - 1), N - 1), em = min(m0 + lane % MT, M - 1);
+    const float ep_scale = (FMT == kW8 || FMT == kW4) ? scale[en] : 1.f;
+    const float ep_bias = bias ? bias[en] : 0.f;
     float ep_res = 0.f;
-    if (fz.res) ep_res = fz.res[(int64_t)min(m0 + min(lane, MT - 1), M - 1) * fz.ldr + n];
+    if (fz.res) ep_res = fz.res[(int64_t)em * fz.ldr + en];
     // Keep those loads here, in the shadow of the weight loads: left to itself
     // the compiler sinks them into the storing lane's branch, one more trip to
     // memory after the reduction (the FMA pass waits for the weights anyway).
@@ -521,9 +526,11 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
         }
     }
 
-    float acc[MT];
+    float acc[R][MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
         const bool own = lane + 64 * u < NC;
@@ -541,21 +548,28 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
                     xf[p].w = (xf[p].w - mean[m]) * rstd[m] * g.w + b.w;
                 }
             }
-            const float part = dot_chunk<FMT>(make_uint4(wv[u].x, wv[u].y, wv[u].z, wv[u].w), xf);
-            acc[m] += own ? part : 0.f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float part = dot_chunk<FMT>(make_uint4(wv[u][r].x, wv[u][r].y, wv[u][r].z, wv[u][r].w), xf);
+                acc[r][m] += own ? part : 0.f;
+            }
         }
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = wave_sum_dpp(acc[m]);
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (lane == m && m0 + m < M) {
-            float v = acc[m] * ep_scale + ep_bias;
-            v = apply_act(v, fz.act);
-            if (fz.res) v += ep_res;
-            store_y<TY>(y + (int64_t)(m0 + m) * ldy + n, v);
+        for (int m = 0; m < MT; ++m) acc[r][m] = wave_sum_dpp(acc[r][m]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (lane == r * MT + m && n0 + r < N && m0 + m < M) {
+                float v = acc[r][m] * ep_scale + ep_bias;
+                v = apply_act(v, fz.act);
+                if (fz.res) v += ep_res;
+                store_y<TY>(y + (int64_t)(m0 + m) * ldy + n0 + r, v);
+            }
         }
-    }
 }
 
 // Fallback for any shape or alignment: one wavefront per output (m, n),
@@ -625,13 +639,14 @@ constexpr bool direct_fits() {
     return UM * MT * (XB >= 16 ? XB / 16 : 1) * 4 <= 128;
 }
 
-template <int MT, int UM, int FMT, typename TX, typename TY, bool LNF>
+template <int MT, int UM, int R, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct(const LinearArgs& a, int& rc) {
     if constexpr (direct_fits<MT, UM, FMT, TX, LNF>()) {
-        const dim3 grid((unsigned)a.N, (unsigned)((a.M + MT - 1) / MT));
-        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, FMT, TX, TY, LNF>), grid, dim3(64), 0, a.stream, a.w,
+        const int G = (int)((a.N + R - 1) / R);
+        const dim3 grid((unsigned)G, (unsigned)((a.M + MT - 1) / MT));
+        hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, R, FMT, TX, TY, LNF>), grid, dim3(64), 0, a.stream, a.w,
                            static_cast<const TX*>(a.x), a.scale, static_cast<TY*>(a.y), (int)a.ldw, (int)a.ldx,
-                           (int)a.N, (int)a.K, (int)a.N, (int)a.M, (int)a.ldy, a.bias, a.fuse);
+                           (int)a.N, (int)a.K, G, (int)a.M, (int)a.ldy, a.bias, a.fuse);
         rc = launch_status();
         return true;
     }
@@ -640,9 +655,16 @@ bool run_direct(const LinearArgs& a, int& rc) {
 
 template <int UM, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct_mt(const LinearArgs& a, int& rc) {
-    if (a.M == 1) return run_direct<1, UM, FMT, TX, TY, LNF>(a, rc);
-    if (a.M == 2) return run_direct<2, UM, FMT, TX, TY, LNF>(a, rc);
-    return run_direct<4, UM, FMT, TX, TY, LNF>(a, rc);
+    if (a.M == 1) {
+        // two weight rows a wavefront share its activation loads: a gain on
+        // wide matrices with short rows (N >= 2048, at most two chunks a
+        // lane), a loss on narrow ones, where it halves the wavefronts
+        if constexpr (UM <= 2)
+            if (a.N >= 2048) return run_direct<1, UM, 2, FMT, TX, TY, LNF>(a, rc);
+        return run_direct<1, UM, 1, FMT, TX, TY, LNF>(a, rc);
+    }
+    if (a.M == 2) return run_direct<2, UM, 1, FMT, TX, TY, LNF>(a, rc);
+    return run_direct<4, UM, 1, FMT, TX, TY, LNF>(a, rc);
 }
 
 template <int FMT, typename TX, typename TY, bool LNF>

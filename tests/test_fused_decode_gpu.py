@@ -352,6 +352,24 @@ def test_embed_and_argmax(dev):
         assert torch.equal(out.cpu()[:2], x.argmax(-1)), cols
 
 
+@pytest.mark.parametrize("rows", [16, 17, 40])
+def test_argmax_many_rows_advances_position_once(dev, rows):
+    """More rows than the final pass has wavefronts: each row's token lands in
+    its id slot and the position advances exactly once."""
+    gen = torch.Generator().manual_seed(rows)
+    logits = torch.randn(rows, 5003, generator=gen)
+    out = torch.zeros(rows, dtype=torch.long, device=dev)
+    ids = torch.zeros(rows, 12, dtype=torch.long, device=dev)
+    p = torch.tensor([9], device=dev)
+    ws = torch.empty(int(_lib.lib().tiq_argmax_rows_workspace(rows)), dtype=torch.uint8, device=dev)
+    rc = _lib.lib().tiq_argmax_rows(logits.to(dev).data_ptr(), rows, 5003, 5003, out.data_ptr(), ids.data_ptr(), 12,
+                                    p.data_ptr(), ws.data_ptr(), ws.numel(), _st())
+    _lib.check(rc, "argmax")
+    ref = logits.argmax(-1)
+    assert torch.equal(out.cpu(), ref) and torch.equal(ids.cpu()[:, 10], ref)
+    assert int(p) == 10 and not ids.cpu()[:, :10].any() and not ids.cpu()[:, 11].any()
+
+
 def _model(cfg, dev):
     torch.manual_seed(0)
     return g.GPT(cfg).to(dev).eval()
