@@ -689,7 +689,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": "gemv_kernel (tiq_linear_w8, M=1)",
+            "kernel": "gemv_direct_kernel (tiq_linear_w8, M=1)",
             "bytes_per_launch": bytes_per_launch,
             "avg_launch_us": head["avg_launch_us"],
         },

@@ -120,7 +120,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 110; }
+extern "C" int tiq_version(void) { return 111; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
