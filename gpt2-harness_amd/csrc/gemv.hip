@@ -735,7 +735,10 @@ int dispatch_fmt(const LinearArgs& a) {
         return run_generic<FMT, TX, TY>(a);
     }
     int rc = TIQ_OK;
-    if (a.M <= 4 && try_direct<FMT, TX, TY>(a, rc)) return rc;
+    // up to 4 rows; up to 16 bf16 rows without fusions on narrow matrices
+    // (N < 2048), four rows a tile, where the batched kernel has too few tiles
+    const bool direct_rows = a.M <= 4 || (a.M <= 16 && a.N < 2048 && a.x_dtype == TIQ_BF16 && !fused);
+    if (direct_rows && try_direct<FMT, TX, TY>(a, rc)) return rc;
     const size_t row_lds = (size_t)a.K * sizeof(float);
     int mt = 4;
     while (mt > 1 && (size_t)mt * row_lds > kMaxLds) mt >>= 1;

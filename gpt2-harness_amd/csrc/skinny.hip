@@ -769,6 +769,10 @@ bool skinny_supported(const LinearArgs& a) {
     // bf16 rows: int8 weights, no LayerNorm, 16-byte rows
     const bool xbf = a.x_dtype == TIQ_BF16;
     if (xbf && (a.fmt != kW8 || a.fuse.ln_w || a.ldx % 8 != 0)) return false;
+    // up to 16 bf16 rows against fewer than 2048 weight rows: too few 32-row
+    // tiles to fill the chip (24 workgroups at N = 768); the decode GEMV's
+    // direct kernel, tiled four activation rows at a time, is faster there
+    if (xbf && a.M <= 16 && a.N < 2048) return false;
     if (!xbf && a.x_dtype != TIQ_F32) return false;
     if (a.M < kSkinnyMinRows || a.M > 64 || a.K % 32 != 0 || a.N > 0x7fffffff) return false;
     const int64_t units = (a.K / 32 + kWaves - 1) / kWaves;
