@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int K, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, int N, TY* __restrict__ y, int64_t ldy,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps, int act,
-    const float* __restrict__ res, int64_t ldr, float* __restrict__ part) {
+    const float* __restrict__ res, int64_t ldr, float* __restrict__ part, uint16_t* __restrict__ x3o) {
     constexpr int WB = (WF == kW8) ? 16 : 64;  // weight bytes a lane loads per unit
     constexpr bool PL = XM == kXPlanes;
     constexpr int kXp = ring_units<WF>();
@@ -352,6 +352,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
             for (int t = 0; t < 2; ++t)
                 if (ep_m + 16 * t < M) ep_res[t] = res[(int64_t)(ep_m + 16 * t) * ldr + ep_n];
         }
+    }
+    // planes out: thread t < 128 finishes row t / 4, columns n0 + 8 (t % 4) + 0..7
+    float4 pe_scale[2] = {make_float4(1.f, 1.f, 1.f, 1.f), make_float4(1.f, 1.f, 1.f, 1.f)};
+    float4 pe_bias[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    if (x3o) {
+        const int c8 = n0 + 8 * (threadIdx.x & 3);  // N % 32 == 0 (the host checks): in range
+        if (WF == kW8) pe_scale[0] = reinterpret_cast<const float4*>(scale + c8)[0], pe_scale[1] = reinterpret_cast<const float4*>(scale + c8)[1];
+        if (bias) pe_bias[0] = reinterpret_cast<const float4*>(bias + c8)[0], pe_bias[1] = reinterpret_cast<const float4*>(bias + c8)[1];
     }
     // LayerNorm statistics of the 32 activation rows (two-pass); its weight
     // and bias go to LDS (read there, they add no global loads to the unit
@@ -578,6 +586,46 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
 #pragma unroll
     for (int q = 0; q < 16; ++q) red[wave][r][8 * (q >> 2) + 4 * h + (q & 3)] = acc[q];
     __syncthreads();
+    if (x3o) {
+        // The tile as the next linear's operand planes: its 32 columns are
+        // unit u = n0 / 32 of that linear's K (= this N), row tile blockIdx.y;
+        // rows past M are not written (the consumer zeroes them).
+        if (threadIdx.x < 128) {
+            const int m = threadIdx.x >> 2, g = threadIdx.x & 3, gm = m0 + m;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float t = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) t += red[w][m][8 * g + i];
+                const float4 sc4 = pe_scale[i >> 2], bi4 = pe_bias[i >> 2];
+                const float sc1 = (i & 3) == 0 ? sc4.x : (i & 3) == 1 ? sc4.y : (i & 3) == 2 ? sc4.z : sc4.w;
+                const float bi1 = (i & 3) == 0 ? bi4.x : (i & 3) == 1 ? bi4.y : (i & 3) == 2 ? bi4.z : bi4.w;
+                v[i] = t * sc1 + bi1;
+            }
+            apply_act<8>(v, act);
+            if (gm < M) {
+                if constexpr (sizeof(TY) == 4) {  // fp32 rows too when asked for
+                    if (y) {
+                        float* yr = y + (int64_t)gm * ldy + n0 + 8 * g;
+                        reinterpret_cast<float4*>(yr)[0] = make_float4(v[0], v[1], v[2], v[3]);
+                        reinterpret_cast<float4*>(yr)[1] = make_float4(v[4], v[5], v[6], v[7]);
+                    }
+                }
+                uint32_t pl[3][4];
+                split3_words(v, pl);
+                const int64_t Uo = N / 32, u = blockIdx.x;
+                const int hh = g >> 1, e = g & 1;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    const int64_t blk = (((int64_t)blockIdx.y * Uo + u) * 3 + q) * 2 + e;
+                    *reinterpret_cast<uint4*>(x3o + (blk * 64 + 32 * hh + m) * 8) =
+                        make_uint4(pl[q][0], pl[q][1], pl[q][2], pl[q][3]);
+                }
+            }
+        }
+        return;
+    }
     // 1024 outputs, two per thread: m = o / 32, n = o % 32 (a row of y per 32 threads)
     float vsum[2];
 #pragma unroll
@@ -632,7 +680,7 @@ int run_skinny(const LinearArgs& a) {
         hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                            reinterpret_cast<const float*>(x3), (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
                            a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
-                           a.fuse.res, a.fuse.ldr, nullptr);
+                           a.fuse.res, a.fuse.ldr, nullptr, nullptr);
         return launch_status();
     }
     if constexpr (WF == kW8) {
@@ -640,14 +688,14 @@ int run_skinny(const LinearArgs& a) {
             hipLaunchKernelGGL((skinny_kernel<kW8, kXBf16, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                                static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale,
                                a.bias, (int)a.N, static_cast<TY*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act,
-                               a.fuse.res, a.fuse.ldr, nullptr);
+                               a.fuse.res, a.fuse.ldr, nullptr, nullptr);
             return launch_status();
         }
     }
     hipLaunchKernelGGL((skinny_kernel<WF, kXRows, TY>), grid, dim3(kWaves * 64), 0, a.stream,
                        static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias,
                        (int)a.N, static_cast<TY*>(a.y), a.ldy, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, a.fuse.act,
-                       a.fuse.res, a.fuse.ldr, nullptr);
+                       a.fuse.res, a.fuse.ldr, nullptr, nullptr);
     return launch_status();
 }
 
@@ -675,16 +723,16 @@ int run_decode_t(const LinearArgs& a, const uint16_t* x3, const float* next_ln_w
                  float next_eps, uint16_t* planes_out, float* part, int64_t S) {
     const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 31) / 32), (unsigned)S);
     const float* xp = reinterpret_cast<const float*>(x3);
-    if (!part) {  // one split and no planes: the product kernel's own epilogue writes y
+    if (!part) {  // one split: the product kernel's own epilogue writes y and / or the planes
         hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, float>), grid, dim3(kWaves * 64), 0, a.stream, xp,
                            (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N,
                            static_cast<float*>(a.y), a.ldy, nullptr, nullptr, 0.f, a.fuse.act, a.fuse.res,
-                           a.fuse.ldr, nullptr);
+                           a.fuse.ldr, nullptr, planes_out);
         return launch_status();
     }
     hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, float>), grid, dim3(kWaves * 64), 0, a.stream, xp, (int64_t)0,
                        (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N, static_cast<float*>(nullptr),
-                       (int64_t)0, nullptr, nullptr, 0.f, 0, nullptr, (int64_t)0, part);
+                       (int64_t)0, nullptr, nullptr, 0.f, 0, nullptr, (int64_t)0, part, nullptr);
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
     const float* sc = WF == kW8 ? a.scale : nullptr;
@@ -717,7 +765,11 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
     // one split, the product kernel's own epilogue
     const bool red_ok = a.N % 8 == 0 && a.N <= kRedMaxCols;
     const int64_t S = (red_ok || planes_out) ? decode_splits(a.M, a.K, a.N) : 1;
-    const bool reduce = S > 1 || planes_out;
+    // planes without a LayerNorm or residual from one split: the product
+    // kernel writes them itself (its 32 columns are one unit of the next
+    // linear's K), no reduction launch
+    const bool product_planes = planes_out && !next_ln_w && !a.fuse.res && S == 1 && a.N % 32 == 0;
+    const bool reduce = !product_planes && (S > 1 || planes_out);
     // every wavefront's share of K fits its weight registers
     const int64_t units = ((a.K / 32 + S - 1) / S + kWaves - 1) / kWaves;
     if (units > (a.fmt == kW8 ? max_units<kW8>() : max_units<kF32>())) return TIQ_EUNSUPPORTED;
@@ -726,6 +778,10 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
                  : (!a.x || !aligned(a.x, 16) || a.ldx % 4 != 0 ||
                     (a.fuse.ln_w && (!aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16)))))
         return x_planes || a.x ? TIQ_EALIGN : TIQ_EINVAL;
+    if (product_planes &&
+        (!aligned(planes_out, 16) || (a.y && (!aligned(a.y, 16) || a.ldy % 4 != 0)) ||
+         (a.fmt == kW8 && !aligned(a.scale, 16)) || (a.bias && !aligned(a.bias, 16))))
+        return TIQ_EALIGN;
     if (reduce) {  // the reduction's 16-byte row accesses and its 8192-column reach
         if (a.N % 8 != 0 || a.N > kRedMaxCols) return TIQ_EUNSUPPORTED;
         if ((a.y && (!aligned(a.y, 16) || a.ldy % 4 != 0)) ||

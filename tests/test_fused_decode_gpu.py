@@ -493,6 +493,32 @@ def test_decode_linear_chain_through_planes(dev, c_oracle, M):
     _f64_check(y3, r0 + OL.linear_ref(h32, w3, b3), r0.double() + h64 @ w3.double().T + b3.double())
 
 
+@pytest.mark.parametrize("M", [5, 32, 40])
+def test_decode_linear_product_writes_planes(dev, c_oracle, M):
+    """One split, planes out without a LayerNorm (the c_fc of a block): the
+    product kernel writes the fp32 rows and the planes itself. The planes are
+    exactly the split of those rows: a projection from them equals the
+    projection from the rows bit for bit."""
+    C, H = 1600, 6400
+    gen = torch.Generator().manual_seed(M + 7)
+    q2, s2, w2 = _w8(c_oracle, H, C, gen, dev)
+    q3, s3, _ = _w8(c_oracle, C, H, gen, dev)
+    b2 = 0.1 * torch.randn(H, generator=gen)
+    x = torch.randn(M, C, generator=gen)
+    L = _lib.lib()
+    pb = torch.empty(int(L.tiq_decode_planes_bytes(M, H)), dtype=torch.uint8, device=dev)
+    h = torch.empty(M, H, device=dev)
+    _lib.check(_dl(x.to(dev), None, M, C, q2, _lib.WF_INT8, s2, b2.to(dev), H, h, act=_lib.ACT_GELU_TANH, planes=pb),
+               "gelu rows + planes")
+    h64 = _gelu(x.double() @ w2.double().T + b2.double())
+    _f64_check(h, _gelu(OL.linear_ref(x, w2, b2)), h64)
+    a = torch.empty(M, C, device=dev)
+    b = torch.empty(M, C, device=dev)
+    _lib.check(_dl(None, pb, M, H, q3, _lib.WF_INT8, s3, None, C, a), "from planes")
+    _lib.check(_dl(h, None, M, H, q3, _lib.WF_INT8, s3, None, C, b), "from rows")
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("M", [6, 32])
 def test_decode_linear_fp32_weights_and_errors(dev, M):
     """fp32 weights (the head) from planes, N not a multiple of 8 (one split,
