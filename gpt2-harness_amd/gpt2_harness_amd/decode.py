@@ -69,7 +69,7 @@ class _DecoderBase:
         from .model import KVCache
 
         cache = KVCache.empty(self.cfg.n_layer)
-        logits = self.model(idx, cache=cache)["logits"][:, -1, :]
+        logits = self.model(idx, cache=cache, last_only=True)["logits"][:, -1, :]
         for i in range(self.cfg.n_layer):
             self.k[i][:, :, :T0].copy_(cache.keys[i])
             self.v[i][:, :, :T0].copy_(cache.values[i])

@@ -217,7 +217,12 @@ class GPT(nn.Module):
         cache: KVCache | None = None,
         need_weights: bool = False,
         collect_taps: bool = False,
+        last_only: bool = False,
     ) -> dict[str, Any]:
+        """``model.py:528-599``. ``last_only`` (an extension; the reference
+        always computes every position) returns logits ``(B, 1, V)`` of the
+        last position only, for a prefill that needs nothing else: the head
+        is the largest product of a long prompt."""
         if collect_taps:
             raise NotImplementedError("activation taps belong to the verification tooling, not this library")
         _, T = idx.shape
@@ -234,6 +239,10 @@ class GPT(nn.Module):
             x, probs = block(x, cache=cache, need_weights=need_weights)
             if probs is not None:
                 attentions.append(probs)
+        if last_only:
+            if targets is not None:
+                raise ValueError("last_only computes no loss: the loss needs every position's logits")
+            x = x[:, -1:, :]
         logits = self.lm_head(self.ln_f(x))
         out: dict[str, Any] = {"logits": logits}
         if need_weights:

@@ -145,3 +145,19 @@ def test_synthetic_token_stream_windows():
         g.SyntheticTokenStream(50, T + 1, T)
     with pytest.raises(ValueError):
         ds.sequential_batches("test", batch_size=4)
+
+
+def test_last_only_logits_equal_the_last_row():
+    """``last_only`` (used by the decoders' prefill) gives the last position's
+    logits of the full forward; it refuses a loss, which needs every row."""
+    torch.manual_seed(0)
+    cfg = g.GPTConfig(vocab_size=64, n_positions=24, n_layer=2, n_head=4, n_embd=32)
+    m = g.GPT(cfg).eval()
+    idx = torch.randint(0, 64, (3, 10))
+    with torch.no_grad():
+        full = m(idx)["logits"]
+        last = m(idx, last_only=True)["logits"]
+    assert last.shape == (3, 1, 64)
+    assert torch.allclose(last[:, 0], full[:, -1], atol=1e-6, rtol=1e-5)
+    with pytest.raises(ValueError):
+        m(idx, targets=idx, last_only=True)
