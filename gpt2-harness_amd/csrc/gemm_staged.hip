@@ -247,9 +247,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
                         if constexpr (sizeof(TY) == 4) {
                             *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
                         } else {
+                            // v_cvt_pk_bf16_f32 (round to nearest even, two values an
+                            // instruction): the bit-level software rounding cost six
+                            // instructions a value, ~60% of a 256 x 256 tile's epilogue
                             uint2 o;
-                            o.x = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
-                            o.y = (uint32_t)f32_to_bf16_bits(v2) | ((uint32_t)f32_to_bf16_bits(v3) << 16);
+                            o.x = pk_bf16(v0, v1);
+                            o.y = pk_bf16(v2, v3);
                             *reinterpret_cast<uint2*>(dst + 8 * (nl % UNIT != 0)) = o;
                         }
                     }
@@ -297,20 +300,23 @@ bool staged_supported_impl(const LinearArgs& a) {
 }
 
 // Tile choice: rounds of co-resident workgroups (256x256 and 256x128 tiles
-// need most of a CU's LDS and registers: one per CU; 128x128 tiles fit two)
-// times the duration of one round, modelled as step_us per k64 step plus a
-// fixed term, both fitted to MI355X measurements of this kernel at the
-// GPT-2-XL Linear shapes with M = 4096 (all 256 CUs busy).
+// need most of a CU's LDS and registers: one per CU; 128x128 tiles fit two,
+// whose rounds overlap: counted in halves) times the duration of one round,
+// modelled as step_us per k64 step plus a fixed term (prologue and epilogue),
+// both fitted to MI355X measurements of this kernel at the GPT-2-XL Linear
+// shapes with M = 4096 (per-workgroup timestamps: prologue 2-3 us, epilogue
+// 1.5-5 us by tile size).
 int staged_choice(int64_t M, int64_t N, int64_t K) {
     struct Opt { int bm, bn, per_cu; double step_us, fixed_us; };
-    static const Opt opts[] = {{256, 256, 1, 1.29, 23.0}, {256, 128, 1, 0.87, 8.4}, {128, 128, 2, 1.07, 0.5}};
+    static const Opt opts[] = {{256, 256, 1, 1.43, 8.7}, {256, 128, 1, 0.893, 5.9}, {128, 128, 2, 1.073, 3.7}};
     const double nk = (double)(K / BK);
     int best = 0;
     double best_t = 1e30;
     for (int o = 0; o < 3; ++o) {
         const int64_t tiles = ((M + opts[o].bm - 1) / opts[o].bm) * ((N + opts[o].bn - 1) / opts[o].bn);
         const int64_t slots = 256 * opts[o].per_cu;
-        const double rounds = (double)((tiles + slots - 1) / slots);
+        const double rounds = opts[o].per_cu == 1 ? (double)((tiles + slots - 1) / slots)
+                                                  : 0.5 * (double)((2 * tiles + slots - 1) / slots);
         const double t = rounds * (nk * opts[o].step_us + opts[o].fixed_us);
         if (t < best_t) { best_t = t; best = o; }
     }
@@ -343,8 +349,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
         *reinterpret_cast<float4*>(yr) = make_float4(o0, o1, o2, o3);
     } else {
         uint2 o;
-        o.x = (uint32_t)f32_to_bf16_bits(o0) | ((uint32_t)f32_to_bf16_bits(o1) << 16);
-        o.y = (uint32_t)f32_to_bf16_bits(o2) | ((uint32_t)f32_to_bf16_bits(o3) << 16);
+        o.x = pk_bf16(o0, o1);
+        o.y = pk_bf16(o2, o3);
         *reinterpret_cast<uint2*>(yr) = o;
     }
 }

@@ -61,23 +61,21 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ x, int64_t ldx, in
     if (i >= (int64_t)M * k4) return;
     const int m = (int)(i / k4), k = (int)(i % k4) * 4;
     const float4 v = *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k);
-    const float in[4] = {v.x, v.y, v.z, v.w};
-    uint16_t p[3][4];
+    // pairs through v_cvt_pk_bf16_f32 (round to nearest even)
+    uint32_t p[3][2];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint16_t hi = f32_to_bf16_bits(in[e]);
-        const float r1 = in[e] - bf16_bits_to_f32(hi);
-        const uint16_t lo = f32_to_bf16_bits(r1);
-        const float r2 = r1 - bf16_bits_to_f32(lo);
+    for (int e = 0; e < 2; ++e) {
+        const float x0 = e ? v.z : v.x, x1 = e ? v.w : v.y;
+        const uint32_t hi = pk_bf16(x0, x1);
+        const float r0 = x0 - bf_lo(hi), r1 = x1 - bf_hi(hi);
+        const uint32_t lo = pk_bf16(r0, r1);
         p[0][e] = hi;
         p[1][e] = lo;
-        p[2][e] = f32_to_bf16_bits(r2);
+        p[2][e] = pk_bf16(r0 - bf_lo(lo), r1 - bf_hi(lo));
     }
     uint16_t* row = x3 + (int64_t)m * 3 * K + k;
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
-        *reinterpret_cast<uint2*>(row + (int64_t)q * K) =
-            make_uint2((uint32_t)p[q][0] | ((uint32_t)p[q][1] << 16), (uint32_t)p[q][2] | ((uint32_t)p[q][3] << 16));
+    for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2*>(row + (int64_t)q * K) = make_uint2(p[q][0], p[q][1]);
 }
 
 size_t split_workspace(int64_t M, int64_t K) { return (size_t)(M * 3 * K * 2 + 255) / 256 * 256; }
