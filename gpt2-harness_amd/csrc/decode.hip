@@ -59,18 +59,25 @@ __device__ __forceinline__ void store_planes(uint16_t* x3, int64_t m, int64_t Kc
     }
 }
 
-template <int NCH>
+// WHOLE: the descriptors cover the whole cache (t_max slots) rather than the
+// pos filled ones, so the first loads need not wait for pos -- for small caches
+// (batch 1), where the unused tail costs less than that wait; the slots past
+// pos are dropped where they are used either way.
+// Grid (head, sequence). The arguments up to t_max are the ones the loads
+// need, in the 14 dwords preloaded into SGPRs.
+template <int NCH, bool WHOLE>
 __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
-    const float* __restrict__ qkv, int64_t ld_qkv, int H, int Hkv, float* __restrict__ kc, float* __restrict__ vc,
-    int t_max, const int64_t* __restrict__ pos_p, float* __restrict__ y, int64_t ldy, uint16_t* __restrict__ x3) {
+    const float* __restrict__ qkv, const int64_t* __restrict__ pos_p, float* __restrict__ kc, float* __restrict__ vc,
+    int ld_qkv, int H, int Hkv, int group, int t_max, float* __restrict__ y, int64_t ldy,
+    uint16_t* __restrict__ x3) {
     constexpr int W = kAttWaves, NI = kLoadsPerChunk;
     __shared__ float qn[kHeadDim], kn[kHeadDim], vn[kHeadDim];
     __shared__ float sc[kMaxSlots];
     __shared__ float red[W];
     __shared__ float4 part[W][4][16];
     __shared__ float ov[kHeadDim];
-    const int b = blockIdx.x / H, h = blockIdx.x % H;
-    const int group = H / Hkv, hk = h / group;
+    const int h = blockIdx.x, b = blockIdx.y;  // no integer division on the way to the first loads
+    const int hk = group == 1 ? h : h / group;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int row = lane >> 4, d4 = (lane & 15) * 4;  // slot within the load, first of 4 dims
     const float* qr = qkv + (int64_t)b * ld_qkv;
@@ -78,18 +85,11 @@ __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
     float* kb = kc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
     float* vb = vc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
 
-    const int64_t pos = *pos_p;
-    if (pos < 0 || pos >= t_max) {  // position outside the cache: flag the output, write nothing else
-        if (tid < kHeadDim) y[(int64_t)b * ldy + h * kHeadDim + tid] = NAN;
-        if (x3 && tid < kHeadDim / 8) {
-            float nan8[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) nan8[i] = NAN;
-            store_planes(x3, b, H * kHeadDim, h * kHeadDim + 8 * tid, nan8);
-        }
-        return;
-    }
-    const int valid = (int)pos * kHeadDim * 4;  // bytes of slots 0 .. pos - 1
+    int64_t pos_in = 0;
+    if constexpr (!WHOLE) pos_in = *pos_p;  // the descriptors need it
+    // bytes of slots 0 .. pos - 1 (0 for a position outside the cache)
+    const int valid =
+        WHOLE ? t_max * kHeadDim * 4 : (pos_in < 0 || pos_in >= t_max ? 0 : (int)pos_in * kHeadDim * 4);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kb, (short)0, valid, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vb, (short)0, valid, 0x00020000);
     const int off0 = ((kSlotsPerWave * wave + row) * kHeadDim + d4) * 4;
@@ -105,6 +105,11 @@ __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
         for (int i = 0; i < NI; ++i) vr[0][i] = cache_load(rv, slot_off(0, i));
     }
     const float4 q4 = *reinterpret_cast<const float4*>(qr + h * kHeadDim + d4);
+    if constexpr (WHOLE) pos_in = *pos_p;  // read behind the loads, which do not need it
+    // A position outside the cache computes on slot 0, writes nothing to the
+    // cache and stores NaN: no branch, so no load is sunk behind the read of pos.
+    const bool ok = pos_in >= 0 && pos_in < t_max;
+    const int64_t pos = ok ? pos_in : 0;
     if (tid < kHeadDim) {
         const float q_new = qr[h * kHeadDim + tid];
         const float k_new = qr[C + hk * kHeadDim + tid];
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
         qn[tid] = q_new;
         kn[tid] = k_new;
         vn[tid] = v_new;
-        if (h % group == 0) {  // one writer per kv head; no workgroup reads slot pos from the cache
+        if (ok && (group == 1 || h % group == 0)) {  // one writer per kv head; no workgroup reads slot pos
             kb[pos * kHeadDim + tid] = k_new;
             vb[pos * kHeadDim + tid] = v_new;
         }
@@ -205,8 +210,9 @@ __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
         for (int w = 0; w < W; ++w)
 #pragma unroll
             for (int r = 0; r < 4; ++r) o += pf[(w * 4 + r) * 64 + tid];
-        y[(int64_t)b * ldy + h * kHeadDim + tid] = o / sum;
-        ov[tid] = o / sum;
+        const float r = ok ? o / sum : NAN;  // a position outside the cache flags the output
+        y[(int64_t)b * ldy + h * kHeadDim + tid] = r;
+        ov[tid] = r;
     }
     if (x3) {  // the head's 64 outputs as the operand planes of the output projection
         __syncthreads();
@@ -316,14 +322,18 @@ static int decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int
     if (!qkv || !k_cache || !v_cache || !pos || !y) return TIQ_EINVAL;
     if (head_dim != kHeadDim || t_max <= 0 || t_max > kMaxSlots) return TIQ_EUNSUPPORTED;
     if (ld_qkv < (n_head + 2 * n_kv_head) * head_dim || ldy < n_head * head_dim) return TIQ_EINVAL;
+    // the kernel takes the row stride as 32 bits and the sequence as grid row
+    if (ld_qkv > INT32_MAX || batch > 65535 || n_head > 65535) return TIQ_EUNSUPPORTED;
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || (planes_out && !aligned(planes_out, 16))) return TIQ_EALIGN;
-    const dim3 grid((unsigned)(batch * n_head)), block(64 * kAttWaves);
-    if (t_max <= 128)
-        hipLaunchKernelGGL(decode_attention_kernel<1>, grid, block, 0, as_stream(stream), qkv, ld_qkv, (int)n_head,
-                           (int)n_kv_head, k_cache, v_cache, (int)t_max, pos, y, ldy, planes_out);
-    else
-        hipLaunchKernelGGL(decode_attention_kernel<2>, grid, block, 0, as_stream(stream), qkv, ld_qkv, (int)n_head,
-                           (int)n_kv_head, k_cache, v_cache, (int)t_max, pos, y, ldy, planes_out);
+    const dim3 grid((unsigned)n_head, (unsigned)batch), block(64 * kAttWaves);
+    // a small cache (keys and values of the layer under 32 MB) is read whole
+    const bool whole = batch * n_kv_head * t_max * kHeadDim * 4 * 2 <= (32ll << 20);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, as_stream(stream), qkv, pos, k_cache, v_cache, (int)ld_qkv,
+                           (int)n_head, (int)n_kv_head, (int)(n_head / n_kv_head), (int)t_max, y, ldy, planes_out);
+    };
+    if (t_max <= 128) whole ? launch(decode_attention_kernel<1, true>) : launch(decode_attention_kernel<1, false>);
+    else whole ? launch(decode_attention_kernel<2, true>) : launch(decode_attention_kernel<2, false>);
     return launch_status();
 }
 
