@@ -16,57 +16,159 @@
 namespace tiq {
 namespace {
 
-constexpr int kRowsPerBlock = 4;  // one wavefront per row, four per workgroup
+// ------------------------------------------------------------- helpers
+// max over each 16-lane row of the wavefront, in every lane of the row
+// (DPP moves: pairs, quads, half rows, rows). All 64 lanes must be active.
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x, uint32_t keep) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)keep, (int)x, CTRL, ROW_MASK, 0xf, false);
+}
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    v = umax(v, dpp_u32<0xB1>(v, 0u));   // quad_perm [1, 0, 3, 2]
+    v = umax(v, dpp_u32<0x4E>(v, 0u));   // quad_perm [2, 3, 0, 1]
+    v = umax(v, dpp_u32<0x141>(v, 0u));  // row_half_mirror
+    v = umax(v, dpp_u32<0x140>(v, 0u));  // row_mirror
+    return v;
+}
+// max over lanes 0-31 in lane 31 and over lanes 32-63 in lane 63
+// (row_bcast:15 adds row 0 into row 1 and row 2 into row 3).
+__device__ __forceinline__ uint32_t half_max_u32(uint32_t v) {
+    v = row16_max_u32(v);
+    return umax(v, dpp_u32<0x142, 0xa>(v, v));
+}
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+    v = half_max_u32(v);
+    v = umax(v, dpp_u32<0x143, 0xc>(v, v));  // row_bcast:31 into rows 2 and 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// v_cvt_i32_f32: round-toward-zero conversion that saturates out-of-range
+// values and maps NaN to 0 (defined for every input, unlike a C++ cast).
+__device__ __forceinline__ int cvt_i32_sat(float f) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+    return r;
+}
+
+// A row as a buffer resource of `bytes` bytes: 16-byte loads past it return
+// zeros and make no memory access, so every load of a row is issued without a
+// bounds branch (a branch per load makes the compiler wait for each load
+// before the next is issued).
+typedef float tiq_qf32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 row_load(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    const tiq_qf32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Codes of four values, clamp(rint(w / s), qmin, qmax) with w / s the
+// correctly rounded quotient, computed as rint(w * inv), inv = 1 / s
+// correctly rounded. For |w / s| <= 130 the exact product w * inv is within
+// 130 * 2^-23 < 2^-15.9 of the rounded quotient and its own rounding within
+// 2^-17, so the rounded product and the quotient round to the same integer
+// unless w * inv lies within 2^-14 of a half-integer. Beyond 130 a wrong
+// neighbour would still clamp to the same end (qmax <= 127, qmin >= -128),
+// and past 2^23 both are the same integer. Only groups of four with a value
+// near a half-integer (about one in 2000) take the exact division, so the
+// codes equal the per-element division's. Infinite and NaN products give
+// the quotient's codes through the saturating conversion (inf -> the clamp
+// end, NaN -> 0), whichever branch they take.
+__device__ __forceinline__ void codes4(const float4& v, float s, float inv, int qmin, int qmax, int (&c)[4]) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    float t[4], e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        t[k] = __builtin_rintf(x[k] * inv);
+        e[k] = fabsf(fabsf(__builtin_fmaf(x[k], inv, -t[k])) - 0.5f);  // exact w*inv - t, rounded once
+    }
+    const float emin = fminf(fminf(e[0], e[1]), fminf(e[2], e[3]));
+    if (!(emin > 0x1p-14f)) {
+        asm volatile("");  // a real branch: the divisions run only in waves that need them
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] = __builtin_rintf(x[k] / s);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int q = max(cvt_i32_sat(t[k]), qmin);
+        c[k] = min(q, qmax);
+    }
+}
 
 // ----------------------------------------------------------- per-channel
-// One wavefront per row, the row held in registers as VPL float4 per lane
-// (columns lane*4 + 256*i). Needs cols % 4 == 0 and 16-byte aligned rows.
+// WPR wavefronts per row, 4 / WPR rows per 256-thread workgroup; the row held
+// in registers as V float4 per lane (float4 index (sub*64 + lane) + 64*WPR*i
+// for wavefront `sub` of the row), so each load instruction reads 1 KB of
+// consecutive memory. |max| per wavefront with DPP moves, across the row's
+// wavefronts through LDS. Needs cols % 4 == 0 and 16-byte aligned rows.
 // Out = int8 codes (PACK == false, 4 codes per 32-bit store) or the
 // reference's nibble packing (PACK == true, 2 bytes per float4).
-template <int VPL, bool PACK>
+template <int V, int WPR, bool PACK>
 __global__ __launch_bounds__(256) void quant_rows_vec(const float* __restrict__ w, int64_t rows,
                                                       int cols, int64_t ldw, float qmin, float qmax,
                                                       uint8_t* __restrict__ out, int64_t ldq,
                                                       float* __restrict__ scale) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= rows) return;  // wave-uniform
-    const float4* wr = reinterpret_cast<const float4*>(w + row * ldw);
-    const int nv = cols >> 2;
-    float4 v[VPL];
+    constexpr int kRows = 4 / WPR;
+    __shared__ uint32_t red[4];
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x >> 6, sub = wv % WPR;
+    const int64_t row = (int64_t)blockIdx.x * kRows + wv / WPR;
+    const bool valid = row < rows;  // wave-uniform; no early return before the barrier
+    const __amdgpu_buffer_rsrc_t wr = row_rsrc(w + (valid ? row : 0) * ldw, valid ? cols * 4 : 0);
+    const int nv = valid ? cols >> 2 : 0;
+    float4 v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = row_load(wr, (sub * kWave + lane + kWave * WPR * i) * 16);
     uint32_t m = 0;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        const int idx = lane + kWave * i;
-        if (idx < nv) {
-            v[i] = wr[idx];
-            uint32_t a = abs_bits(v[i].x), b = abs_bits(v[i].y), c = abs_bits(v[i].z), d = abs_bits(v[i].w);
-            a = a > b ? a : b;
-            c = c > d ? c : d;
-            a = a > c ? a : c;
-            m = a > m ? a : m;
-        }
+    for (int i = 0; i < V; ++i) {
+        const uint32_t a = abs_bits(v[i].x), b = abs_bits(v[i].y), c = abs_bits(v[i].z), d = abs_bits(v[i].w);
+        m = umax(m, umax(umax(a, b), umax(c, d)));
     }
-    m = wave_max_u32(m);
-    const float s = scale_from_amax(__uint_as_float(m), qmax);
-    if (lane == 0) scale[row] = s;
+    m = wave_max_u32_dpp(m);
+    if (WPR > 1) {
+        if (lane == 0) red[wv] = m;
+        __syncthreads();
+        m = red[wv - sub];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        const int idx = lane + kWave * i;
+        for (int j = 1; j < WPR; ++j) m = umax(m, red[wv - sub + j]);
+    }
+    const float s = scale_from_amax(__uint_as_float(m), qmax);
+    const float inv = 1.0f / s;
+    if (valid && sub == 0 && lane == 0) scale[row] = s;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int idx = sub * kWave + lane + kWave * WPR * i;
         if (idx < nv) {
-            const int c0 = code_of(v[i].x, s, qmin, qmax), c1 = code_of(v[i].y, s, qmin, qmax);
-            const int c2 = code_of(v[i].z, s, qmin, qmax), c3 = code_of(v[i].w, s, qmin, qmax);
+            int c[4];
+            codes4(v[i], s, inv, (int)qmin, (int)qmax, c);
             if (PACK) {
-                const uint16_t b = (uint16_t)(((c0 + 8) & 0xf) | (((c1 + 8) & 0xf) << 4) |
-                                              (((c2 + 8) & 0xf) << 8) | (((c3 + 8) & 0xf) << 12));
+                const uint16_t b = (uint16_t)(((c[0] + 8) & 0xf) | (((c[1] + 8) & 0xf) << 4) |
+                                              (((c[2] + 8) & 0xf) << 8) | (((c[3] + 8) & 0xf) << 12));
                 reinterpret_cast<uint16_t*>(out + row * (int64_t)(cols >> 1))[idx] = b;
             } else {
-                const uint32_t b = (uint32_t)(c0 & 0xff) | ((uint32_t)(c1 & 0xff) << 8) |
-                                   ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
+                const uint32_t b = (uint32_t)(c[0] & 0xff) | ((uint32_t)(c[1] & 0xff) << 8) |
+                                   ((uint32_t)(c[2] & 0xff) << 16) | ((uint32_t)(c[3] & 0xff) << 24);
                 reinterpret_cast<uint32_t*>(out + row * ldq)[idx] = b;
             }
         }
     }
+}
+
+// Wavefronts per row for a row of nv float4: the fewest that keep at most 8
+// float4 per lane (32 with 4 wavefronts) and give at least 4096 wavefronts
+// (4 per SIMD), else the most that fit; 0 when none fits.
+int rows_split(int64_t rows, int64_t nv, int* per_lane) {
+    int best = 0;
+    for (int wpr = 1; wpr <= 4; wpr *= 2) {
+        const int64_t pl = (nv + 64 * wpr - 1) / (64 * wpr);
+        if (pl > (wpr == 4 ? 32 : 8)) continue;
+        best = wpr;
+        *per_lane = (int)pl;
+        if (rows * wpr >= 4096) break;
+    }
+    return best;
 }
 
 // Any shape / alignment: one workgroup per row, two passes over the row
@@ -108,25 +210,28 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const float* __restric
 int launch_quant_rows(const float* w, int64_t rows, int64_t cols, int64_t ldw, int bits, uint8_t* out,
                       int64_t ldq, float* scale, bool pack, hipStream_t st) {
     const float qmax = (float)((1 << (bits - 1)) - 1), qmin = (float)(-(1 << (bits - 1)));
+    const int64_t nv = cols / 4;
+    int per_lane = 0;
+    const int wpr = rows_split(rows, nv, &per_lane);
     const bool vec = (cols % 4 == 0) && (ldw % 4 == 0) && aligned(w, 16) &&
-                     (pack || ((ldq % 4 == 0) && aligned(out, 4))) && (!pack || aligned(out, 2)) &&
-                     cols <= 64 * 4 * 32;
+                     (pack || ((ldq % 4 == 0) && aligned(out, 4))) && (!pack || aligned(out, 2)) && wpr > 0;
     if (!vec) {
         if (pack) hipLaunchKernelGGL(quant_rows_generic<true>, dim3((unsigned)rows), dim3(256), 0, st, w, rows, cols, ldw, qmin, qmax, out, ldq, scale);
         else hipLaunchKernelGGL(quant_rows_generic<false>, dim3((unsigned)rows), dim3(256), 0, st, w, rows, cols, ldw, qmin, qmax, out, ldq, scale);
         return launch_status();
     }
-    const int nv = (int)(cols / 4);
-    const int per_lane = (nv + kWave - 1) / kWave;
-    const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)), block(256);
+    const int rpb = 4 / wpr;
+    const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(256);
     const int c = (int)cols;
-#define TIQ_QR(V)                                                                                             \
-    if (per_lane <= V) {                                                                                      \
-        if (pack) hipLaunchKernelGGL((quant_rows_vec<V, true>), grid, block, 0, st, w, rows, c, ldw, qmin, qmax, out, ldq, scale); \
-        else hipLaunchKernelGGL((quant_rows_vec<V, false>), grid, block, 0, st, w, rows, c, ldw, qmin, qmax, out, ldq, scale);    \
-        return launch_status();                                                                               \
+#define TIQ_QR(V, W)                                                                                              \
+    if (wpr == W && per_lane <= V) {                                                                              \
+        if (pack) hipLaunchKernelGGL((quant_rows_vec<V, W, true>), grid, block, 0, st, w, rows, c, ldw, qmin, qmax, out, ldq, scale); \
+        else hipLaunchKernelGGL((quant_rows_vec<V, W, false>), grid, block, 0, st, w, rows, c, ldw, qmin, qmax, out, ldq, scale);    \
+        return launch_status();                                                                                   \
     }
-    TIQ_QR(1) TIQ_QR(2) TIQ_QR(4) TIQ_QR(8) TIQ_QR(16) TIQ_QR(32)
+    TIQ_QR(1, 1) TIQ_QR(2, 1) TIQ_QR(4, 1) TIQ_QR(8, 1)
+    TIQ_QR(1, 2) TIQ_QR(2, 2) TIQ_QR(4, 2) TIQ_QR(8, 2)
+    TIQ_QR(1, 4) TIQ_QR(2, 4) TIQ_QR(4, 4) TIQ_QR(8, 4) TIQ_QR(16, 4) TIQ_QR(32, 4)
 #undef TIQ_QR
     return TIQ_EUNSUPPORTED;
 }
@@ -212,42 +317,73 @@ int partial_blocks(int64_t n) {
 }
 
 // ----------------------------------------------------------- group-wise
-// Group-wise int4, group 128, one wavefront per row: a group is 32 float4,
-// i.e. one half of the wavefront in iteration i (lanes 0-31: group 2i,
-// lanes 32-63: group 2i+1), so the group max is a half-wave reduction.
-template <int VPL>
-__global__ __launch_bounds__(256) void quant_g128_vec(const float* __restrict__ w, int64_t rows, int cols,
-                                                      uint8_t* __restrict__ packed,
-                                                      uint16_t* __restrict__ scale16) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float4* wr = reinterpret_cast<const float4*>(w + row * (int64_t)cols);
-    const int nv = cols >> 2;
-    const int ngroups = (cols + 127) >> 7;
-    uint16_t* prow = reinterpret_cast<uint16_t*>(packed + row * (int64_t)(cols >> 1));
+// Group-wise int4, group 128, over the flattened (row, group) space: eight
+// lanes per group, a wavefront takes 8 * U consecutive groups (U rounds of 8,
+// in the same or the next rows). Lane 8 * lg + sl of round u holds float4
+// sl + 8 j (j < 4) of group 8 u + lg, so each load instruction reads whole
+// 128-byte lines; the group max is a DPP reduction over 8 lanes and the
+// scale (two divisions) is computed once per 16 values of a lane. The
+// weight is one buffer resource: loads past a group's end (a ragged last
+// group) or past the last row go to an offset beyond it and return zeros.
+template <int U>
+__global__ __launch_bounds__(256) void quant_g128_groups(const float* __restrict__ w, int rows, int cols, int ng,
+                                                         uint8_t* __restrict__ packed,
+                                                         uint16_t* __restrict__ scale16) {
+    const int lane = threadIdx.x & (kWave - 1), sl = lane & 7, lg = lane >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+    const uint32_t gid0 = (uint32_t)wave * 8u * U;  // rows * ng + 64 < 2^31 (checked by the launcher)
+    const int r0 = (int)(gid0 / (uint32_t)ng), g0 = (int)(gid0 % (uint32_t)ng);
+    const __amdgpu_buffer_rsrc_t wr = row_rsrc(w, rows * cols * 4);
+    int r[U], g[U], nq[U];
+    uint32_t base[U];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        const int idx = lane + kWave * i;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        uint32_t m = 0;
-        if (idx < nv) {
-            v = wr[idx];
-            uint32_t a = abs_bits(v.x), b = abs_bits(v.y), c = abs_bits(v.z), d = abs_bits(v.w);
-            a = a > b ? a : b;
-            c = c > d ? c : d;
-            m = a > c ? a : c;
+    for (int u = 0; u < U; ++u) {  // every group's place first, so all loads issue together
+        int gg = g0 + 8 * u + lg, rr = r0;
+        while (gg >= ng) {
+            gg -= ng;
+            ++rr;
         }
-        m = group_max_u32<32>(m);
+        r[u] = rr;
+        g[u] = gg;
+        nq[u] = rr < rows ? min(32, (cols - gg * 128) >> 2) : 0;  // float4 in the group
+        base[u] = ((uint32_t)rr * (uint32_t)cols + (uint32_t)gg * 128u) * 4u;
+    }
+    float4 v[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = sl + 8 * j;
+            v[u][j] = row_load(wr, (int)(f < nq[u] ? base[u] + (uint32_t)f * 16u : 0x7ffffff0u));
+        }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first wait
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            m = umax(m, umax(umax(abs_bits(v[u][j].x), abs_bits(v[u][j].y)),
+                             umax(abs_bits(v[u][j].z), abs_bits(v[u][j].w))));
+        m = umax(m, dpp_u32<0xB1>(m, 0u));   // quad_perm [1, 0, 3, 2]
+        m = umax(m, dpp_u32<0x4E>(m, 0u));   // quad_perm [2, 3, 0, 1]
+        m = umax(m, dpp_u32<0x141>(m, 0u));  // row_half_mirror: the 8 lanes of the group
         uint16_t h = f32_to_f16_bits(__uint_as_float(m) / 7.0f);
         if (h == 0) h = 1;
         if (h > 0x7bffu) h = 0x7bffu;
         const float s = f16_bits_to_f32(h);
-        if (idx < nv) {
-            if ((idx & 31) == 0) scale16[row * ngroups + (idx >> 5)] = h;
-            const int c0 = code_of(v.x, s, -8.f, 7.f) + 8, c1 = code_of(v.y, s, -8.f, 7.f) + 8;
-            const int c2 = code_of(v.z, s, -8.f, 7.f) + 8, c3 = code_of(v.w, s, -8.f, 7.f) + 8;
-            prow[idx] = (uint16_t)(c0 | (c1 << 4) | (c2 << 8) | (c3 << 12));
+        const float inv = 1.0f / s;
+        if (nq[u] > 0) {
+            if (sl == 0) scale16[(int64_t)r[u] * ng + g[u]] = h;
+            uint16_t* pg = reinterpret_cast<uint16_t*>(packed + (int64_t)r[u] * (cols >> 1) + g[u] * 64);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = sl + 8 * j;
+                if (f < nq[u]) {
+                    int c[4];
+                    codes4(v[u][j], s, inv, -8, 7, c);
+                    pg[f] = (uint16_t)((c[0] + 8) | ((c[1] + 8) << 4) | ((c[2] + 8) << 8) | ((c[3] + 8) << 12));
+                }
+            }
         }
     }
 }
@@ -417,19 +553,18 @@ extern "C" int tiq_quantize_groupwise_int4(const float* w, int64_t rows, int64_t
     if (rows == 0) return TIQ_OK;
     if (!w || !packed || !scale_f16) return TIQ_EINVAL;
     hipStream_t st = as_stream(stream);
-    const int64_t nv = cols / 4;
-    if (group == 128 && cols % 4 == 0 && aligned(w, 16) && aligned(packed, 2) && nv <= 64 * 32 &&
-        rows <= 0x7fffffffLL) {
-        const int per_lane = (int)((nv + 63) / 64);
-        const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)), block(256);
-        const int c = (int)cols;
-#define TIQ_QG(V)                                                                                      \
-    if (per_lane <= V) {                                                                               \
-        hipLaunchKernelGGL((quant_g128_vec<V>), grid, block, 0, st, w, rows, c, packed, scale_f16); \
-        return launch_status();                                                                        \
-    }
-        TIQ_QG(1) TIQ_QG(2) TIQ_QG(4) TIQ_QG(8) TIQ_QG(16) TIQ_QG(32)
-#undef TIQ_QG
+    const int64_t ng = (cols + 127) / 128;
+    if (group == 128 && cols % 4 == 0 && aligned(w, 16) && aligned(packed, 2) &&
+        (rows + 16) * cols * 4 < 0x7ffffff0LL) {
+        const int64_t G = rows * ng;
+        const int u = G >= 2048 * 16 ? 2 : 1;
+        const int64_t waves = (G + 8 * u - 1) / (8 * u);
+        const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+        if (u == 2)
+            hipLaunchKernelGGL(quant_g128_groups<2>, grid, block, 0, st, w, (int)rows, (int)cols, (int)ng, packed, scale_f16);
+        else
+            hipLaunchKernelGGL(quant_g128_groups<1>, grid, block, 0, st, w, (int)rows, (int)cols, (int)ng, packed, scale_f16);
+        return launch_status();
     }
     const int64_t ngroups = (cols + group - 1) / group;
     const int64_t threads = rows * ngroups;

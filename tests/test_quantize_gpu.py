@@ -178,6 +178,80 @@ def test_groupwise_other_group_sizes(dev, c_oracle, group):
     assert np.array_equal(p.cpu().numpy(), p_ref)
 
 
+def _near_halves(s: float, kmin: int, kmax: int) -> np.ndarray:
+    """Values whose quotient by the fp32 scale ``s`` is a half-integer
+    k + 0.5 (kmin <= k < kmax) or within 1..3 ulps of one, both signs."""
+    base = ((np.arange(kmin, kmax) + 0.5) * np.float64(s)).astype(np.float32)
+    bits = base.view(np.int32)
+    out = [base] + [(bits + d).view(np.float32) for d in (-3, -2, -1, 1, 2, 3)]
+    return np.concatenate(out)
+
+
+def _halfway_matrix(rows: int, cols: int, qmax: int, seed: int) -> np.ndarray:
+    """Rows with |max| = amax (so s = fl(amax / qmax)) whose other entries sit
+    on or next to the rounding boundaries of w / s."""
+    rng = np.random.default_rng(seed)
+    amaxes = [qmax * 2.0**-7, 1.0, 0.0173, 3.3e-3, 0.02 * 20, 1e-30]
+    w = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        amax = np.float32(amaxes[r % len(amaxes)])
+        s = np.float32(amax / np.float32(qmax))
+        vals = _near_halves(float(s), -qmax, qmax)
+        vals = vals[np.abs(vals) <= amax]
+        w[r] = rng.choice(vals, cols)
+        w[r, rng.integers(cols)] = amax
+    return w
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("shape", [(4800, 1600), (37, 6400), (2049, 768)])
+def test_per_channel_half_integer_quotients(dev, c_oracle, shape, bits):
+    """Quotients on and within three ulps of k + 0.5: the kernel's product
+    with the reciprocal is replaced by the exact division exactly there."""
+    w = _halfway_matrix(*shape, qmax=(1 << (bits - 1)) - 1, seed=bits)
+    q, s = g.quantize_tensor(torch.from_numpy(w).to(dev), bits)
+    q_ref, s_ref = c_oracle.quantize_per_channel(w, bits)
+    _assert_codes(q, s, q_ref, s_ref)
+    if bits == 4:
+        lin = torch.nn.Linear(shape[1], shape[0]).to(dev)
+        with torch.no_grad():
+            lin.weight.copy_(torch.from_numpy(w))
+        mod, _ = g.quantize_linear(lin, 4)
+        assert np.array_equal(mod.codes.cpu().numpy(), c_oracle.pack_int4(q_ref))
+
+
+@pytest.mark.parametrize("shape", [(4800, 1600), (37, 6400), (2049, 768)])
+def test_groupwise_half_integer_quotients(dev, c_oracle, shape):
+    rng = np.random.default_rng(7)
+    rows, cols = shape
+    w = np.empty(shape, np.float32)
+    scales = [2.0**-6, 0.0123, 3.1e-5, 1.5e-7, 60000.0]  # fp16 normal, subnormal, huge
+    for r in range(rows):
+        for g0 in range(0, cols, 128):
+            s16 = np.float32(np.float16(scales[(r + g0 // 128) % len(scales)]))
+            vals = _near_halves(float(s16), -8, 7)
+            n = min(128, cols - g0)
+            w[r, g0:g0 + n] = rng.choice(vals, n)
+            w[r, g0 + rng.integers(n)] = np.float32(7.0) * s16
+    p, sc = g.quantize_groupwise_int4(torch.from_numpy(w).to(dev), 128)
+    p_ref, s_ref = c_oracle.quantize_groupwise_int4(w, 128)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint16), s_ref.view(np.uint16))
+    assert np.array_equal(p.cpu().numpy(), p_ref)
+
+
+@pytest.mark.parametrize("shape", [(4095, 1600), (2049, 768), (7, 1600), (9, 32768), (3, 32772), (1, 4)])
+def test_rows_split_over_wavefronts(dev, c_oracle, shape):
+    """One, two and four wavefronts per row, a last workgroup with fewer rows
+    than it has room for, the longest register-resident row and one past it."""
+    w = weight(*shape, seed=31)
+    q, s = g.quantize_tensor(w.to(dev), 8)
+    _assert_codes(q, s, *c_oracle.quantize_per_channel(w.numpy(), 8))
+    p, s16 = g.quantize_groupwise_int4(w.to(dev), 128)
+    p_ref, s_ref = c_oracle.quantize_groupwise_int4(w.numpy(), 128)
+    assert np.array_equal(s16.cpu().numpy().view(np.uint16), s_ref.view(np.uint16))
+    assert np.array_equal(p.cpu().numpy(), p_ref)
+
+
 def test_dequantize_is_q_times_scale(dev, c_oracle):
     w = weight(300, 640, seed=4)
     q_ref, s_ref = c_oracle.quantize_per_channel(w.numpy(), 8)
