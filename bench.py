@@ -194,6 +194,30 @@ def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed):
     return res
 
 
+def hbm_stream_section(dev, reps=10):
+    """Measured-achievable HBM rate beside the 8 TB/s datasheet figure:
+    torch's device copy of 1 GiB (read + write counted), the median of `reps`
+    launches between HIP events. (A one-launch pure read reaches 6.2 TB/s at
+    200 MB, csrc/hbm_read_probe.hip.)"""
+    import torch
+
+    n = 1 << 28
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    del src, dst
+    return {"copy": {"GB/s": 8 * n / (statistics.median(ts) * 1e-3) / 1e9, "bytes": 8 * n}}
+
+
 def gemm_section(M, kn, dev, reps=20):
     """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws) per shape: `reps` launches back
     to back between one HIP event pair. Beside it, as the measured-achievable
@@ -669,6 +693,7 @@ def main() -> int:
             detail[f"gemv_small_M{M}"] = gemv_section(M, SMALL_KN, 12, 6, max(10, args.steps // 2), 2, dev, seed=M)
         detail["gemv_xl_M1"] = gemv_section(1, XL_KN, 12, 3, 10, 2, dev, seed=7)
         print("# gemv detail done", file=sys.stderr, flush=True)
+    hbm = hbm_stream_section(dev)
     if not args.quick and args.only is None:
         for M in (256, 1024, 4096):
             detail[f"gemm_xl_M{M}"] = gemm_section(M, XL_KN, dev)
@@ -724,9 +749,11 @@ def main() -> int:
             "kernel": "gemv_direct_kernel (tiq_linear_w8, M=1)",
             "bytes_per_launch": bytes_per_launch,
             "avg_launch_us": head["avg_launch_us"],
+            "measured_hbm_GBs": {k: v["GB/s"] for k, v in hbm.items()},
+            "frac_of_measured_copy": achieved / hbm["copy"]["GB/s"],
         },
         "cpu_baseline": cpu,
-        "detail": {"gemv_small_M1": head, **detail},
+        "detail": {"gemv_small_M1": head, "hbm_measured": hbm, **detail},
     }
     print(json.dumps(line))
     return 0
