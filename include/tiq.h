@@ -33,7 +33,7 @@ enum tiq_status {
     TIQ_EINVAL = -1,        /* bad size, null pointer, out-of-range argument   */
     TIQ_EBITS = -2,         /* bits outside [2, 8] (quantization.py:98-99)       */
     TIQ_EALIGN = -3,        /* pointer or leading dimension misaligned          */
-    TIQ_EUNSUPPORTED = -4,  /* valid request this build has no kernel for       */
+    TIQ_EUNSUPPORTED = -4,  /* valid request the library has no kernel for     */
     TIQ_EWORKSPACE = -5,    /* workspace too small                              */
     TIQ_EHIP_BASE = -1000   /* TIQ_EHIP_BASE - hipError_t                        */
 };
