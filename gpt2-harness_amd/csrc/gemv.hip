@@ -433,14 +433,20 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
     // alternative through register moves, which wait for every load issued
     // before them and so serialize the trips to memory.
     u32x4 wv[UM][R];
+    auto load_weights = [&]() {
 #pragma unroll
-    for (int u = 0; u < UM; ++u) {
-        const int c = min(lane + 64 * u, NC - 1);
+        for (int u = 0; u < UM; ++u) {
+            const int c = min(lane + 64 * u, NC - 1);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            wv[u][r] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(w + (int64_t)min(n0 + r, N - 1) * ldw + 16 * (int64_t)c));
-    }
+            for (int r = 0; r < R; ++r)
+                wv[u][r] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(w + (int64_t)min(n0 + r, N - 1) * ldw + 16 * (int64_t)c));
+        }
+    };
+    // With a LayerNorm the activations are requested first: a wavefront's
+    // loads complete in order, so the statistics (which need only the
+    // activations) are computed while the weights are still in flight.
+    if constexpr (!LNF) load_weights();
     // activations of the same K range: rows past M repeat row M - 1 (their
     // outputs are not stored)
     u32x4 xv[UM][MT][XQ];
@@ -460,6 +466,11 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
                 }
             }
         }
+    }
+    if constexpr (LNF) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_weights();
+        __builtin_amdgcn_sched_barrier(0);  // nothing that waits on the argument fetch ahead of them
     }
     // LayerNorm weight and bias of the lane's columns
     float4 gv[LNF ? UM : 1][P], bv[LNF ? UM : 1][P];
@@ -482,10 +493,6 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
     const float ep_bias = bias ? bias[en] : 0.f;
     float ep_res = 0.f;
     if (fz.res) ep_res = fz.res[(int64_t)em * fz.ldr + en];
-    // Keep those loads here, in the shadow of the weight loads: left to itself
-    // the compiler sinks them into the storing lane's branch, one more trip to
-    // memory after the reduction (the FMA pass waits for the weights anyway).
-    asm volatile("" ::"v"(ep_scale), "v"(ep_bias), "v"(ep_res));
 
     auto x_of = [&](int u, int m, int p) -> float4 {
         if constexpr (sizeof(TX) == 2) return x4_of<TX>(xv[u][m][p / 2], p % 2);
@@ -525,6 +532,14 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
             rstd[m] = 1.0f / sqrtf(wave_sum_dpp(d) / (float)K + fz.ln_eps);
         }
     }
+    // Keep the epilogue loads in the shadow of the weight loads: left to
+    // itself the compiler sinks them into the storing lane's branch, one more
+    // trip to memory after the reduction. Pinned after the LayerNorm
+    // statistics (an operand of the pin, so that it is not hoisted above
+    // them), which so need not wait for the weights; the FMA pass waits for
+    // them anyway.
+    if constexpr (LNF) asm volatile("" ::"v"(ep_scale), "v"(ep_bias), "v"(ep_res), "v"(rstd[MT - 1]));
+    else asm volatile("" ::"v"(ep_scale), "v"(ep_bias), "v"(ep_res));
 
     float acc[R][MT];
 #pragma unroll
