@@ -213,6 +213,44 @@ def test_gemm_split_k(dev, c_oracle, K, N, M, x_dtype):
             assert err <= 8 * max(err32, 2.0 ** -24 * float(ref64.abs().max())), (err, err32)
 
 
+# Full-size prefill products through the workspace entry points (bf16 rows
+# and the fp32 three-plane path, including 400 tiles of 256 x 256 on 256 CUs):
+# each product run twice, both runs bit-identical, and the bf16 output the
+# rounding of the fp32 one.
+@pytest.mark.parametrize("K,N,M,x_dtype", [(1600, 6400, 4096, torch.bfloat16), (6400, 1600, 4096, torch.bfloat16),
+                                           (1600, 4800, 1024, torch.float32), (1600, 1600, 4096, torch.float32)])
+def test_gemm_large_shapes_deterministic(dev, c_oracle, K, N, M, x_dtype):
+    L = _lib.lib()
+    xd = _lib.dtype_code(x_dtype)
+    n_ws = int(L.tiq_gemm_w8_workspace(xd, M, K, N))
+    ws = torch.empty(max(n_ws, 16), dtype=torch.uint8, device=dev)
+    entry = "tiq_gemm_w8_ws" if x_dtype == torch.bfloat16 else "tiq_linear_w8_ws"
+    for rows in (M, M - 37):
+        w, x, b = _inputs(K, N, rows, rows + K + 1, x_dtype)
+        q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+        qd, sd, bd, xg = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
+        ys = [torch.full((rows, N), float("nan"), device=dev) for _ in range(2)]
+        ybf = torch.empty(rows, N, device=dev, dtype=torch.bfloat16)
+        for y in (*ys, ybf):
+            rc = getattr(L, entry)(xg.data_ptr(), xd, rows, K, K, qd.data_ptr(), sd.data_ptr(), bd.data_ptr(), N,
+                                   y.data_ptr(), _lib.dtype_code(y.dtype), N, ws.data_ptr(), n_ws,
+                                   torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, entry)
+        torch.cuda.synchronize()
+        y32 = ys[0].cpu()
+        assert torch.isfinite(y32).all()
+        assert torch.equal(y32, ys[1].cpu()), "results differ between two runs"
+        assert torch.equal(ybf.cpu(), y32.to(torch.bfloat16))
+        w_hat = OL.dequantize(q, s)
+        ok, err, bound = OL.within_tolerance(y32, OL.linear_ref(x, w_hat, b), TOL)
+        assert ok, (rows, err, bound)
+        if x_dtype == torch.float32:   # the exact planes: fp32-accurate
+            ref64 = x.double() @ w_hat.double().T + b.double()
+            err = float((y32.double() - ref64).abs().max())
+            err32 = float((OL.linear_ref(x, w_hat, b).double() - ref64).abs().max())
+            assert err <= 8 * max(err32, 2.0 ** -24 * float(ref64.abs().max())), (err, err32)
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 256])
 def test_linear_w8_dispatch(dev, c_oracle, M):
     _run_w8("tiq_linear_w8", dev, c_oracle, 1600, 4800, M, torch.bfloat16, seed=M)
