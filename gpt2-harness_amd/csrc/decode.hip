@@ -309,6 +309,23 @@ __global__ __launch_bounds__(64 * kArgFinalWaves) void argmax_final_kernel(
     }
 }
 
+
+// y = gelu_tanh(x) elementwise (the MLP activation of a prefill, one pass in
+// place of the reference's op chain at model.py:57-75): 4 values a thread per
+// step of a grid-stride loop; n % 4 tail by the first threads.
+__global__ __launch_bounds__(256) void gelu_tanh_kernel(const float* x, float* y, int64_t n) {
+    const int64_t n4 = n / 4, stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+        float4 v = reinterpret_cast<const float4*>(x)[i];
+        v.x = gelu_tanh(v.x);
+        v.y = gelu_tanh(v.y);
+        v.z = gelu_tanh(v.z);
+        v.w = gelu_tanh(v.w);
+        reinterpret_cast<float4*>(y)[i] = v;
+    }
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t < n - 4 * n4) y[4 * n4 + t] = gelu_tanh(x[4 * n4 + t]);
+}
 }  // namespace
 }  // namespace tiq
 
@@ -351,6 +368,17 @@ extern "C" int tiq_decode_attention_planes(const float* qkv, int64_t ld_qkv, int
     if (!planes_out) return TIQ_EINVAL;
     return decode_attention(qkv, ld_qkv, batch, n_head, n_kv_head, head_dim, k_cache, v_cache, t_max, pos, y, ldy,
                             planes_out, stream);
+}
+
+extern "C" int tiq_gelu_tanh(const float* x, float* y, int64_t n, void* stream) {
+    if (n < 0) return TIQ_EINVAL;
+    if (n == 0) return TIQ_OK;
+    if (!x || !y) return TIQ_EINVAL;
+    if (!aligned(x, 16) || !aligned(y, 16)) return TIQ_EALIGN;
+    int64_t blocks = (n / 4 + 255) / 256;
+    blocks = blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks);
+    hipLaunchKernelGGL(gelu_tanh_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), x, y, n);
+    return launch_status();
 }
 
 extern "C" int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte, int64_t vocab,

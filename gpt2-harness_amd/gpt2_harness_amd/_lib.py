@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_decode_attention": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _i32),
     "tiq_decode_attention_planes": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
+    "tiq_gelu_tanh": ([_vp, _vp, _i64, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),
     "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _vp], _i32),
 }

@@ -32,7 +32,22 @@ __all__ = ["GPT", "MLP", "Block", "CausalSelfAttention", "KVCache", "gelu_tanh"]
 
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
-    """``0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))`` (``model.py:57-75``)."""
+    """``0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))`` (``model.py:57-75``).
+
+    fp32 tensors on the GPU go through one HIP pass (``tiq_gelu_tanh``; the
+    op chain below reads and writes the tensor eight times); other tensors
+    (CPU, other dtypes) are computed with the torch ops of the reference.
+    """
+    if x.is_cuda and x.dtype == torch.float32:
+        from . import _lib
+
+        xc = x.contiguous()
+        if xc.data_ptr() % 16:
+            xc = xc.clone()  # a fresh allocation is 16-byte aligned
+        y = torch.empty_like(xc)
+        _lib.check(_lib.lib().tiq_gelu_tanh(xc.data_ptr(), y.data_ptr(), xc.numel(), _lib.stream_of(xc)),
+                   "gelu_tanh")
+        return y
     return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x.pow(3))))
 
 

@@ -277,6 +277,12 @@ int tiq_decode_attention_planes(const float* qkv, int64_t ld_qkv, int64_t batch,
                                 int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
                                 float* y, int64_t ldy, uint16_t* planes_out, void* stream);
 
+/* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) elementwise over n fp32
+ * values (16-byte aligned; y may alias x): the MLP activation gelu_tanh
+ * (model.py:57-75, applied at model.py:354) in one pass instead of the
+ * reference's chain of torch ops. */
+int tiq_gelu_tanh(const float* x, float* y, int64_t n, void* stream);
+
 /* x[b] = wte[tokens[b]] + wpe[*pos]  (model.py:561-564 for one position). */
 int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte, int64_t vocab,
                      const float* wpe, int64_t n_positions, int64_t batch, int64_t n_embd, float* x,

@@ -587,3 +587,29 @@ def test_decode_attention_planes_feed_the_projection(dev, c_oracle, B, H, pos):
     _lib.check(_dl(y1, None, B, C, qd, _lib.WF_INT8, sd, None, C, a), "from rows")
     _lib.check(_dl(None, planes, B, C, qd, _lib.WF_INT8, sd, None, C, b), "from planes")
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1000, 4096 * 6400 + 3])
+def test_gelu_tanh_pass(dev, n):
+    """The one-pass GELU against the formula in float64 (model.py:57-75), in
+    place and out of place, with a ragged tail; large and tiny magnitudes."""
+    gen = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=gen) * 4.0
+    x[: min(n, 8)] = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 30.0, -30.0, 1e4, -1e4])[: min(n, 8)]
+    ref = (0.5 * x.double() * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x.double() + 0.044715 * x.double() ** 3))))
+    xd = x.to(dev)
+    y = torch.empty_like(xd)
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(L.tiq_gelu_tanh(xd.data_ptr(), y.data_ptr(), n, st), "gelu")
+    inplace = xd.clone()
+    _lib.check(L.tiq_gelu_tanh(inplace.data_ptr(), inplace.data_ptr(), n, st), "gelu in place")
+    torch.cuda.synchronize()
+    err = (y.cpu().double() - ref).abs()
+    assert bool((err <= 4e-6 * ref.abs() + 1e-6).all()), float((err - 4e-6 * ref.abs()).max())
+    assert torch.equal(y.cpu(), inplace.cpu())
+    from gpt2_harness_amd.model import gelu_tanh
+
+    assert torch.equal(gelu_tanh(xd).cpu(), y.cpu())
+    torch_chain = 0.5 * xd * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd.pow(3))))
+    assert torch.allclose(y, torch_chain, rtol=1e-5, atol=1e-6)
