@@ -4,11 +4,12 @@
 // (src/transformer_internals/quantization.py:78-116):
 //   abs -> amax -> div -> clamp -> div -> round -> clamp -> to(int8)
 // with one pass over HBM: each row is read once into registers, its |max| is
-// reduced across the wavefront, and the codes are written from the same
-// registers. Codes and scales are bit-identical to the reference because every
-// step is the same IEEE operation: an unsigned max on |w| bits (order-free,
-// NaN-propagating), the correctly rounded fp32 divide, rint (half to even)
-// and the same clamps.
+// reduced across the row's wavefronts, and the codes are written from the same
+// registers. Codes and scales are bit-identical to the reference: an unsigned
+// max on |w| bits (order-free, NaN-propagating), the correctly rounded fp32
+// scale divide, codes rint(w / s) (half to even) with the same clamps, where
+// the row kernels form w / s as a product with the reciprocal and take the
+// division itself wherever the two could round differently (codes4).
 //
 // Memory: per-channel int8 reads 4*rows*cols bytes and writes rows*cols + 4*rows.
 #include "tiq_common.hpp"
