@@ -334,10 +334,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     if (i >= (int64_t)M * N) return;
     const int m = (int)(i / N), n = (int)(i % N);
     const int64_t slice = (int64_t)M * N;
+    // the slices eight at a time (S <= 8 in practice: one trip to memory), all
+    // requested before any is added (indices clamped instead of a branch, the
+    // repeats not added), summed in slice order
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int z = 0; z < S; ++z) {
-        const float4 v = *reinterpret_cast<const float4*>(part + z * slice + i);
-        a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+    for (int z0 = 0; z0 < S; z0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(part + min(z0 + j, S - 1) * slice + i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool use = z0 + j < S;
+            a.x = use ? a.x + v[j].x : a.x;
+            a.y = use ? a.y + v[j].y : a.y;
+            a.z = use ? a.z + v[j].z : a.z;
+            a.w = use ? a.w + v[j].w : a.w;
+        }
     }
     const float4 sc = *reinterpret_cast<const float4*>(scale + n);
     float4 bi = make_float4(0.f, 0.f, 0.f, 0.f);
