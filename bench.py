@@ -11,11 +11,14 @@ bytes per launch = N*K + 4*N + 2*M*K + 2*M*N; value = bytes / wall time of
 the K timed steps (HIP events on the launch stream; one step is one replay
 of a captured HIP graph of the 48 launches).
 
-``detail`` adds the other configurations: M = 4 / 16 at the same shapes,
-GPT-2-XL layer shapes at M = 1 (per shape), the int8->bf16 MFMA GEMM at
-GPT-2-XL shapes with M = 4096, the quantize kernels, and GPT-2 small int8
-greedy decode (64-token prompt, 64 new tokens) with its token parity against
-the reference fixture. ``cpu_baseline`` times the oracle's dequantize-then-
+``roofline`` also carries a 1 GiB device copy timed in the same run as the
+measured-achievable HBM rate. ``detail`` adds the other configurations:
+M = 4 / 16 at the same shapes, GPT-2-XL layer shapes at M = 1 (per shape),
+the int8->bf16 MFMA GEMM at GPT-2-XL shapes with M = 256 / 1024 / 4096, the
+quantize kernels at GPT-2-XL shapes (a graph of calls over cold weight
+copies), GPT-2 small int8 greedy decode (64-token prompt, 64 new tokens)
+with its token parity against the reference fixture, and GPT-2-XL batch-32
+greedy decode. ``cpu_baseline`` times the oracle's dequantize-then-
 fp32-matmul (the reference's runtime arithmetic) on the host cores over a
 bounded sample of the same GEMV workload; ``detail["cpu_oracle"]`` times the
 oracle on bounded samples of the other configurations (greedy decode,
