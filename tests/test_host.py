@@ -55,6 +55,10 @@ def test_arguments_checked_before_any_launch():
     assert lib.tiq_linear_w8(None, 3, 1, 16, 16, None, None, None, 4, None, 0, 4, None) == -1
     assert lib.tiq_linear_w4g(None, 0, 1, 16, 16, None, None, 3, None, 4, None, 0, 4, None) == -1
     assert lib.tiq_quantize_per_tensor_workspace(1 << 20) >= 4
+    assert lib.tiq_gelu_tanh(None, None, -1, None) == -1
+    assert lib.tiq_gelu_tanh(None, None, 0, None) == 0
+    assert lib.tiq_gelu_tanh(None, None, 8, None) == -1
+    assert lib.tiq_gelu_tanh(4, 16, 8, None) == -3  # misaligned (never dereferenced)
 
 
 def test_api_errors_match_reference_without_gpu():
