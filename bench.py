@@ -651,8 +651,8 @@ def main() -> int:
                          "used to calibrate the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the benchmark runs the path on a single GPU)", file=sys.stderr)
         return 2
 
     import torch
