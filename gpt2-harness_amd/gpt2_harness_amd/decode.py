@@ -11,15 +11,15 @@ level is a device scalar, so the captured step is the same for every token.
 Two step implementations:
 
 * :class:`FusedDecoder` (used when the model fits: four quantized Linears per
-  block, pre-LN, learned positions, ``gelu_tanh``, head_dim 64, fp32 tied
-  head): the library's decode kernels only -- an embedding kernel, then per
+  block, head_dim 64, an fp32 or quantized tied head): the library's decode kernels only -- an embedding kernel, then per
   block LayerNorm+``c_attn``, attention over the cache, ``c_proj``+residual,
   LayerNorm+``c_fc``+GELU, ``c_proj``+residual (5 launches), then
   LayerNorm+``lm_head`` (fp32, or int8 / int4 codes when the embedding was
   quantized) and ``argmax`` -- 5 * n_layer + 4 launches per token;
 * :class:`GraphDecoder`: the model's own modules as torch ops with attention
   over all ``T_max`` slots, the slots after the current position masked to
-  ``-inf`` (probability exactly 0), for any other model layout.
+  ``-inf`` (probability exactly 0), for models the fused step does not take
+  (unquantized or partly quantized blocks, other head widths).
 
 Greedy token ids are the reference's; logits agree with an eager forward to
 fp32 rounding.
@@ -30,7 +30,6 @@ from __future__ import annotations
 import math
 
 import torch
-import torch.nn.functional as F
 
 from . import _lib
 from .qlinear import FMT_W4, FMT_W4G, FMT_W8, QuantLinear
@@ -143,7 +142,7 @@ class _DecoderBase:
 
 
 class GraphDecoder(_DecoderBase):
-    """Decode step from the model's own modules (any reference layout)."""
+    """Decode step from the model's own modules as torch ops."""
 
     def __init__(self, model, batch: int, max_len: int) -> None:
         super().__init__(model, batch, max_len)
@@ -151,37 +150,20 @@ class GraphDecoder(_DecoderBase):
 
     def _step(self) -> None:
         m, cfg = self.model, self.cfg
-        B, H, Hkv, hd, C = self.B, self.H, self.Hkv, self.hd, cfg.n_embd
+        B, H, hd, C = self.B, self.H, self.hd, cfg.n_embd
         pos = self.pos
-        x = m.wte(self.tok) + m.position_embeddings(pos.view(1, 1).expand(B, 1))
-        visible = (self.slots <= pos).view(1, 1, 1, self.T)
-        pre = cfg.norm_position == "pre"
+        x = m.wte(self.tok) + m.wpe(pos.view(1, 1).expand(B, 1))
+        hidden = (self.slots > pos).view(1, 1, 1, self.T)  # slots after the current position
         for i, block in enumerate(m.h):
             attn = block.attn
-            h = block.ln_1(x) if pre else x
-            q, k, v = attn.c_attn(h).split([C, Hkv * hd, Hkv * hd], dim=2)
-            q = q.view(B, 1, H, hd).transpose(1, 2)
-            k = k.view(B, 1, Hkv, hd).transpose(1, 2)
-            v = v.view(B, 1, Hkv, hd).transpose(1, 2)
-            self.k[i].index_copy_(2, pos, k)
-            self.v[i].index_copy_(2, pos, v)
-            K, V = self.k[i], self.v[i]
-            if Hkv != H:
-                K = K.repeat_interleave(H // Hkv, dim=1)
-                V = V.repeat_interleave(H // Hkv, dim=1)
-            att = (q @ K.transpose(-2, -1)) / math.sqrt(hd)
-            att = att.masked_fill(~visible, float("-inf"))
-            att = F.softmax(att, dim=-1)
-            y = att @ V
-            if attn.head_mask is not None:
-                y = y * attn.head_mask.to(att.device, att.dtype).view(1, -1, 1, 1)
-            a = attn.c_proj(y.transpose(1, 2).contiguous().view(B, 1, C))
-            if pre:
-                x = x + a
-                x = x + block.mlp(block.ln_2(x))
-            else:
-                x = block.ln_1(x + a)
-                x = block.ln_2(x + block.mlp(x))
+            q, k, v = attn.c_attn(block.ln_1(x)).view(B, 3, H, hd).unbind(1)
+            self.k[i].index_copy_(2, pos, k.unsqueeze(2))
+            self.v[i].index_copy_(2, pos, v.unsqueeze(2))
+            scores = torch.matmul(q.unsqueeze(2), self.k[i].transpose(-2, -1)) / math.sqrt(hd)
+            probs = torch.softmax(scores.masked_fill(hidden, float("-inf")), dim=-1)
+            y = torch.matmul(probs, self.v[i])  # (B, H, 1, hd)
+            x = x + attn.c_proj(y.view(B, 1, C))
+            x = x + block.mlp(block.ln_2(x))
         logits = m.lm_head(m.ln_f(x))[:, -1, :]
         nxt = logits.argmax(dim=-1, keepdim=True)
         self.tok.copy_(nxt)
@@ -195,8 +177,6 @@ _WF = {FMT_W8: _lib.WF_INT8, FMT_W4: _lib.WF_INT4, FMT_W4G: _lib.WF_INT4G}
 def fused_supported(model) -> str | None:
     """``None`` when :class:`FusedDecoder` can run ``model``, else the reason."""
     cfg = model.config
-    if cfg.norm_position != "pre" or cfg.pos_embedding != "learned" or cfg.activation != "gelu_tanh":
-        return "needs pre-LN, learned positions and gelu_tanh"
     if cfg.head_dim != 64 or cfg.n_positions > 1024:
         return "needs head_dim 64 and n_positions <= 1024"
     if cfg.n_embd % 32:
@@ -205,8 +185,6 @@ def fused_supported(model) -> str | None:
         for lin in (block.attn.c_attn, block.attn.c_proj, block.mlp.c_fc, block.mlp.c_proj):
             if not isinstance(lin, QuantLinear):
                 return "every target Linear must be quantized"
-        if block.attn.head_mask is not None or block.mlp.neuron_mask is not None:
-            return "head / neuron masks are not fused"
     head = model.lm_head
     if model.wte.weight.dtype != torch.float32 or head.bias is not None:
         return "needs an fp32 embedding and a bias-free lm_head"

@@ -1,25 +1,32 @@
-"""GPT-2 host model whose four Linear slots take :class:`QuantLinear` modules.
+"""GPT-2 decoder whose four Linear slots take :class:`QuantLinear` modules.
 
-The module tree, parameter names and initialisation order are those of the
-reference's ``GPT`` (``src/transformer_internals/model.py:445-518``) because
-three things depend on them: the ``TARGET_SUFFIXES`` lookup of
-``quantize_model`` (``attn.c_attn``, ``attn.c_proj``, ``mlp.c_fc``,
-``mlp.c_proj``), state-dict compatibility with reference checkpoints, and the
-seed-0 random weights the benchmarks are quoted on (module construction draws,
-then ``_init_weights`` in module order -- the tied ``lm_head`` redraws ``wte``
--- then residual scaling of both ``c_proj`` weights).
+This is the inference model of the quantized path: pre-LN GPT-2 blocks with
+learned positions, the tanh GELU and a tied head. The reference's ablation
+switches (post-LN, sinusoidal positions, other activations, grouped-query
+heads, attention / neuron masks, activation taps) are not part of that path
+and are refused at construction.
 
-The forward pass is the reference's arithmetic (``model.py:528-599``):
-pre-LN blocks, fused ``c_attn`` split into q/k/v, explicit softmax attention
-with the causal mask taken at absolute positions, ``gelu_tanh`` MLP, tied fp32
-``lm_head``. Attention, LayerNorm and the head run as torch ops on the GPU;
-the four projections per block are the HIP kernels once quantized.
+Three things are interface and therefore fixed:
+
+* the module names (``wte``, ``wpe``, ``h.<i>.ln_1``, ``h.<i>.attn.c_attn``,
+  ``h.<i>.attn.c_proj``, ``h.<i>.ln_2``, ``h.<i>.mlp.c_fc``,
+  ``h.<i>.mlp.c_proj``, ``ln_f``, ``lm_head``): ``quantize_model`` finds its
+  targets by these suffixes and checkpoints are keyed by them;
+* the order of the random draws at construction and initialisation, which
+  fixes the seed-0 weights every benchmark is quoted on
+  (``src/transformer_internals/model.py:457-518``; see :meth:`GPT._seeded_init`);
+* ``forward(idx, targets=None, cache=None)`` returning ``{"logits", "loss"}``
+  and the ``KVCache`` calls made by the greedy loop
+  (``sampling.py:100-181``, ``model.py:106-172``).
+
+The arithmetic is GPT-2's (``model.py:57-75,227-320,351-355,528-599``); on the
+GPU the quantized projections are the library's HIP kernels and the prefill's
+GELU is one HIP pass.
 """
 
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
 from typing import Any
 
 import torch
@@ -30,244 +37,262 @@ from .config import GPTConfig
 
 __all__ = ["GPT", "MLP", "Block", "CausalSelfAttention", "KVCache", "gelu_tanh"]
 
+_SQRT_2_OVER_PI = math.sqrt(2.0 / math.pi)
+
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
-    """``0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))`` (``model.py:57-75``).
+    """GELU in GPT-2's tanh form, ``0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))``.
 
-    fp32 tensors on the GPU go through one HIP pass (``tiq_gelu_tanh``; the
-    op chain below reads and writes the tensor eight times); other tensors
-    (CPU, other dtypes) are computed with the torch ops of the reference.
+    An fp32 GPU tensor that needs no gradient goes through one HIP pass
+    (``tiq_gelu_tanh``: one read and one write instead of the eight passes
+    of the op chain). Anything else -- CPU tensors, other dtypes, or a tensor
+    autograd must differentiate -- is computed with torch ops, which carry the
+    gradient.
     """
-    if x.is_cuda and x.dtype == torch.float32:
+    if x.is_cuda and x.dtype == torch.float32 and not (torch.is_grad_enabled() and x.requires_grad):
         from . import _lib
 
-        xc = x.contiguous()
-        if xc.data_ptr() % 16:
-            xc = xc.clone()  # a fresh allocation is 16-byte aligned
-        y = torch.empty_like(xc)
-        _lib.check(_lib.lib().tiq_gelu_tanh(xc.data_ptr(), y.data_ptr(), xc.numel(), _lib.stream_of(xc)),
+        src = x.contiguous()
+        if src.data_ptr() % 16:
+            src = src.clone()  # fresh allocations are 16-byte aligned
+        out = torch.empty_like(src)
+        _lib.check(_lib.lib().tiq_gelu_tanh(src.data_ptr(), out.data_ptr(), src.numel(), _lib.stream_of(src)),
                    "gelu_tanh")
-        return y
-    return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x.pow(3))))
+        return out
+    inner = _SQRT_2_OVER_PI * (x + 0.044715 * x.pow(3))
+    return 0.5 * x * (1.0 + torch.tanh(inner))
 
 
-def _sinusoid(n_positions: int, n_embd: int) -> torch.Tensor:
-    pos = torch.arange(n_positions, dtype=torch.float32)[:, None]
-    inv = torch.exp(torch.arange(0, n_embd, 2, dtype=torch.float32) * (-math.log(10000.0) / n_embd))
-    pe = torch.zeros(n_positions, n_embd)
-    pe[:, 0::2] = torch.sin(pos * inv)
-    pe[:, 1::2] = torch.cos(pos * inv)[:, : n_embd // 2]
-    return pe
-
-
-@dataclass
 class KVCache:
-    """Per-layer key/value history, appended by concatenation (``model.py:106-172``).
+    """Per-layer key / value history for cached decoding.
 
-    ``length(layer)`` -- not the model-level ``seq_len`` -- gives the causal
-    offset inside a layer, since earlier layers already hold the current step.
+    Each layer owns a buffer ``(B, heads, capacity, head_dim)`` that grows by
+    doubling, so appending a step writes only the new rows (the reference's
+    ``torch.cat`` copies the whole history every step, ``model.py:153-172``).
+    ``length(layer)`` is that layer's own fill level -- inside one forward
+    pass the earlier layers already hold the current step, so the causal
+    offset of a layer must come from it, not from :attr:`seq_len`
+    (``model.py:139-151``).
     """
 
-    keys: list[torch.Tensor | None]
-    values: list[torch.Tensor | None]
+    def __init__(self, n_layer: int) -> None:
+        self._k: list[torch.Tensor | None] = [None] * n_layer
+        self._v: list[torch.Tensor | None] = [None] * n_layer
+        self._len = [0] * n_layer
 
     @classmethod
     def empty(cls, n_layer: int) -> KVCache:
-        return cls(keys=[None] * n_layer, values=[None] * n_layer)
+        return cls(n_layer)
 
     @property
     def seq_len(self) -> int:
-        return self.length(0)
+        """Positions already processed (layer 0's fill level): the absolute
+        position of the tokens a forward pass is about to add."""
+        return self._len[0]
 
     def length(self, layer: int) -> int:
-        k = self.keys[layer]
-        return 0 if k is None else int(k.shape[-2])
+        return self._len[layer]
+
+    @property
+    def keys(self) -> list[torch.Tensor | None]:
+        return [None if b is None else b[:, :, :n] for b, n in zip(self._k, self._len)]
+
+    @property
+    def values(self) -> list[torch.Tensor | None]:
+        return [None if b is None else b[:, :, :n] for b, n in zip(self._v, self._len)]
 
     def update(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        pk, pv = self.keys[layer], self.values[layer]
-        if pk is not None and pv is not None:
-            k = torch.cat([pk, k], dim=-2)
-            v = torch.cat([pv, v], dim=-2)
-        self.keys[layer], self.values[layer] = k, v
-        return k, v
+        """Append ``k, v`` ``(B, heads, T_new, head_dim)`` to ``layer``; return
+        views of the whole history ``(B, heads, length, head_dim)``."""
+        n, t = self._len[layer], k.shape[-2]
+        buf_k, buf_v = self._k[layer], self._v[layer]
+        if buf_k is None or n + t > buf_k.shape[-2]:
+            cap = max(16, 2 * (n + t))
+            grown_k = k.new_empty(*k.shape[:-2], cap, k.shape[-1])
+            grown_v = v.new_empty(*v.shape[:-2], cap, v.shape[-1])
+            if buf_k is not None:
+                grown_k[:, :, :n] = buf_k[:, :, :n]
+                grown_v[:, :, :n] = buf_v[:, :, :n]
+            self._k[layer], self._v[layer] = buf_k, buf_v = grown_k, grown_v
+        buf_k[:, :, n : n + t] = k
+        buf_v[:, :, n : n + t] = v
+        self._len[layer] = n + t
+        return buf_k[:, :, : n + t], buf_v[:, :, : n + t]
+
+
+def _causal_softmax_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, first: int,
+                              p_drop: float) -> torch.Tensor:
+    """``softmax(q k^T / sqrt(hd) + mask) v`` for queries at absolute positions
+    ``first .. first + T - 1`` over keys ``0 .. S - 1`` (``model.py:284-309``).
+
+    Key ``j`` is visible to query ``i`` iff ``j <= first + i``; hidden scores
+    are ``-inf``, so they get probability exactly 0. A query block that sees
+    every key (one new token over the cache) needs no mask at all.
+    """
+    T, S = q.shape[-2], k.shape[-2]
+    scores = torch.matmul(q, k.transpose(-2, -1)) / math.sqrt(q.shape[-1])
+    if not (T == 1 and first + 1 == S):
+        qpos = torch.arange(first, first + T, device=q.device).unsqueeze(1)
+        kpos = torch.arange(S, device=q.device).unsqueeze(0)
+        scores = scores.masked_fill(kpos > qpos, float("-inf"))
+    probs = torch.softmax(scores, dim=-1)
+    if p_drop:
+        probs = F.dropout(probs, p_drop, training=True)
+    return torch.matmul(probs, v)
 
 
 class CausalSelfAttention(nn.Module):
+    """Fused ``c_attn`` (q, k, v side by side), heads of 64 columns, causal
+    attention over the cache, ``c_proj``."""
+
     def __init__(self, config: GPTConfig, layer_idx: int = 0) -> None:
         super().__init__()
         self.config = config
         self.layer_idx = layer_idx
-        self.n_head, self.n_kv_head = config.n_head, config.kv_heads
-        self.n_embd, self.head_dim = config.n_embd, config.head_dim
-        self.kv_dim = self.n_kv_head * self.head_dim
-        self.c_attn = nn.Linear(config.n_embd, config.n_embd + 2 * self.kv_dim, bias=config.attn_bias)
+        self.n_head, self.head_dim, self.n_embd = config.n_head, config.head_dim, config.n_embd
+        self.c_attn = nn.Linear(config.n_embd, 3 * config.n_embd, bias=config.attn_bias)
         self.c_proj = nn.Linear(config.n_embd, config.n_embd, bias=config.attn_bias)
-        self.attn_dropout = nn.Dropout(config.dropout)
-        self.resid_dropout = nn.Dropout(config.dropout)
-        self.head_mask: torch.Tensor | None = None
 
-    def forward(self, x: torch.Tensor, cache: KVCache | None = None, need_weights: bool = False):
+    def forward(self, x: torch.Tensor, cache: KVCache | None = None) -> torch.Tensor:
         B, T, C = x.shape
-        past = cache.length(self.layer_idx) if cache is not None else 0
-        q, k, v = self.c_attn(x).split([self.n_embd, self.kv_dim, self.kv_dim], dim=2)
-        q = q.view(B, T, self.n_head, self.head_dim).transpose(1, 2)
-        k = k.view(B, T, self.n_kv_head, self.head_dim).transpose(1, 2)
-        v = v.view(B, T, self.n_kv_head, self.head_dim).transpose(1, 2)
+        first = 0 if cache is None else cache.length(self.layer_idx)
+        # (B, T, 3C) -> (3, B, heads, T, hd): q, k, v heads in one permute
+        q, k, v = self.c_attn(x).view(B, T, 3, self.n_head, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
         if cache is not None:
             k, v = cache.update(self.layer_idx, k, v)
-        total = k.shape[-2]
-        if self.n_kv_head != self.n_head:
-            g = self.n_head // self.n_kv_head
-            k = k.repeat_interleave(g, dim=1)
-            v = v.repeat_interleave(g, dim=1)
-        # key j is visible to query i (absolute position past + i) iff j <= past + i
-        qpos = torch.arange(past, past + T, device=x.device)[:, None]
-        kpos = torch.arange(total, device=x.device)[None, :]
-        allowed = kpos <= qpos
-        probs = None
-        if self.config.use_sdpa and not need_weights:
-            y = F.scaled_dot_product_attention(q, k, v, attn_mask=allowed.view(1, 1, T, total),
-                                               dropout_p=self.config.dropout if self.training else 0.0)
-        else:
-            kt = k.transpose(-2, -1)
-            if kt.dtype == torch.bfloat16:
-                kt = kt.contiguous()
-            att = (q @ kt) / math.sqrt(self.head_dim)
-            att = att.masked_fill(~allowed.view(1, 1, T, total), float("-inf"))
-            att = F.softmax(att, dim=-1)
-            probs = att if need_weights else None
-            y = self.attn_dropout(att) @ v
-        if self.head_mask is not None:
-            y = y * self.head_mask.to(y.device, y.dtype).view(1, -1, 1, 1)
-        y = y.transpose(1, 2).contiguous().view(B, T, C)
-        return self.resid_dropout(self.c_proj(y)), probs
+        p = self.config.dropout if self.training else 0.0
+        y = _causal_softmax_attention(q, k, v, first, p)
+        return self.c_proj(y.transpose(1, 2).reshape(B, T, C))
 
 
 class MLP(nn.Module):
+    """``c_proj(gelu_tanh(c_fc(x)))``, 4x expansion."""
+
     def __init__(self, config: GPTConfig) -> None:
         super().__init__()
-        self.config = config
         self.c_fc = nn.Linear(config.n_embd, 4 * config.n_embd, bias=config.mlp_bias)
         self.c_proj = nn.Linear(4 * config.n_embd, config.n_embd, bias=config.mlp_bias)
-        self.dropout = nn.Dropout(config.dropout)
-        self.neuron_mask: torch.Tensor | None = None
-
-    def act(self, x: torch.Tensor) -> torch.Tensor:
-        if self.config.activation == "gelu_tanh":
-            return gelu_tanh(x)
-        if self.config.activation == "gelu_exact":
-            return F.gelu(x)
-        return F.relu(x)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        h = self.act(self.c_fc(x))
-        if self.neuron_mask is not None:
-            h = h * self.neuron_mask.to(h.device, h.dtype)
-        return self.dropout(self.c_proj(h))
+        return self.c_proj(gelu_tanh(self.c_fc(x)))
 
 
 class Block(nn.Module):
+    """Pre-LN block: ``x + attn(ln_1(x))``, then ``x + mlp(ln_2(x))``."""
+
     def __init__(self, config: GPTConfig, layer_idx: int = 0) -> None:
         super().__init__()
-        self.config = config
+        self.p_drop = config.dropout
+        # construction order = registration order = the order of the RNG draws
         self.ln_1 = nn.LayerNorm(config.n_embd, eps=config.layer_norm_epsilon)
         self.attn = CausalSelfAttention(config, layer_idx=layer_idx)
         self.ln_2 = nn.LayerNorm(config.n_embd, eps=config.layer_norm_epsilon)
         self.mlp = MLP(config)
 
-    def forward(self, x: torch.Tensor, cache: KVCache | None = None, need_weights: bool = False):
-        if self.config.norm_position == "pre":
-            a, probs = self.attn(self.ln_1(x), cache=cache, need_weights=need_weights)
-            x = x + a
-            x = x + self.mlp(self.ln_2(x))
-        else:
-            a, probs = self.attn(x, cache=cache, need_weights=need_weights)
-            x = self.ln_1(x + a)
-            x = self.ln_2(x + self.mlp(x))
-        return x, probs
+    def _drop(self, t: torch.Tensor) -> torch.Tensor:
+        return F.dropout(t, self.p_drop, training=True) if self.training and self.p_drop else t
+
+    def forward(self, x: torch.Tensor, cache: KVCache | None = None) -> torch.Tensor:
+        x = x + self._drop(self.attn(self.ln_1(x), cache))
+        return x + self._drop(self.mlp(self.ln_2(x)))
+
+
+def _refuse_unsupported(config: GPTConfig) -> None:
+    """The layouts of the quantized path only: GPT-2 as released."""
+    unsupported = {
+        "norm_position": (config.norm_position, "pre"),
+        "pos_embedding": (config.pos_embedding, "learned"),
+        "activation": (config.activation, "gelu_tanh"),
+        "n_kv_head": (config.kv_heads, config.n_head),
+        "use_sdpa": (config.use_sdpa, False),
+    }
+    for field, (got, want) in unsupported.items():
+        if got != want:
+            raise NotImplementedError(
+                f"{field}={got!r}: this model implements GPT-2's inference layout only ({field}={want!r})")
 
 
 class GPT(nn.Module):
+    """GPT-2 with a tied head (``lm_head.weight is wte.weight``)."""
+
     def __init__(self, config: GPTConfig) -> None:
         super().__init__()
+        _refuse_unsupported(config)
+        if not config.tie_weights:
+            raise NotImplementedError("tie_weights=False: GPT-2's head is the embedding matrix")
         self.config = config
         self.wte = nn.Embedding(config.vocab_size, config.n_embd)
-        if config.pos_embedding == "learned":
-            self.wpe: nn.Embedding | None = nn.Embedding(config.n_positions, config.n_embd)
-        else:
-            self.wpe = None
-            self.register_buffer("sinusoidal_pe", _sinusoid(config.n_positions, config.n_embd), persistent=False)
-        self.drop = nn.Dropout(config.dropout)
-        self.h = nn.ModuleList([Block(config, layer_idx=i) for i in range(config.n_layer)])
+        self.wpe = nn.Embedding(config.n_positions, config.n_embd)
+        self.h = nn.ModuleList(Block(config, layer_idx=i) for i in range(config.n_layer))
         self.ln_f = nn.LayerNorm(config.n_embd, eps=config.layer_norm_epsilon)
         self.lm_head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
-        if config.tie_weights:
-            self.lm_head.weight = self.wte.weight
-        self.apply(self._init_weights)
-        if config.residual_scaled_init:
-            std = 0.02 / math.sqrt(2 * config.n_layer)
-            for block in self.h:
-                nn.init.normal_(block.attn.c_proj.weight, mean=0.0, std=std)
-                nn.init.normal_(block.mlp.c_proj.weight, mean=0.0, std=std)
+        self.lm_head.weight = self.wte.weight
+        self._seeded_init()
 
-    @staticmethod
-    def _init_weights(module: nn.Module) -> None:
-        if isinstance(module, nn.Linear):
-            nn.init.normal_(module.weight, mean=0.0, std=0.02)
-            if module.bias is not None:
-                nn.init.zeros_(module.bias)
-        elif isinstance(module, nn.Embedding):
-            nn.init.normal_(module.weight, mean=0.0, std=0.02)
-        elif isinstance(module, nn.LayerNorm):
-            nn.init.ones_(module.weight)
-            nn.init.zeros_(module.bias)
+    @torch.no_grad()
+    def _seeded_init(self) -> None:
+        """GPT-2's initialisation, drawn in the reference's order.
+
+        Every Linear and Embedding weight ~ N(0, 0.02), biases 0, LayerNorm
+        scale 1 and shift 0, visiting the leaf modules in registration order
+        (so the tied ``lm_head``, last, redraws the embedding); then the two
+        residual-writing projections of each block are redrawn with
+        ``std = 0.02 / sqrt(2 * n_layer)``, attention's before the MLP's. With
+        the construction draws of the ``nn`` modules before it, this sequence
+        reproduces the reference's seed-0 weights bit for bit
+        (``model.py:457-518``).
+        """
+        for mod in self.modules():
+            if isinstance(mod, (nn.Linear, nn.Embedding)):
+                mod.weight.normal_(0.0, 0.02)
+                if getattr(mod, "bias", None) is not None:
+                    mod.bias.zero_()
+            elif isinstance(mod, nn.LayerNorm):
+                mod.weight.fill_(1.0)
+                mod.bias.zero_()
+        if self.config.residual_scaled_init:
+            std = 0.02 / math.sqrt(2 * self.config.n_layer)
+            for block in self.h:
+                block.attn.c_proj.weight.normal_(0.0, std)
+                block.mlp.c_proj.weight.normal_(0.0, std)
 
     def position_embeddings(self, pos: torch.Tensor) -> torch.Tensor:
-        return self.wpe(pos) if self.wpe is not None else self.sinusoidal_pe[pos]
+        return self.wpe(pos)
 
     def forward(
         self,
         idx: torch.Tensor,
         targets: torch.Tensor | None = None,
         cache: KVCache | None = None,
-        need_weights: bool = False,
-        collect_taps: bool = False,
         last_only: bool = False,
     ) -> dict[str, Any]:
-        """``model.py:528-599``. ``last_only`` (an extension; the reference
-        always computes every position) returns logits ``(B, 1, V)`` of the
-        last position only, for a prefill that needs nothing else: the head
-        is the largest product of a long prompt."""
-        if collect_taps:
-            raise NotImplementedError("activation taps belong to the verification tooling, not this library")
-        _, T = idx.shape
-        past = cache.seq_len if cache is not None else 0
-        if past + T > self.config.n_positions:
+        """Logits ``(B, T, vocab)`` of ``idx`` ``(B, T)`` (``model.py:528-599``).
+
+        With a ``cache``, ``idx`` holds only the new tokens, placed after the
+        cached ones. ``targets`` adds the mean cross entropy (``-100``
+        ignored) as ``loss``. ``last_only`` returns the last position's logits
+        ``(B, 1, vocab)`` only -- all a prefill needs, and the head is the
+        largest product of a long prompt.
+        """
+        T = idx.shape[1]
+        first = 0 if cache is None else cache.seq_len
+        if first + T > self.config.n_positions:
             raise ValueError(
-                f"sequence of length {past + T} exceeds n_positions={self.config.n_positions}; "
+                f"sequence of length {first + T} exceeds n_positions={self.config.n_positions}; "
                 f"learned position embeddings cannot extrapolate"
             )
-        pos = torch.arange(past, past + T, dtype=torch.long, device=idx.device)
-        x = self.drop(self.wte(idx) + self.position_embeddings(pos))
-        attentions = []
+        if last_only and targets is not None:
+            raise ValueError("last_only computes no loss: the loss needs every position's logits")
+        pos = torch.arange(first, first + T, device=idx.device)
+        x = self.wte(idx) + self.wpe(pos)
+        if self.training and self.config.dropout:
+            x = F.dropout(x, self.config.dropout, training=True)
         for block in self.h:
-            x, probs = block(x, cache=cache, need_weights=need_weights)
-            if probs is not None:
-                attentions.append(probs)
+            x = block(x, cache)
         if last_only:
-            if targets is not None:
-                raise ValueError("last_only computes no loss: the loss needs every position's logits")
-            x = x[:, -1:, :]
+            x = x[:, -1:]
         logits = self.lm_head(self.ln_f(x))
         out: dict[str, Any] = {"logits": logits}
-        if need_weights:
-            out["attentions"] = attentions
         if targets is not None:
-            out["loss"] = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.reshape(-1), ignore_index=-100)
+            out["loss"] = F.cross_entropy(logits.flatten(0, 1), targets.reshape(-1), ignore_index=-100)
         return out
-
-    def num_parameters(self, non_embedding: bool = False) -> int:
-        n = sum(p.numel() for p in self.parameters())
-        if non_embedding and self.wpe is not None:
-            n -= self.wpe.weight.numel()
-        return n

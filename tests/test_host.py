@@ -96,7 +96,7 @@ def test_host_model_init_matches_reference(reference_decode, label):
 def test_param_count_and_tying():
     torch.manual_seed(0)
     m = g.GPT(g.GPTConfig())
-    assert m.num_parameters() == 124_439_808
+    assert sum(p.numel() for p in m.parameters()) == 124_439_808   # the tied matrix once
     assert m.lm_head.weight is m.wte.weight
 
 
@@ -165,3 +165,59 @@ def test_last_only_logits_equal_the_last_row():
     assert torch.allclose(last[:, 0], full[:, -1], atol=1e-6, rtol=1e-5)
     with pytest.raises(ValueError):
         m(idx, targets=idx, last_only=True)
+
+
+@pytest.mark.parametrize("field,value", [("norm_position", "post"), ("pos_embedding", "sinusoidal"),
+                                         ("activation", "relu"), ("n_kv_head", 2), ("use_sdpa", True),
+                                         ("tie_weights", False)])
+def test_model_refuses_layouts_outside_gpt2(field, value):
+    """The host model is GPT-2's inference layout; the reference's ablation
+    switches raise instead of silently computing something else."""
+    cfg = g.GPTConfig(vocab_size=64, n_positions=16, n_layer=1, n_head=4, n_embd=32, **{field: value})
+    with pytest.raises(NotImplementedError, match=field):
+        g.GPT(cfg)
+
+
+def test_kv_cache_growth_equals_concatenation():
+    """Appends of 1..7 rows across several capacity doublings hold exactly the
+    concatenated history, per layer, with per-layer lengths."""
+    gen = torch.Generator().manual_seed(1)
+    c = g.KVCache.empty(2)
+    hist = []
+    for t in (5, 1, 1, 7, 3, 1, 1, 6, 2):
+        k = torch.randn(2, 3, t, 4, generator=gen)
+        v = torch.randn(2, 3, t, 4, generator=gen)
+        hist.append((k, v))
+        kk, vv = c.update(0, k, v)
+        assert torch.equal(kk, torch.cat([h[0] for h in hist], dim=2))
+        assert torch.equal(vv, torch.cat([h[1] for h in hist], dim=2))
+    assert c.seq_len == 27 and c.length(1) == 0
+    assert torch.equal(c.keys[0], kk) and c.keys[1] is None
+
+
+def test_time_call_and_bench_rows_on_cpu():
+    calls = []
+    t = g.time_call(lambda: calls.append(1), "cpu", repeats=4, warmup=2)
+    assert len(calls) == 6 and set(t) == {"median_s", "min_s", "mean_s", "std_s"} and t["min_s"] >= 0
+    torch.manual_seed(0)
+    m = g.GPT(g.GPTConfig(vocab_size=64, n_positions=24, n_layer=1, n_head=4, n_embd=32))
+    rows = g.benchmark_generation(m, [5, 20], new_tokens=6, device="cpu", repeats=1, warmup=0, mode="eager")
+    assert [(r.use_cache, r.prompt_len) for r in rows] == [(True, 5), (False, 5)]   # 20 + 6 > 24: skipped
+    d = rows[0].to_dict()
+    assert list(d)[:10] == ["use_cache", "prompt_len", "new_tokens", "batch_size", "median_s", "min_s", "std_s",
+                            "ms_per_token", "tokens_per_s", "device"]
+    assert d["decoder"] == "eager" and d["tokens_per_s"] == pytest.approx(6 / d["median_s"])
+    with pytest.raises(ValueError):
+        g.benchmark_generation(m, [5], mode="sampled", device="cpu")
+
+
+def test_paired_loss_delta():
+    from gpt2_harness_amd.experiment import paired_loss_delta
+
+    d = paired_loss_delta([2.0, 2.5, 3.0, 3.5], [1.9, 2.3, 2.9, 3.3])
+    assert d["per_chunk"] == pytest.approx([0.1, 0.2, 0.1, 0.2])
+    assert d["mean"] == pytest.approx(0.15) and d["stderr"] == pytest.approx(0.05 / 3 ** 0.5)   # sd 0.1/sqrt(3), n 4
+    assert d["distinguishable"]
+    assert not paired_loss_delta([1.0, 1.2], [1.1, 1.1])["distinguishable"]   # mean 0
+    with pytest.raises(ValueError):
+        paired_loss_delta([1.0], [1.0, 2.0])
