@@ -7,8 +7,10 @@ package does not touch the GPU; the first kernel call loads the library and
 raises if it is missing or no ROCm GPU is visible.
 """
 
+from .benchmark import BenchRow, benchmark_generation, model_size_bytes, time_call
 from .config import GPT2_SIZES, GPTConfig, gpt2_config
 from .decode import FusedDecoder, GraphDecoder, generate_graph, make_decoder
+from .experiment import SCHEMES, run_quantization_table
 from .model import GPT, KVCache
 from .qlinear import QuantLinear
 from .quantization import (
@@ -30,6 +32,7 @@ from .quantization import (
 from .sampling import generate
 
 __all__ = [
+    "BenchRow",
     "GPT",
     "GPT2_SIZES",
     "FusedDecoder",
@@ -38,13 +41,16 @@ __all__ = [
     "KVCache",
     "QuantLinear",
     "QuantResult",
+    "SCHEMES",
     "SyntheticTokenStream",
     "TARGET_SUFFIXES",
+    "benchmark_generation",
     "generate",
     "generate_graph",
     "gpt2_config",
     "load_packed",
     "make_decoder",
+    "model_size_bytes",
     "pack_int4",
     "packed_size_bytes",
     "perplexity_with_error_bars",
@@ -53,6 +59,8 @@ __all__ = [
     "quantize_linear",
     "quantize_model",
     "quantize_tensor",
+    "run_quantization_table",
     "save_packed",
+    "time_call",
     "unpack_int4",
 ]
