@@ -207,6 +207,16 @@ extern "C" int tiq_gemm_w8(const void* x, int x_dtype, int64_t M, int64_t K, int
     return launch_gemm(a);
 }
 
+extern "C" int tiq_gemm_w8_tile(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,
+                                const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                                int tile, void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, reinterpret_cast<const uint8_t*>(q), K, scale, nullptr, 0, bias,
+                             N, y, y_dtype, ldy, stream, kW8);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    return launch_gemm_tile(a, tile);
+}
+
 extern "C" int tiq_linear_w4(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                              const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
                              void* stream) {

@@ -709,9 +709,6 @@ int64_t decode_splits(int64_t M, int64_t K, int64_t N) {
     (void)M;
     int64_t S = (K / 32) / (kWaves * 6);
     if (S <= 1 && (N + 31) / 32 <= 64 && K / 32 >= 2 * kWaves) S = 2;
-    // TIQ_DECODE_SPLITS (read on every call, far cheaper than a launch) fixes
-    // the count, so that one process can measure each
-    if (const char* e = getenv("TIQ_DECODE_SPLITS")) S = std::max(1, atoi(e));
     S = std::min<int64_t>(S, (K / 32) / kWaves);
     return std::max<int64_t>(1, std::min<int64_t>(S, 32));
 }

@@ -56,6 +56,9 @@ int check_linear(const LinearArgs& a);
 
 int launch_gemv(const LinearArgs& a);
 int launch_gemm(const LinearArgs& a);
+// The GEMM with a given tile configuration: 0 automatic, 1-4 the LDS-dequant
+// kernel's tiles (gemm.hip), 10-12 the staged int8 kernel's (256x256, 256x128, 128x128).
+int launch_gemm_tile(const LinearArgs& a, int tile);
 // True when the MFMA GEMM has a kernel for these arguments.
 bool gemm_supported(const LinearArgs& a);
 

@@ -166,6 +166,17 @@ int tiq_gemm_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                 const int8_t* q, const float* scale, const float* bias, int64_t N,
                 void* y, int y_dtype, int64_t ldy, void* stream);
 
+/* tiq_gemm_w8 with an explicit tile configuration, for tests and
+ * measurement: 0 = the automatic choice, 1-4 = the LDS-dequant kernel at
+ * 128x128 / 256x128 / 128x256 / 256x128 (8 wavefronts) tiles, 10-12 = the
+ * register-staged kernel at 256x256 / 256x128 / 128x128 tiles (falls back to
+ * the automatic tile when that kernel does not take the shape). No
+ * counterpart in the reference (same interface as tiq_gemm_w8); the product
+ * path never calls it. */
+int tiq_gemm_w8_tile(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                     const int8_t* q, const float* scale, const float* bias, int64_t N,
+                     void* y, int y_dtype, int64_t ldy, int tile, void* stream);
+
 /* int4 weights in the reference's nibble layout (per-row scale, K even,
  * row n at byte n * K / 2). Same contract as tiq_linear_w8. */
 int tiq_linear_w4(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
