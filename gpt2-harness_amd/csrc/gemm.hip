@@ -80,16 +80,26 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
 
+// Group-wise int4 (FMT == kW4G): the nibbles are staged exactly as the
+// reference layout's, and every group of `group` columns (a multiple of BK, so
+// no k step straddles two groups) is accumulated into its own fp32 partial
+// sums (MFMA from zero at the group's first step); at the group's last step
+// each partial is multiplied by its column's fp16 scale (converted exactly to
+// fp32) and added to the running sums, so the result is
+//     y[m, n] = sum_g s[n, g] * (sum_{k in g} x[m, k] * q[n, k]) + bias[n]
+// with no rounding beyond fp32 accumulation. The last group may be short
+// (K = 1600 with group 128: twelve groups of two steps and one of one).
 template <int BM, int BN, int WAVES_M, int WAVES_N, int OCC, int FMT, typename TY>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
-    const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
-    int K) {
+    const float* __restrict__ scale, const uint16_t* __restrict__ scale16, int group,
+    const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N, int K) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
     constexpr int TM = WM / 32, TN = WN / 32;            // 32 x 32 MFMA tiles per wave
     constexpr int A_VEC = BM * BK / 8 / NT;              // 16-byte chunks of A per thread
     constexpr int CODES = (FMT == kW8) ? 16 : 32;        // weight codes per 16-byte load
+    constexpr bool GROUPED = FMT == kW4G;
     constexpr int B_VEC = BN * BK / CODES / NT;
     constexpr int B_PER_ROW = BK / CODES;
     static_assert(A_VEC >= 1 && B_VEC >= 1 && BM * BK % (8 * NT) == 0 && BN * BK % (CODES * NT) == 0,
@@ -136,6 +146,20 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    // group-wise scales: this lane's output columns (one per 32-wide tile
+    // column j, clamped for a partial tile), the group's partial sums, and the
+    // group's scales, requested at the group's first step
+    const int steps_per_group = GROUPED ? group / BK : 1;
+    const int ngroups = GROUPED ? (K + group - 1) / group : 1;
+    int64_t srow[TN];
+    floatx16 part[GROUPED ? TM : 1][GROUPED ? TN : 1];
+    uint16_t gsc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = n_blk + wn + j * 32 + (lane & 31);
+        srow[j] = (int64_t)(n < N ? n : N - 1) * ngroups;
+        gsc[j] = 0;
+    }
 
     const int frag_row = lane & 31, frag_c = lane >> 5;  // row in the tile, chunk within a k16 step
     const int nk = K / BK;
@@ -180,6 +204,19 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
         const int buf = s & 1;
         const int kn = (s + 1 < nk) ? (s + 1) * BK : s * BK;
         TIQ_LOAD_TILES(kn)
+        if constexpr (GROUPED) {
+            if (s % steps_per_group == 0) {  // a new group: its scales, and partial sums from zero
+                const int g = s / steps_per_group;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) gsc[j] = scale16[srow[j] + g];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) part[i][j][r] = 0.f;
+            }
+        }
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
             bf16x8 af[TM], bfr[TN];
@@ -193,8 +230,24 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TN; ++j) {
+                    if constexpr (GROUPED)
+                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], part[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        if constexpr (GROUPED) {
+            if ((s + 1) % steps_per_group == 0 || s + 1 == nk) {  // the group's last step
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const float sg = f16_bits_to_f32(gsc[j]);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(part[i][j][r], sg, acc[i][j][r]);
+                }
+            }
         }
         TIQ_STORE_TILES(buf ^ 1)
         __syncthreads();
@@ -206,7 +259,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     for (int j = 0; j < TN; ++j) {
         const int n = n_blk + wn + j * 32 + (lane & 31);
         if (n >= N) continue;
-        const float s = scale[n];
+        const float s = GROUPED ? 1.f : scale[n];
         const float b = bias ? bias[n] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -228,13 +281,13 @@ template <int BM, int BN, int WMW, int WNW, int OCC, int FMT, typename TY>
 int run_gemm32(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     hipLaunchKernelGGL((gemm32_kernel<BM, BN, WMW, WNW, OCC, FMT, TY>), dim3((unsigned)tiles), dim3(WMW * WNW * 64),
-                       0, a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
-                       static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K);
+                       0, a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.scale16, a.group,
+                       a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K);
     return launch_status();
 }
 
-// Tile configurations, selectable for measurement through TIQ_GEMM_TILE
-// (0 = automatic).
+// Tile configurations (0 = automatic), selectable through tiq_gemm_w8_tile
+// for tests and measurement.
 template <int FMT, typename TY>
 int dispatch_tile(const LinearArgs& a, int tile) {
     switch (tile) {
@@ -250,16 +303,8 @@ int dispatch_tile(const LinearArgs& a, int tile) {
     return run_gemm32<128, 128, 2, 2, 2, FMT, TY>(a);
 }
 
-int tile_override() {
-    // read on every call (a getenv is far cheaper than a launch) so that one
-    // process can measure or test each tile configuration
-    const char* e = getenv("TIQ_GEMM_TILE");
-    return e ? atoi(e) : 0;
-}
-
 template <int FMT>
-int dispatch_gemm(const LinearArgs& a) {
-    const int tile = tile_override();
+int dispatch_gemm(const LinearArgs& a, int tile) {
     if (FMT == kW8 && (tile == 0 || tile >= 10) && staged_gemm_supported(a))
         return launch_staged_gemm(a, tile >= 10 ? tile - 10 : staged_gemm_choice(a.M, a.N, a.K));
     if (a.y_dtype == TIQ_F32) return dispatch_tile<FMT, float>(a, tile);
@@ -270,7 +315,9 @@ int dispatch_gemm(const LinearArgs& a) {
 
 bool gemm_supported(const LinearArgs& a) {
     if (a.x_dtype != TIQ_BF16) return false;
-    if (a.fmt == kW4G) return false;
+    if (a.fmt == kF32) return false;
+    // group-wise int4: whole k steps per group (the GPT-2 group of 128 is two)
+    if (a.fmt == kW4G && (a.group % BK != 0 || !aligned(a.scale16, 2))) return false;
     if (a.K % BK != 0) return false;
     if (!aligned(a.x, 16) || a.ldx % 8 != 0) return false;
     if (!aligned(a.w, 16) || a.ldw % 16 != 0) return false;
@@ -278,10 +325,14 @@ bool gemm_supported(const LinearArgs& a) {
     return true;
 }
 
-int launch_gemm(const LinearArgs& a) {
+int launch_gemm_tile(const LinearArgs& a, int tile) {
     if (!gemm_supported(a)) return TIQ_EUNSUPPORTED;
-    if (a.fmt == kW8) return dispatch_gemm<kW8>(a);
-    return dispatch_gemm<kW4>(a);
+    if (tile < 0 || (tile > 4 && (tile < 10 || tile > 12))) return TIQ_EINVAL;
+    if (a.fmt == kW8) return dispatch_gemm<kW8>(a, tile);
+    if (a.fmt == kW4G) return dispatch_gemm<kW4G>(a, tile);
+    return dispatch_gemm<kW4>(a, tile);
 }
+
+int launch_gemm(const LinearArgs& a) { return launch_gemm_tile(a, 0); }
 
 }  // namespace tiq

@@ -44,6 +44,9 @@ def _call(entry, x, q, scale, b, N, y, *extra):
         group = extra[0]
         rc = fn(x.data_ptr(), xd, M, K, x.stride(0), q.data_ptr(), scale.data_ptr(), group, bp, N, y.data_ptr(), yd,
                 y.stride(0), st)
+    elif entry == "tiq_gemm_w8_tile":
+        rc = fn(x.data_ptr(), xd, M, K, x.stride(0), q.data_ptr(), scale.data_ptr(), bp, N, y.data_ptr(), yd,
+                y.stride(0), extra[0], st)
     else:
         rc = fn(x.data_ptr(), xd, M, K, x.stride(0), q.data_ptr(), scale.data_ptr(), bp, N, y.data_ptr(), yd,
                 y.stride(0), st)
@@ -51,7 +54,7 @@ def _call(entry, x, q, scale, b, N, y, *extra):
     torch.cuda.synchronize()
 
 
-def _run_w8(entry, dev, c_oracle, K, N, M, x_dtype, seed=0, bias=True):
+def _run_w8(entry, dev, c_oracle, K, N, M, x_dtype, seed=0, bias=True, *extra):
     w, x, b = _inputs(K, N, M, seed, x_dtype, bias)
     q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
     qd, sd = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev)
@@ -59,8 +62,8 @@ def _run_w8(entry, dev, c_oracle, K, N, M, x_dtype, seed=0, bias=True):
     xd = x.to(dev)
     y32 = torch.empty(M, N, device=dev)
     ybf = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-    _call(entry, xd, qd, sd, bd, N, y32)
-    _call(entry, xd, qd, sd, bd, N, ybf)
+    _call(entry, xd, qd, sd, bd, N, y32, *extra)
+    _call(entry, xd, qd, sd, bd, N, ybf, *extra)
     y_ref = OL.linear_ref(x, OL.dequantize(q, s), b)
     ok, err, bound = OL.within_tolerance(y32, y_ref, TOL)
     assert ok, f"{entry} M={M} K={K} N={N} {x_dtype}: max err {err:.3g} > {bound:.3g}"
@@ -91,14 +94,26 @@ def test_gemm_w8_small_shapes(dev, c_oracle, KN, M):
     _run_w8("tiq_gemm_w8", dev, c_oracle, *KN, M, torch.bfloat16, seed=M, bias=False)
 
 
-# Every GEMM tile configuration (TIQ_GEMM_TILE: 10/11/12 the register-staged
-# int8 kernel at 256x256 / 256x128 / 128x128 tiles, 1 the 128x128 kernel that
-# also serves int4), on full, partial-row and partial-column tiles.
-@pytest.mark.parametrize("tile", [10, 11, 12, 1])
+# Every GEMM tile configuration through tiq_gemm_w8_tile (10/11/12 the
+# register-staged int8 kernel at 256x256 / 256x128 / 128x128 tiles, 1-4 the
+# LDS-dequant kernel that also serves int4), on full, partial-row and
+# partial-column tiles.
+@pytest.mark.parametrize("tile", [10, 11, 12, 1, 2, 3, 4])
 @pytest.mark.parametrize("K,N,M", [(1600, 1600, 512), (1600, 4800, 300), (6400, 1600, 257), (768, 2304, 1024)])
-def test_gemm_w8_tiles(dev, c_oracle, monkeypatch, tile, K, N, M):
-    monkeypatch.setenv("TIQ_GEMM_TILE", str(tile))
-    _run_w8("tiq_gemm_w8", dev, c_oracle, K, N, M, torch.bfloat16, seed=tile + M, bias=M % 2 == 0)
+def test_gemm_w8_tiles(dev, c_oracle, tile, K, N, M):
+    _run_w8("tiq_gemm_w8_tile", dev, c_oracle, K, N, M, torch.bfloat16, tile + M, M % 2 == 0, tile)
+
+
+def test_gemm_w8_tile_rejects_unknown_configuration(dev):
+    L = _lib.lib()
+    x = torch.zeros(256, 64, device=dev, dtype=torch.bfloat16)
+    q = torch.zeros(64, 64, device=dev, dtype=torch.int8)
+    s = torch.ones(64, device=dev)
+    y = torch.empty(256, 64, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    for bad in (-1, 5, 9, 13):
+        assert L.tiq_gemm_w8_tile(x.data_ptr(), 1, 256, 64, 64, q.data_ptr(), s.data_ptr(), None, 64, y.data_ptr(),
+                                  0, 64, bad, st) == -1
 
 
 # fp32 activations through the matrix cores (three exact bf16 planes): the
@@ -302,6 +317,39 @@ def test_linear_w4_groupwise(dev, c_oracle, KN, M):
     w_hat = torch.from_numpy(OQ.dequantize_groupwise_int4(packed, s16, K, 128))
     ok, err, bound = OL.within_tolerance(y, OL.linear_ref(x, w_hat, b))
     assert ok, (err, bound)
+
+
+def _run_w4g(dev, c_oracle, K, N, M, group, seed, bias=True):
+    w, x, b = _inputs(K, N, M, seed, torch.bfloat16, bias)
+    packed, s16 = c_oracle.quantize_groupwise_int4(w.numpy(), group)
+    pd, sd = torch.from_numpy(packed).to(dev), torch.from_numpy(s16.view(np.uint16).copy()).to(dev)
+    bd, xd = (None if b is None else b.to(dev)), x.to(dev)
+    y32 = torch.empty(M, N, device=dev)
+    ybf = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    _call("tiq_linear_w4g", xd, pd, sd, bd, N, y32, group)
+    _call("tiq_linear_w4g", xd, pd, sd, bd, N, ybf, group)
+    w_hat = torch.from_numpy(OQ.dequantize_groupwise_int4(packed, s16, K, group))
+    ok, err, bound = OL.within_tolerance(y32, OL.linear_ref(x, w_hat, b))
+    assert ok, f"w4g M={M} K={K} N={N} group={group}: max err {err:.3g} > {bound:.3g}"
+    assert torch.equal(ybf.cpu(), y32.cpu().to(torch.bfloat16)), "bf16 output is not RNE of the fp32 output"
+
+
+# Group-wise int4 at prefill sizes: the MFMA GEMM with one fp32 partial per
+# 128-column group, the group's fp16 scale applied to it (K = 1600: twelve
+# groups and a ragged 64-column one; K = 6400: fifty groups).
+@pytest.mark.parametrize("KN", XL)
+@pytest.mark.parametrize("M", [256, 1024, 4096])
+def test_gemm_w4_groupwise_prefill(dev, c_oracle, KN, M):
+    _run_w4g(dev, c_oracle, *KN, M, 128, seed=M + KN[0], bias=M != 1024)
+
+
+# other group widths (multiples of the 64-column k step, a last group of one
+# step), partial row and column tiles, and a width the GEMM does not take
+# (32: the vector-ALU kernel serves it)
+@pytest.mark.parametrize("K,N,M,group", [(1600, 4800, 300, 64), (1600, 1600, 257, 192), (768, 2304, 513, 256),
+                                         (3072, 768, 129, 1024), (1600, 1000, 256, 32), (6400, 1600, 384, 6400)])
+def test_gemm_w4_groupwise_widths_and_partial_tiles(dev, c_oracle, K, N, M, group):
+    _run_w4g(dev, c_oracle, K, N, M, group, seed=M + group)
 
 
 def test_zero_rows_is_a_no_op(dev):
