@@ -200,8 +200,7 @@ def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed):
 def hbm_stream_section(dev, reps=10):
     """Measured-achievable HBM rate beside the 8 TB/s datasheet figure:
     torch's device copy of 1 GiB (read + write counted), the median of `reps`
-    launches between HIP events. (A one-launch pure read reaches 6.2 TB/s at
-    200 MB, csrc/hbm_read_probe.hip.)"""
+    launches between HIP events."""
     import torch
 
     n = 1 << 28
@@ -221,11 +220,16 @@ def hbm_stream_section(dev, reps=10):
     return {"copy": {"GB/s": 8 * n / (statistics.median(ts) * 1e-3) / 1e9, "bytes": 8 * n}}
 
 
-def gemm_section(M, kn, dev, reps=20):
-    """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws) per shape: `reps` launches back
-    to back between one HIP event pair. Beside it, as the measured-achievable
-    reference (not this library's path), the platform's bf16 GEMM
-    (torch.matmul -> hipBLASLt) on bf16 weights of the same shape."""
+def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
+    """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws; with fmt="int4_g128" the
+    group-wise int4 GEMM, tiq_linear_w4g, group 128) per shape: `reps` launches back
+    to back between one HIP event pair, rotating over `copies` independent
+    (activation, weight, output) sets (at M = 4096 on 1600 x 6400 the eight
+    sets hold 600 MB, past the 256 MB Infinity Cache), so no launch finds its
+    operands left in the caches by the one before. Beside it, as the
+    measured-achievable reference (not this library's path), the platform's
+    bf16 GEMM (torch.matmul -> hipBLASLt) on bf16 weights of the same shape,
+    rotated the same way."""
     import torch
 
     import gpt2_harness_amd as g
@@ -235,45 +239,54 @@ def gemm_section(M, kn, dev, reps=20):
     out = {}
     gen = torch.Generator(device=dev).manual_seed(1)
 
-    def timed(fn):
-        for _ in range(3):
-            fn()
+    def timed(fns):
+        for f in fns[:3]:
+            f()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        for _ in range(reps):
-            fn()
+        for i in range(reps):
+            fns[i % len(fns)]()
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1e3 / reps
 
     for K, N in kn:
-        w = torch.randn(N, K, generator=gen, device=dev) * 0.02
-        q, s = g.quantize_tensor(w, 8)
-        s = s.reshape(-1).contiguous()
-        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
-        y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-        st = torch.cuda.current_stream().cuda_stream
-
         n_ws = int(L.tiq_gemm_w8_workspace(1, M, K, N))  # split-K partials when the tiles are few
         ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=dev)
+        st = torch.cuda.current_stream().cuda_stream
+        sets, lib_sets = [], []
+        for _ in range(copies):
+            w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+            if fmt == "int8":
+                q, s = g.quantize_tensor(w, 8)
+                s = s.reshape(-1).contiguous()
+            else:
+                q, s = g.quantize_groupwise_int4(w, 128)
+            x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+            sets.append((x, q, s, torch.empty(M, N, device=dev, dtype=torch.bfloat16)))
+            lib_sets.append((x, w.to(torch.bfloat16)))
+            del w
 
-        def run():
-            rc = L.tiq_gemm_w8_ws(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1, N,
-                                  ws.data_ptr(), n_ws, st)
+        def run(x, q, s, y):
+            if fmt == "int8":
+                rc = L.tiq_gemm_w8_ws(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1,
+                                      N, ws.data_ptr(), n_ws, st)
+            else:
+                rc = L.tiq_linear_w4g(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), 128, None, N, y.data_ptr(),
+                                      1, N, st)
             if rc:
-                raise RuntimeError(f"tiq_gemm_w8_ws status {rc}")
+                raise RuntimeError(f"{fmt} GEMM status {rc}")
 
-        us = timed(run)
+        us = timed([lambda a=a: run(*a) for a in sets])
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
-        wb = w.to(torch.bfloat16)
-        del w
-        us_lib = timed(lambda: torch.matmul(x, wb.T))
+        us_lib = timed([lambda x=x, wb=wb: torch.matmul(x, wb.T) for x, wb in lib_sets])
         tf_lib = 2.0 * M * N * K / (us_lib * 1e-6) / 1e12
         out[f"{K}x{N}"] = {"us": us, "TFLOP/s": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
                            "library_bf16_us": us_lib, "library_bf16_TFLOP/s": tf_lib,
                            "vs_library_bf16": tf / tf_lib}
-    return {"M": M, "per_shape": out}
+        del sets, lib_sets
+    return {"M": M, "weights": fmt, "copies": copies, "per_shape": out}
 
 
 def quantize_section(dev, reps=5, copies=8):
@@ -436,25 +449,32 @@ def eval_section(dev):
     return res
 
 
-def decode_xl_section(dev, new_tokens=128):
+def decode_xl_section(dev, new_tokens=128, check_steps=4):
     """GPT-2-XL (48 layers, d 1600, 25 heads) seed 0, int8 per-channel, batch
     32, 128-token random prompts, greedy +new_tokens: end-to-end tokens/s
     (prefill + decode) and the per-Linear decode time / GB/s at M = 32.
     The step is the fused decoder's batched chain (tiq_decode_linear,
-    tiq_decode_attention_planes), captured once and replayed per token."""
+    tiq_decode_attention_planes), captured once and replayed per token.
+    ``tokens_match_oracle``: the first ``check_steps`` generated tokens of all
+    32 sequences against the oracle's fp32 CPU generation of the same seed-0
+    quantized model."""
     import torch
 
     import gpt2_harness_amd as g
     from gpt2_harness_amd import _lib
+    from oracle import model as OM
 
     torch.manual_seed(0)
     cfg = g.gpt2_config("gpt2-xl")
-    model = g.GPT(cfg).to(dev).eval()
+    model = g.GPT(cfg).eval()
+    p_cpu = {k: v.detach().clone() for k, v in model.state_dict().items() if k != "lm_head.weight"}
+    model = model.to(dev)
     qm, _ = g.quantize_model(model, 8)
     del model
     torch.manual_seed(0)
     B, T0 = 32, 128
-    prompt = torch.randint(0, cfg.vocab_size, (B, T0)).to(dev)
+    prompt_cpu = torch.randint(0, cfg.vocab_size, (B, T0))
+    prompt = prompt_cpu.to(dev)
     dec = g.FusedDecoder(qm, B, T0 + new_tokens)
     dec.start(prompt)
     dec.capture()
@@ -468,49 +488,102 @@ def decode_xl_section(dev, new_tokens=128):
         dec.graph.replay()
     torch.cuda.synchronize()
     t_dec = time.perf_counter() - t0
+    got = dec.out[:, : T0 + check_steps].cpu()
     res = {"model": "gpt2-xl (1.56B) seed 0, int8 per-channel", "batch": B, "prompt": T0, "new_tokens": new_tokens,
            "prefill_ms": t_pre * 1e3, "decode_ms_per_step": t_dec * 1e3 / (new_tokens - 1),
            "tokens_per_s": B * new_tokens / (t_pre + t_dec),
            "decode_tokens_per_s": B * (new_tokens - 1) / t_dec}
-    # per-Linear decode time of layer 0 at M = 32, each called as the decode
-    # step calls it (tiq_decode_linear from the previous op's operand planes),
-    # 20 calls captured in a HIP graph, the graph replayed 5 times (HIP
-    # events); GB/s by the decode GEMV formula N K + 4 N + 2 M K + 2 M N
+    # per-Linear decode time at M = 32, each called as the decode step calls it
+    # (tiq_decode_linear from the previous op's operand planes): a graph of the
+    # 48 layers' calls of one Linear (their weights: 123-492 MB, past the 256 MB
+    # Infinity Cache for all but attn.c_proj), replayed after a 512 MiB write has
+    # evicted the caches, HIP events around each replay; GB/s by the decode GEMV
+    # formula N K + 4 N + 2 M K + 2 M N
     per = {}
-    blk = qm.h[0]
     W8, gelu = _lib.WF_INT8, _lib.ACT_GELU_TANH
-    calls = (("c_attn", blk.attn.c_attn, lambda l: dec._dl(l, W8, y=dec.qkv, planes_in=dec.p_ln1)),
-             ("attn.c_proj", blk.attn.c_proj, lambda l: dec._dl(l, W8, y=dec.x, planes_in=dec.p_att, res=dec.x,
-                                                               next_ln=blk.ln_2, planes_out=dec.p_ln2)),
-             ("c_fc", blk.mlp.c_fc, lambda l: dec._dl(l, W8, planes_in=dec.p_ln2, act=gelu, planes_out=dec.p_hid)),
-             ("mlp.c_proj", blk.mlp.c_proj, lambda l: dec._dl(l, W8, y=dec.x, planes_in=dec.p_hid, res=dec.x,
-                                                             next_ln=qm.h[1].ln_1, planes_out=dec.p_ln1)))
+    calls = (("c_attn", lambda b: b.attn.c_attn, lambda l, b, nb: dec._dl(l, W8, y=dec.qkv, planes_in=dec.p_ln1)),
+             ("attn.c_proj", lambda b: b.attn.c_proj,
+              lambda l, b, nb: dec._dl(l, W8, y=dec.x, planes_in=dec.p_att, res=dec.x, next_ln=b.ln_2,
+                                       planes_out=dec.p_ln2)),
+             ("c_fc", lambda b: b.mlp.c_fc,
+              lambda l, b, nb: dec._dl(l, W8, planes_in=dec.p_ln2, act=gelu, planes_out=dec.p_hid)),
+             ("mlp.c_proj", lambda b: b.mlp.c_proj,
+              lambda l, b, nb: dec._dl(l, W8, y=dec.x, planes_in=dec.p_hid, res=dec.x, next_ln=nb,
+                                       planes_out=dec.p_ln1)))
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
     s_cap = torch.cuda.Stream()
-    for name, lin, fn in calls:
-        K, N = lin.in_features, lin.out_features
+    blocks = list(qm.h)
+    for name, pick, fn in calls:
+        lin0 = pick(blocks[0])
+        K, N = lin0.in_features, lin0.out_features
+        layer_calls = [(pick(b), b, blocks[i + 1].ln_1 if i + 1 < len(blocks) else qm.ln_f)
+                       for i, b in enumerate(blocks)]
         with torch.cuda.stream(s_cap):
-            fn(lin)
+            fn(*layer_calls[0])
             torch.cuda.synchronize()
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr, stream=s_cap):
-                for _ in range(20):
-                    fn(lin)
+                for c in layer_calls:
+                    fn(*c)
         gr.replay()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(5):
+        ts = []
+        for _ in range(3):
+            flush.fill_(1)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
             gr.replay()
-        b.record()
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / 100
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / len(layer_calls))
+        us = statistics.median(ts)
         nbytes = N * K + 4 * N + 2 * B * K + 2 * B * N
         per[f"{K}x{N}"] = {"linear": name, "us": us, "GB/s": nbytes / (us * 1e-6) / 1e9}
         del gr
-    res["decode_linear_M32"] = per
+    del flush
+    res["decode_linear_M32_cold"] = per
     del dec, qm
     torch.cuda.empty_cache()
+    # the oracle on the same seed-0 weights, first check_steps tokens
+    threads = torch.get_num_threads()
+    torch.set_num_threads(min(16, host_cores()))
+    try:
+        t0 = time.perf_counter()
+        qp, _ = OM.quantize_params(p_cpu, 8, impl="c")
+        del p_cpu
+        want, margins = OM.generate_greedy(qp, OM.GPT2_XL, prompt_cpu, check_steps)
+        del qp
+    finally:
+        torch.set_num_threads(threads)
+    res["tokens_match_oracle"] = bool(torch.equal(got, want))
+    res["oracle_check"] = {"steps": check_steps, "sequences": B, "min_top2_margin": min(margins),
+                           "oracle_s": time.perf_counter() - t0}
     return res
+
+
+def schemes_section(dev):
+    """The reference experiment's table (run_quantization.py:31-158) on seed-0
+    GPT-2 small over synthetic tokens: fp32 baseline and the five schemes,
+    perplexity over 8 chunks x 2 batches x 4 windows of 128 tokens, paired
+    per-chunk loss deltas, quantize_model's size statistics, and speed = greedy
+    decode (64-token prompt, 16 new tokens) through the captured decoder."""
+    import torch
+
+    import gpt2_harness_amd as g
+
+    torch.manual_seed(0)
+    model = g.GPT(g.GPTConfig()).to(dev).eval()
+    ds = g.SyntheticTokenStream(50257, 8 * 2 * 4 * 128 + 1, 128, seed=0)
+    table = g.run_quantization_table(model, ds, device=dev)
+    del model
+    keep = ("label", "packed_bytes", "compression_ratio", "highlight")
+    rows = [{**{k: r[k] for k in keep if k in r}, "ppl": r["quality"]["ppl_of_mean_loss"],
+             "paired_dloss": r["quality"]["paired_loss_delta"]["mean"],
+             "paired_dloss_stderr": r["quality"]["paired_loss_delta"]["stderr"],
+             "tokens_per_s": r["speed"]["tokens_per_s"]} for r in table["rows"]]
+    b = table["baseline"]
+    return {"baseline": {"ppl": b["ppl_of_mean_loss"], "bytes": b["bytes"], "tokens_per_s": b["speed"]["tokens_per_s"]},
+            "rows": rows, "data": "synthetic uniform tokens (seed 0); random-init weights"}
 
 
 def cpu_baseline(budget_s: float = 10.0):
@@ -645,7 +718,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "quantize", "decode", "decode_xl", "eval", "copy"],
+    ap.add_argument("--only", choices=["gemv", "gemm", "gemm_g128", "quantize", "decode", "decode_xl", "eval", "schemes", "copy"],
                     default=None,
                     help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
                          "used to calibrate the HBM byte counters")
@@ -673,6 +746,9 @@ def main() -> int:
     if args.only == "gemm":
         print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev) for M in (256, 1024, 4096)}))
         return 0
+    if args.only == "gemm_g128":
+        print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev, fmt="int4_g128") for M in (256, 1024, 4096)}))
+        return 0
     if args.only == "quantize":
         print(json.dumps(quantize_section(dev)))
         return 0
@@ -684,6 +760,9 @@ def main() -> int:
         return 0
     if args.only == "eval":
         print(json.dumps(eval_section(dev)))
+        return 0
+    if args.only == "schemes":
+        print(json.dumps(schemes_section(dev)))
         return 0
 
     head = gemv_section(1, SMALL_KN, 12, 6, args.steps, args.warmup, dev, seed=0)
@@ -700,6 +779,8 @@ def main() -> int:
     if not args.quick and args.only is None:
         for M in (256, 1024, 4096):
             detail[f"gemm_xl_M{M}"] = gemm_section(M, XL_KN, dev)
+        for M in (256, 1024, 4096):
+            detail[f"gemm_xl_g128_M{M}"] = gemm_section(M, XL_KN, dev, fmt="int4_g128")
         print("# gemm done", file=sys.stderr, flush=True)
         detail["quantize_xl"] = quantize_section(dev)
         detail["decode_gpt2_small_int8"] = decode_section(dev)
@@ -707,6 +788,7 @@ def main() -> int:
         detail["decode_gpt2_xl_int8_b32"] = decode_xl_section(dev)
         print("# xl decode done", file=sys.stderr, flush=True)
         detail["eval_gpt2_small_int8"] = eval_section(dev)
+        detail["schemes_gpt2_small"] = schemes_section(dev)
         print("# eval done", file=sys.stderr, flush=True)
         cpu = cpu_baseline()
         detail["cpu_oracle"] = cpu_configs()

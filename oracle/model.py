@@ -105,23 +105,44 @@ def init_params(cfg: Shape, seed: int | None = 0) -> dict[str, torch.Tensor]:
 
 
 def quantize_params(p: dict[str, torch.Tensor], bits: int = 8, granularity: str = "per_channel",
-                    include_embedding: bool = False):
+                    include_embedding: bool = False, impl: str = "numpy"):
     """Simulated quantization of the target weights (``quantization.py:186-197``);
     with ``include_embedding`` also ``wte`` (``:189-192``), whose ``W_hat`` the
     tied head then uses (``forward`` reads ``wte.weight`` for both).
 
+    ``impl="c"`` codes per-channel weights with the C restatement
+    (``quant_oracle.c``, equal to the numpy one on every pinned case), one
+    host thread per tensor, for models too large for the numpy passes.
+
     Returns ``(params_with_W_hat, codes)`` where ``codes[name] = (q, scale)``.
     """
+    if impl not in ("numpy", "c"):
+        raise ValueError(f"impl must be 'numpy' or 'c', got {impl!r}")
     out = dict(p)
-    codes = {}
-    for key, w in p.items():
+    names = []
+    for key in p:
         name = key[: -len(".weight")] if key.endswith(".weight") else None
         is_emb = include_embedding and name == "wte"
-        if name is None or not (name.endswith(TARGET_SUFFIXES) or is_emb):
-            continue
-        q, s = Q.quantize_tensor(w.numpy(), bits, granularity)
+        if name is not None and (name.endswith(TARGET_SUFFIXES) or is_emb):
+            names.append(name)
+
+    def code(name):
+        w = p[name + ".weight"].numpy()
+        if impl == "c" and granularity == "per_channel":
+            return Q.c_oracle().quantize_per_channel(w, bits)
+        return Q.quantize_tensor(w, bits, granularity)
+
+    if impl == "c":
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=min(16, len(names) or 1)) as pool:
+            coded = list(pool.map(code, names))
+    else:
+        coded = [code(n) for n in names]
+    codes = {}
+    for name, (q, s) in zip(names, coded):
         codes[name] = (q, s)
-        out[key] = torch.from_numpy(q.astype(np.float32) * s)
+        out[name + ".weight"] = torch.from_numpy(q).to(torch.float32) * torch.from_numpy(np.asarray(s))
     return out, codes
 
 
@@ -140,8 +161,10 @@ class Cache:
 
 
 @torch.no_grad()
-def forward(p, cfg: Shape, idx: torch.Tensor, cache: Cache | None = None) -> torch.Tensor:
-    """Logits ``(B, T, V)`` of ``GPT.forward`` (fp32, explicit attention)."""
+def forward(p, cfg: Shape, idx: torch.Tensor, cache: Cache | None = None, last_only: bool = False) -> torch.Tensor:
+    """Logits ``(B, T, V)`` of ``GPT.forward`` (fp32, explicit attention);
+    ``last_only`` applies ``ln_f`` and the head to the last position only
+    (``(B, 1, V)``, the rows ``generate`` reads)."""
     B, T = idx.shape
     C, H = cfg.n_embd, cfg.n_head
     hd = C // H
@@ -180,6 +203,8 @@ def forward(p, cfg: Shape, idx: torch.Tensor, cache: Cache | None = None) -> tor
         m = F.linear(gelu_tanh(F.linear(h2, lw("mlp.c_fc.weight"), lw("mlp.c_fc.bias"))),
                      lw("mlp.c_proj.weight"), lw("mlp.c_proj.bias"))
         x = x + m
+    if last_only:
+        x = x[:, -1:]
     x = F.layer_norm(x, (C,), p["ln_f.weight"], p["ln_f.bias"], cfg.layer_norm_epsilon)
     return F.linear(x, p["wte.weight"])
 
@@ -194,7 +219,7 @@ def generate_greedy(p, cfg: Shape, idx: torch.Tensor, max_new_tokens: int):
         if idx.size(1) >= cfg.n_positions:
             break
         step_input = idx if step == 0 else idx[:, -1:]
-        logits = forward(p, cfg, step_input, cache)[:, -1, :]
+        logits = forward(p, cfg, step_input, cache, last_only=True)[:, -1, :]
         top2 = logits.topk(2, dim=-1).values
         margins.append(float((top2[:, 0] - top2[:, 1]).min()))
         nxt = logits.argmax(dim=-1, keepdim=True)

@@ -271,10 +271,16 @@ def test_fused_f32_head_with_ln(dev):
 
 @pytest.mark.parametrize("B,H,Hkv,pos,T", [(1, 12, 12, 0, 256), (1, 12, 12, 127, 256), (3, 25, 25, 200, 256),
                                            (2, 8, 2, 63, 256), (1, 12, 12, 127, 128), (2, 4, 4, 99, 100),
-                                           (2, 4, 4, 150, 200), (1, 4, 2, 700, 1024), (1, 3, 3, 1023, 1024)])
+                                           (2, 4, 4, 150, 200), (1, 4, 2, 700, 1024), (1, 3, 3, 1023, 1024),
+                                           (32, 25, 25, 0, 256), (32, 25, 25, 130, 256), (32, 25, 25, 255, 256),
+                                           (32, 25, 25, 256, 384), (32, 25, 25, 300, 384), (32, 25, 25, 383, 384),
+                                           (16, 25, 25, 100, 128)])
 def test_decode_attention(dev, B, H, Hkv, pos, T):
     """Slots past 128 / 256 (histories streamed chunk by chunk), caches whose
-    length is not a multiple of the 128-slot chunk, grouped kv heads."""
+    length is not a multiple of the 128-slot chunk, grouped kv heads. Layers
+    whose keys and values pass 32 MB (batch 32 at 25 heads: 105-157 MB; batch
+    16 at 128 slots: 26 MB does not) take the kernel whose reads are sized by
+    the filled slots instead of the whole cache."""
     hd = 64
     gen = torch.Generator().manual_seed(pos + H)
     qkv = torch.randn(B, (H + 2 * Hkv) * hd, generator=gen)
@@ -300,8 +306,12 @@ def test_decode_attention(dev, B, H, Hkv, pos, T):
     assert torch.equal(kd.cpu()[:, :, pos + 1 :], kc[:, :, pos + 1 :])
 
 
-def test_out_of_range_position_gives_nan_without_writes(dev):
-    B, H, hd, T = 1, 2, 64, 16
+@pytest.mark.parametrize("B,H,T", [(1, 2, 16), (32, 25, 256)])
+def test_out_of_range_position_gives_nan_without_writes(dev, B, H, T):
+    """A position outside the cache writes nothing and flags every output row
+    NaN, for the whole-cache kernel (small caches) and the filled-slot one
+    (the 105 MB batch-32 layer)."""
+    hd = 64
     qkv = torch.ones(B, 3 * H * hd, device=dev)
     kc = torch.zeros(B, H, T, hd, device=dev)
     vc = torch.zeros(B, H, T, hd, device=dev)

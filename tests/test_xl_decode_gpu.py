@@ -1,0 +1,121 @@
+"""GPT-2-XL shapes end to end: batched greedy decode against the oracle.
+
+The workload of the GPT-2-XL batch-32 benchmark (48 layers, d_model 1600,
+25 heads, vocab 50257, int8 per-channel Linears, 32 prompts of 128 tokens
+seeded as ``benchmark_generation`` seeds them, ``benchmark.py:167-170``) runs
+through the captured fused decoder -- the batched decode chain of
+``tiq_decode_linear`` / ``tiq_decode_attention_planes`` -- and its token ids
+are compared with the oracle's fp32 CPU generation of the same quantized
+model (``sampling.py:100-181`` + ``model.py:528-599``, restated in
+``oracle/model.py``).
+
+The weights follow GPT-2's init distribution (N(0, 0.02), residual-writing
+projections N(0, 0.02 / sqrt(2 n_layer)), unit LayerNorms, zero biases) drawn
+on the GPU from a seeded generator: drawing the reference's exact seed-0 CPU
+stream for 1.56B parameters takes about a minute, and that order is pinned
+separately by the GPT-2 small and tiny weight digests. Both sides then hold
+bit-identical fp32 weights.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+import time
+from pathlib import Path
+
+import pytest
+import torch
+
+import gpt2_harness_amd as g
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+
+
+def _host_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if quota != "max":
+            n = min(n, int(int(quota) / int(period)))
+    except (OSError, ValueError):
+        pass
+    return max(1, min(n, 16))
+
+
+def _params_on_gpu(shp: OM.Shape, seed: int, dev) -> dict[str, torch.Tensor]:
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    C, L = shp.n_embd, shp.n_layer
+
+    def normal(rows, cols, std=0.02):
+        return torch.randn(rows, cols, generator=gen, device=dev) * std
+
+    p = {"wte.weight": normal(shp.vocab_size, C), "wpe.weight": normal(shp.n_positions, C)}
+    for i in range(L):
+        pre = f"h.{i}."
+        for ln in ("ln_1", "ln_2"):
+            p[pre + ln + ".weight"] = torch.ones(C, device=dev)
+            p[pre + ln + ".bias"] = torch.zeros(C, device=dev)
+        for name, (n, k) in (("attn.c_attn", (3 * C, C)), ("attn.c_proj", (C, C)), ("mlp.c_fc", (4 * C, C)),
+                             ("mlp.c_proj", (C, 4 * C))):
+            std = 0.02 / math.sqrt(2 * L) if name.endswith("c_proj") else 0.02
+            p[pre + name + ".weight"] = normal(n, k, std)
+            p[pre + name + ".bias"] = torch.zeros(n, device=dev)
+    p["ln_f.weight"], p["ln_f.bias"] = torch.ones(C, device=dev), torch.zeros(C, device=dev)
+    return p
+
+
+def _model_from_params(shp: OM.Shape, p: dict[str, torch.Tensor], dev) -> g.GPT:
+    cfg = g.GPTConfig(vocab_size=shp.vocab_size, n_positions=shp.n_positions, n_layer=shp.n_layer,
+                      n_head=shp.n_head, n_embd=shp.n_embd)
+    with torch.device("meta"):
+        m = g.GPT(cfg)
+    m = m.to_empty(device=dev)
+    m.lm_head.weight = m.wte.weight
+    missing, unexpected = m.load_state_dict(p, strict=False)
+    assert set(missing) == {"lm_head.weight"} and not unexpected
+    return m.eval()
+
+
+def _decode_vs_oracle(shp, dev, batch, prompt_len, new_tokens, seed):
+    p = _params_on_gpu(shp, seed, dev)
+    p_cpu = {k: v.cpu() for k, v in p.items()}
+    qm, stats = g.quantize_model(_model_from_params(shp, p, dev), 8)
+    del p
+    assert stats["n_quantized_tensors"] == 4 * shp.n_layer
+    prompt = OM.benchmark_prompt(shp.vocab_size, batch, prompt_len)
+    dec = g.FusedDecoder(qm, batch, prompt_len + new_tokens)
+    assert dec.chain  # batched rows: the decode-chain kernels
+    got = g.generate_graph(qm, prompt.to(dev), new_tokens, decoder=dec).cpu()
+    del dec, qm
+    torch.cuda.empty_cache()
+    threads = torch.get_num_threads()
+    torch.set_num_threads(_host_threads())
+    try:
+        t0 = time.perf_counter()
+        qp, _ = OM.quantize_params(p_cpu, 8, impl="c")
+        del p_cpu
+        want, margins = OM.generate_greedy(qp, shp, prompt, new_tokens)
+        print(f"oracle {time.perf_counter() - t0:.1f} s; min top-2 margin {min(margins):.3g}", flush=True)
+    finally:
+        torch.set_num_threads(threads)
+    return got, want, margins
+
+
+def test_gpt2_xl_batch32_greedy_matches_oracle(dev):
+    """48 layers at batch 32, 128-token prompts: the prefill (three-plane MFMA
+    GEMMs at M = 4096), then 6 captured decode steps at positions 128..133."""
+    got, want, margins = _decode_vs_oracle(OM.GPT2_XL, dev, batch=32, prompt_len=128, new_tokens=6, seed=0)
+    assert got.shape == (32, 134)
+    assert got.tolist() == want.tolist(), f"min margin {min(margins):.3g}"
+
+
+def test_xl_width_batch32_decode_across_slot_256(dev):
+    """Two XL-width layers, batch 32, a 250-token prompt and 12 new tokens: the
+    cache of a layer (32 x 25 x 262 slots, 107 MB) takes the attention kernel
+    that sizes its reads by the filled slots, and positions 250..261 cross the
+    256 slots requested at launch into the chunked tail."""
+    shp = OM.Shape(n_layer=2, n_head=25, n_embd=1600)
+    got, want, margins = _decode_vs_oracle(shp, dev, batch=32, prompt_len=250, new_tokens=12, seed=1)
+    assert got.tolist() == want.tolist(), f"min margin {min(margins):.3g}"
