@@ -1,5 +1,8 @@
 // Linear entry points of the C ABI: argument checks and the choice between
 // the decode GEMV (vector ALUs) and the prefill GEMM (matrix cores).
+#include <atomic>
+#include <mutex>
+
 #include "tiq_internal.hpp"
 
 namespace tiq {
@@ -128,6 +131,7 @@ extern "C" const char* tiq_status_string(int status) {
         case TIQ_EALIGN: return "misaligned pointer or leading dimension";
         case TIQ_EUNSUPPORTED: return "unsupported shape or layout";
         case TIQ_EWORKSPACE: return "workspace too small";
+        case TIQ_ESCRATCH: return "request exceeds the fixed scratch of the allocation-free entry point";
         default: break;
     }
     if (status <= TIQ_EHIP_BASE) return hipGetErrorString((hipError_t)(TIQ_EHIP_BASE - status));
@@ -298,6 +302,56 @@ extern "C" size_t tiq_decode_planes_bytes(int64_t M, int64_t K) {
     return decode_planes_bytes(M, K);
 }
 
+// ------------------------------------------- allocation-free decode linear
+// tiq_decode_linear_noalloc runs tiq_decode_linear with this fixed array as
+// its workspace: TIQ_NOALLOC_SCRATCH_BYTES per GPU, held by the loaded code
+// object until the process ends. In host code the array's name only names the
+// symbol; its device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current, and only that address is passed to
+// the kernels. Every call on one GPU shares the array (calls that overlap on
+// one GPU race); nothing in it needs clearing between calls (the planes and
+// the partial slices are written whole before they are read).
+static __device__ __align__(256) uint8_t scratch[TIQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The scratch address on the device that runs `stream`.
+int noalloc_scratch(hipStream_t stream, void** out) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return status_of(e);
+    int dev = cur;
+    if (stream) {
+        e = hipStreamGetDevice(stream, &dev);
+        if (e != hipSuccess) return status_of(e);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return TIQ_EUNSUPPORTED;
+    void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (p) {
+        *out = p;
+        return TIQ_OK;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return status_of(e);
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t back = dev != cur ? hipSetDevice(cur) : hipSuccess;
+        if (e != hipSuccess) return status_of(e);
+        if (back != hipSuccess) return status_of(back);
+        if (!p) return TIQ_EINVAL;
+        g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return TIQ_OK;
+}
+
+}  // namespace
+
 extern "C" int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M, int64_t K,
                                  const void* w, int w_format, const float* scale, const float* bias, int64_t N,
                                  float* y, int64_t ldy, const float* ln_weight, const float* ln_bias, float ln_eps,
@@ -326,4 +380,24 @@ extern "C" int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_
     a.ws = workspace;
     a.ws_bytes = workspace_bytes;
     return run_decode_linear(a, x_planes, next_ln_weight, next_ln_bias, next_ln_eps, planes_out);
+}
+
+extern "C" int tiq_decode_linear_noalloc(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M,
+                                         int64_t K, const void* w, int w_format, const float* scale,
+                                         const float* bias, int64_t N, float* y, int64_t ldy,
+                                         const float* ln_weight, const float* ln_bias, float ln_eps, int activation,
+                                         const float* residual, int64_t ld_residual, const float* next_ln_weight,
+                                         const float* next_ln_bias, float next_ln_eps, uint16_t* planes_out,
+                                         void* stream) {
+    // the workspace tiq_decode_linear may use for this shape, against the fixed
+    // array (host arithmetic only: nothing is launched for a refused request)
+    if (tiq_decode_linear_workspace(w_format, M, K, N) > TIQ_NOALLOC_SCRATCH_BYTES) return TIQ_ESCRATCH;
+    void* ws = nullptr;
+    if (M > 0 && N > 0) {
+        const int rc = noalloc_scratch(as_stream(stream), &ws);
+        if (rc != TIQ_OK) return rc;
+    }
+    return tiq_decode_linear(x, ldx, x_planes, M, K, w, w_format, scale, bias, N, y, ldy, ln_weight, ln_bias, ln_eps,
+                             activation, residual, ld_residual, next_ln_weight, next_ln_bias, next_ln_eps, planes_out,
+                             ws, TIQ_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -51,6 +51,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_decode_planes_bytes": ([_i64, _i64], _sz),
     "tiq_decode_linear": ([_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _f32, _i32,
                            _vp, _i64, _vp, _vp, _f32, _vp, _vp, _sz, _vp], _i32),
+    "tiq_decode_linear_noalloc": ([_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _f32,
+                                   _i32, _vp, _i64, _vp, _vp, _f32, _vp, _vp], _i32),
     "tiq_linear_fused_workspace": ([_i32, _i32, _i64, _i64, _i64], _sz),
     "tiq_linear_fused_ws": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
                              _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp, _sz, _vp], _i32),

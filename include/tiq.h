@@ -35,6 +35,7 @@ enum tiq_status {
     TIQ_EALIGN = -3,        /* pointer or leading dimension misaligned          */
     TIQ_EUNSUPPORTED = -4,  /* valid request the library has no kernel for     */
     TIQ_EWORKSPACE = -5,    /* workspace too small                              */
+    TIQ_ESCRATCH = -6,      /* beyond the fixed scratch of tiq_decode_linear_noalloc */
     TIQ_EHIP_BASE = -1000   /* TIQ_EHIP_BASE - hipError_t                        */
 };
 
@@ -267,6 +268,28 @@ int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int
                       const float* residual, int64_t ld_residual, const float* next_ln_weight,
                       const float* next_ln_bias, float next_ln_eps, uint16_t* planes_out, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* Bytes of the fixed device scratch of tiq_decode_linear_noalloc (per GPU,
+ * held from the library's load until the process ends). */
+#define TIQ_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* tiq_decode_linear without a workspace argument: for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation). No counterpart in the reference. Same
+ * arguments, kernels and results as tiq_decode_linear; its workspace is a
+ * fixed TIQ_NOALLOC_SCRATCH_BYTES array on the device of `stream`, so it
+ * allocates nothing and returns TIQ_ESCRATCH (before any launch) when
+ * tiq_decode_linear_workspace(w_format, M, K, N) exceeds that size (GPT-2-XL
+ * shapes at M <= 64 need at most 4 MB). Every call on one GPU shares the
+ * array: calls that overlap on one GPU (concurrent streams, threads) race.
+ * The first call on a device looks up the array's device address
+ * (hipGetSymbolAddress); make that call outside stream capture. */
+int tiq_decode_linear_noalloc(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M, int64_t K,
+                              const void* w, int w_format, const float* scale, const float* bias, int64_t N,
+                              float* y, int64_t ldy, const float* ln_weight, const float* ln_bias, float ln_eps,
+                              int activation, const float* residual, int64_t ld_residual,
+                              const float* next_ln_weight, const float* next_ln_bias, float next_ln_eps,
+                              uint16_t* planes_out, void* stream);
 
 /* Self-attention of one new token per sequence (model.py:248-318 at T = 1,
  * KVCache.update model.py:153-172): qkv is the (batch, (n_head + 2 n_kv_head)
