@@ -183,16 +183,17 @@ def per_shape_graph_times(ls: LinearSet, reps: int, entry: str = "tiq_linear_w8"
     return out
 
 
-def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed):
+def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed, per_shape=True):
     ls = LinearSet(kn, layers, copies, M, dev, seed)
     ms = replay_ms(capture_graphs(ls), steps, warmup)
     gbs = ls.bytes_per_copy / (ms * 1e-3) / 1e9
-    per = per_shape_graph_times(ls, 5)
-    shapes = {f"{K}x{N}": {"us": per[(K, N)] * 1e3,
-                           "GB/s": gemv_bytes(M, K, N) / (per[(K, N)] * 1e-3) / 1e9} for K, N in kn}
     res = {"M": M, "ms_per_step": ms, "GB/s": gbs, "launches_per_step": ls.launches_per_copy,
-           "bytes_per_step": ls.bytes_per_copy, "avg_launch_us": ms * 1e3 / ls.launches_per_copy,
-           "per_shape_graph": shapes}
+           "bytes_per_step": ls.bytes_per_copy, "avg_launch_us": ms * 1e3 / ls.launches_per_copy}
+    if per_shape:
+        per = per_shape_graph_times(ls, 5)
+        res["per_shape_graph"] = {f"{K}x{N}": {"us": per[(K, N)] * 1e3,
+                                              "GB/s": gemv_bytes(M, K, N) / (per[(K, N)] * 1e-3) / 1e9}
+                                  for K, N in kn}
     del ls
     return res
 
@@ -718,7 +719,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "gemm_g128", "quantize", "decode", "decode_xl", "eval", "schemes", "copy"],
+    ap.add_argument("--only", choices=["headline", "gemv", "gemv_xl", "gemm", "gemm4096", "gemm_g128", "quantize", "decode", "decode_xl", "eval", "schemes", "copy"],
                     default=None,
                     help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
                          "used to calibrate the HBM byte counters")
@@ -743,8 +744,19 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 5}))
         return 0
+    if args.only == "headline":  # the timed headline replays alone (what its kernel profile covers)
+        h = gemv_section(1, SMALL_KN, 12, 6, args.steps, args.warmup, dev, seed=0, per_shape=False)
+        print(json.dumps(h))
+        return 0
+    if args.only == "gemv_xl":  # the GPT-2-XL-shape replays alone (what their kernel profile covers)
+        print(json.dumps(gemv_section(1, XL_KN, 12, 3, args.steps, args.warmup, dev, seed=7, per_shape=False)))
+        return 0
     if args.only == "gemm":
         print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev) for M in (256, 1024, 4096)}))
+        return 0
+    if args.only == "gemm4096":
+        print(json.dumps({"int8": gemm_section(4096, XL_KN, dev), "int4_g128": gemm_section(4096, XL_KN, dev,
+                                                                                          fmt="int4_g128")}))
         return 0
     if args.only == "gemm_g128":
         print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev, fmt="int4_g128") for M in (256, 1024, 4096)}))

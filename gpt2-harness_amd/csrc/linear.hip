@@ -121,7 +121,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 111; }
+extern "C" int tiq_version(void) { return 112; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {

@@ -299,9 +299,10 @@ constexpr int kXbUnits = 12;
 template <int WF, int XM, typename TY>
 __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     const float* __restrict__ x, int64_t ldx, int M, int K, const uint8_t* __restrict__ w, int64_t ldw,
-    const float* __restrict__ scale, const float* __restrict__ bias, int N, TY* __restrict__ y, int64_t ldy,
+    const float* __restrict__ scale, const float* __restrict__ bias, int N, TY* y, int64_t ldy,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps, int act,
-    const float* __restrict__ res, int64_t ldr, float* __restrict__ part, uint16_t* __restrict__ x3o) {
+    const float* res, int64_t ldr, float* __restrict__ part, uint16_t* __restrict__ x3o) {
+    // y may alias res (x = x + f(x) in place): neither is __restrict__
     constexpr int WB = (WF == kW8) ? 16 : 64;  // weight bytes a lane loads per unit
     constexpr bool PL = XM == kXPlanes;
     constexpr int kXp = ring_units<WF>();
