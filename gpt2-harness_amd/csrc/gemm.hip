@@ -306,7 +306,7 @@ int dispatch_tile(const LinearArgs& a, int tile) {
 template <int FMT>
 int dispatch_gemm(const LinearArgs& a, int tile) {
     if (FMT == kW8 && (tile == 0 || tile >= 10) && staged_gemm_supported(a))
-        return launch_staged_gemm(a, tile >= 10 ? tile - 10 : staged_gemm_choice(a.M, a.N, a.K));
+        return launch_staged_gemm(a, tile >= 10 ? tile - 10 : staged_gemm_choice(a));
     if (a.y_dtype == TIQ_F32) return dispatch_tile<FMT, float>(a, tile);
     return dispatch_tile<FMT, uint16_t>(a, tile);
 }
@@ -327,7 +327,7 @@ bool gemm_supported(const LinearArgs& a) {
 
 int launch_gemm_tile(const LinearArgs& a, int tile) {
     if (!gemm_supported(a)) return TIQ_EUNSUPPORTED;
-    if (tile < 0 || (tile > 4 && (tile < 10 || tile > 12))) return TIQ_EINVAL;
+    if (tile < 0 || (tile > 4 && (tile < 10 || tile > 15))) return TIQ_EINVAL;
     if (a.fmt == kW8) return dispatch_gemm<kW8>(a, tile);
     if (a.fmt == kW4G) return dispatch_gemm<kW4G>(a, tile);
     return dispatch_gemm<kW4>(a, tile);

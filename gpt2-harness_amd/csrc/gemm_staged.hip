@@ -19,8 +19,13 @@ constexpr int kXcds = 8;
 
 // ------------------------------------------------------------ staged GEMM
 // The int8 GEMM used for large M. One workgroup of 4 wavefronts (one per
-// SIMD) owns a BM x BN output tile; each wavefront a (BM/2) x (BN/2) block of
-// 32 x 32 x 16 bf16 MFMA tiles (accumulators in AGPRs).
+// SIMD) owns a BM x BN output tile; the wavefronts are laid out WMW x (4 /
+// WMW) over it, each owning a (BM / WMW) x (BN * WMW / 4) block of
+// 32 x 32 x 16 bf16 MFMA tiles (accumulators in AGPRs). WMW = 2 gives square
+// wave blocks (256 x 256, 256 x 128, 128 x 128 tiles); WMW = 1 puts the four
+// side by side along N, which admits tile heights that are odd multiples of
+// 32 (224 x 256, 160 x 256, 224 x 128): those make the tile count of the
+// GPT-2-XL shapes at M = 4096 just under a whole number of rounds of 256 CUs.
 //
 //   * Staging through registers: every k64 step each thread loads 16-byte
 //     chunks of x (bf16) and of the int8 weight rows into one of two register
@@ -69,23 +74,25 @@ __device__ __forceinline__ uint32_t bf16x2_of_bytes_perm(uint32_t d, int sh) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-template <int BM, int BN, typename TY>
+template <int BM, int BN, int WMW, typename TY>
 __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
     int K, int kw) {
     constexpr int NT = 256;
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int WNW = 4 / WMW;
+    constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int TMm = WM / 32, TNn = WN / 32;
     constexpr int XS = BM * 128, WS = BN * 128, STAGE = XS + WS;
     constexpr int XL = BM * 8 / NT, WL = BN * 4 / NT, NL = XL + WL;  // staging loads per thread per step
     constexpr int NMF = TMm * TNn, NRD = TMm + TNn;                  // per k16
+    static_assert((WMW == 1 || WMW == 2) && WM % 32 == 0 && WN % 32 == 0, "wave layout");
     static_assert(XL * NT == BM * 8 && WL * NT == BN * 4, "staging split");
-    static_assert(NL <= 3 * NMF && NRD <= NMF, "one staging op per bundle");
+    static_assert(NL <= 3 * NMF && NRD <= 2 * NMF, "staging ops and fragment reads per bundle");
     constexpr int UNIT = 16 / (int)sizeof(TY);  // output elements per 16-byte chunk
     constexpr int UNITS = BN / UNIT;            // chunks per output row
     constexpr int PASSES = (BM * BN * (int)sizeof(TY) + 2 * STAGE - 1) / (2 * STAGE);
-    static_assert(PASSES == 1 || PASSES == 2, "output tile passes");
+    static_assert(PASSES == 1 || (PASSES == 2 && WMW == 2), "output tile passes");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
     __shared__ __attribute__((aligned(16))) float sb_s[2][BN];  // the tile's scale and bias
 
@@ -95,7 +102,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     const int m_blk = tm * BM, n_blk = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    const int wm = (wave / WNW) * WM, wn = (wave % WNW) * WN;
 
     // staging: x rows xrow + 32 q (8 threads per row), weight rows wrow + 64 j
     // (4 threads per row); rows are clamped for a partial tile
@@ -194,7 +201,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
 #pragma unroll
             for (int t = 0; t < NMF; ++t) {
                 mfma_set(set, t);
-                if (t < NRD) fread(cur, kk + 1, set ^ 1, t);
+                if constexpr (NRD <= NMF) {
+                    if (t < NRD) fread(cur, kk + 1, set ^ 1, t);
+                } else {  // more fragments than MFMAs: spread over the bundles
+#pragma unroll
+                    for (int q = t * NRD / NMF; q < (t + 1) * NRD / NMF; ++q) fread(cur, kk + 1, set ^ 1, q);
+                }
                 const int b = kk * NMF + t;
                 if ((b + 1) * NL / (3 * NMF) > b * NL / (3 * NMF)) lstore(nxt, p ^ 1, b * NL / (3 * NMF));
                 if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
@@ -206,7 +218,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
 #pragma unroll
         for (int t = 0; t < NMF; ++t) {
             mfma_set(1, t);
-            if (t < NRD) fread(nxt, 0, 0, t);
+            if constexpr (NRD <= NMF) {
+                if (t < NRD) fread(nxt, 0, 0, t);
+            } else {
+#pragma unroll
+                for (int q = t * NRD / NMF; q < (t + 1) * NRD / NMF; ++q) fread(nxt, 0, 0, q);
+            }
             const int b = 3 * NMF + t;
             if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
             asm volatile("" ::: "memory");
@@ -276,10 +293,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     }
 }
 
-template <int BM, int BN, typename TY>
+template <int BM, int BN, int WMW, typename TY>
 int run_staged(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_w8_staged<BM, BN, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
+    hipLaunchKernelGGL((gemm_w8_staged<BM, BN, WMW, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
                        static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
                        a.scale, a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K,
                        (int)(a.kw ? a.kw : a.K));
@@ -299,20 +316,23 @@ bool staged_supported_impl(const LinearArgs& a) {
     return true;
 }
 
-// Tile choice: rounds of co-resident workgroups (256x256 and 256x128 tiles
-// need most of a CU's LDS and registers: one per CU; 128x128 tiles fit two,
-// whose rounds overlap: counted in halves) times the duration of one round,
-// modelled as step_us per k64 step plus a fixed term (prologue and epilogue),
-// both fitted to MI355X measurements of this kernel at the GPT-2-XL Linear
-// shapes with M = 4096 (per-workgroup timestamps: prologue 2-3 us, epilogue
-// 1.5-5 us by tile size).
-int staged_choice(int64_t M, int64_t N, int64_t K) {
+// Tile choice: rounds of co-resident workgroups (the WMW = 2 256-row tiles and
+// every WMW = 1 tile need most of a CU's LDS and registers: one per CU;
+// 128x128 tiles fit two, whose rounds overlap: counted in halves) times the
+// duration of one round, modelled as step_us per k64 step plus a fixed term
+// (prologue, epilogue, launch), both least-squares fits to MI355X timings of
+// every tile at the GPT-2-XL Linear shapes with M = 256 / 1024 / 4096 (bf16
+// output, operands rotated over six copies; within 12% of every timing but
+// one, and choosing the fastest tile or one within 1% of it at all twelve).
+int staged_choice(int64_t M, int64_t N, int64_t K, bool bf16_out) {
     struct Opt { int bm, bn, per_cu; double step_us, fixed_us; };
-    static const Opt opts[] = {{256, 256, 1, 1.43, 8.7}, {256, 128, 1, 0.893, 5.9}, {128, 128, 2, 1.073, 3.7}};
+    // 3-5: the WMW = 1 tiles (bf16 output only)
+    static const Opt opts[] = {{256, 256, 1, 1.180, 14.14}, {256, 128, 1, 0.704, 7.60}, {128, 128, 2, 1.033, 2.49},
+                               {224, 256, 1, 1.072, 12.94}, {160, 256, 1, 0.880, 9.58}, {224, 128, 1, 0.739, 5.83}};
     const double nk = (double)(K / BK);
     int best = 0;
     double best_t = 1e30;
-    for (int o = 0; o < 3; ++o) {
+    for (int o = 0; o < (bf16_out ? 6 : 3); ++o) {
         const int64_t tiles = ((M + opts[o].bm - 1) / opts[o].bm) * ((N + opts[o].bn - 1) / opts[o].bn);
         const int64_t slots = 256 * opts[o].per_cu;
         const double rounds = opts[o].per_cu == 1 ? (double)((tiles + slots - 1) / slots)
@@ -385,24 +405,34 @@ size_t staged_split_workspace(int64_t M, int64_t N, int64_t K) {
     return S > 1 ? (size_t)((S * M * N * 4 + 255) / 256 * 256) : 0;
 }
 
-template <typename TY>
-int dispatch_staged_t(const LinearArgs& a, int choice) {
+int dispatch_staged_f32(const LinearArgs& a, int choice) {
     switch (choice) {
-        case 0: return run_staged<256, 256, TY>(a);
-        case 1: return run_staged<256, 128, TY>(a);
-        default: return run_staged<128, 128, TY>(a);
+        case 0: return run_staged<256, 256, 2, float>(a);
+        case 1: return run_staged<256, 128, 2, float>(a);
+        default: return run_staged<128, 128, 2, float>(a);
+    }
+}
+
+int dispatch_staged_bf16(const LinearArgs& a, int choice) {
+    switch (choice) {
+        case 0: return run_staged<256, 256, 2, uint16_t>(a);
+        case 1: return run_staged<256, 128, 2, uint16_t>(a);
+        case 3: return run_staged<224, 256, 1, uint16_t>(a);
+        case 4: return run_staged<160, 256, 1, uint16_t>(a);
+        case 5: return run_staged<224, 128, 1, uint16_t>(a);
+        default: return run_staged<128, 128, 2, uint16_t>(a);
     }
 }
 
 
 bool staged_gemm_supported(const LinearArgs& a) { return staged_supported_impl(a); }
 
-int staged_gemm_choice(int64_t M, int64_t N, int64_t K) { return staged_choice(M, N, K); }
+int staged_gemm_choice(const LinearArgs& a) { return staged_choice(a.M, a.N, a.K, a.y_dtype == TIQ_BF16); }
 
 int launch_staged_gemm(const LinearArgs& a, int choice) {
     if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
-    if (a.y_dtype == TIQ_F32) return dispatch_staged_t<float>(a, choice);
-    return dispatch_staged_t<uint16_t>(a, choice);
+    if (a.y_dtype == TIQ_F32) return dispatch_staged_f32(a, choice);
+    return dispatch_staged_bf16(a, choice);
 }
 
 int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
@@ -413,7 +443,7 @@ int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     float* part = static_cast<float*>(ws);
     const int64_t tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
     // the products: raw fp32 slices [S][M][N] (unit scale, no bias in the kernel)
-    hipLaunchKernelGGL((gemm_w8_staged<128, 128, float>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
+    hipLaunchKernelGGL((gemm_w8_staged<128, 128, 2, float>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
                        a.stream, static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
                        a.scale, a.bias, part, (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
     int rc = launch_status();

@@ -105,7 +105,7 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     const size_t planes = split_workspace(a.M, a.K);
     rc = launch_staged_gemm_split(g, static_cast<uint8_t*>(ws) + planes, ws_bytes - planes);
     if (rc != TIQ_EUNSUPPORTED) return rc;
-    return launch_staged_gemm(g, staged_gemm_choice(g.M, g.N, g.K));
+    return launch_staged_gemm(g, staged_gemm_choice(g));
 }
 
 int run_linear(const LinearArgs& a) {

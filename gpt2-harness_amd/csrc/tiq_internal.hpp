@@ -57,7 +57,8 @@ int check_linear(const LinearArgs& a);
 int launch_gemv(const LinearArgs& a);
 int launch_gemm(const LinearArgs& a);
 // The GEMM with a given tile configuration: 0 automatic, 1-4 the LDS-dequant
-// kernel's tiles (gemm.hip), 10-12 the staged int8 kernel's (256x256, 256x128, 128x128).
+// kernel's tiles (gemm.hip), 10-15 the staged int8 kernel's (256x256, 256x128,
+// 128x128; with bf16 output 224x256, 160x256, 224x128).
 int launch_gemm_tile(const LinearArgs& a, int tile);
 // True when the MFMA GEMM has a kernel for these arguments.
 bool gemm_supported(const LinearArgs& a);
@@ -81,10 +82,10 @@ size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N);
 size_t decode_planes_bytes(int64_t M, int64_t K);
 
 // The register-staged int8 GEMM (gemm_staged.hip): whether it takes these
-// arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128) and
-// its launch.
+// arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128; bf16
+// output also 3: 224 x 256, 4: 160 x 256, 5: 224 x 128) and its launch.
 bool staged_gemm_supported(const LinearArgs& a);
-int staged_gemm_choice(int64_t M, int64_t N, int64_t K);
+int staged_gemm_choice(const LinearArgs& a);
 int launch_staged_gemm(const LinearArgs& a, int choice);
 // Split-K for products with few output tiles: S (1 = none), the workspace
 // bytes of its fp32 partial slices, and the launch (TIQ_EUNSUPPORTED when no

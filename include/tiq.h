@@ -169,9 +169,10 @@ int tiq_gemm_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
 
 /* tiq_gemm_w8 with an explicit tile configuration, for tests and
  * measurement: 0 = the automatic choice, 1-4 = the LDS-dequant kernel at
- * 128x128 / 256x128 / 128x256 / 256x128 (8 wavefronts) tiles, 10-12 = the
- * register-staged kernel at 256x256 / 256x128 / 128x128 tiles (falls back to
- * the automatic tile when that kernel does not take the shape). No
+ * 128x128 / 256x128 / 128x256 / 256x128 (8 wavefronts) tiles, 10-15 = the
+ * register-staged kernel at 256x256 / 256x128 / 128x128 tiles and, with bf16
+ * output, 224x256 / 160x256 / 224x128 (128x128 with fp32 output; falls back
+ * to the automatic tile when that kernel does not take the shape). No
  * counterpart in the reference (same interface as tiq_gemm_w8); the product
  * path never calls it. */
 int tiq_gemm_w8_tile(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,

@@ -95,11 +95,14 @@ def test_gemm_w8_small_shapes(dev, c_oracle, KN, M):
 
 
 # Every GEMM tile configuration through tiq_gemm_w8_tile (10/11/12 the
-# register-staged int8 kernel at 256x256 / 256x128 / 128x128 tiles, 1-4 the
+# register-staged int8 kernel at 256x256 / 256x128 / 128x128 tiles, 13/14/15
+# the same kernel with its wavefronts side by side along N at 224x256 /
+# 160x256 / 224x128 (bf16 output; 128x128 for fp32 output), 1-4 the
 # LDS-dequant kernel that also serves int4), on full, partial-row and
 # partial-column tiles.
-@pytest.mark.parametrize("tile", [10, 11, 12, 1, 2, 3, 4])
-@pytest.mark.parametrize("K,N,M", [(1600, 1600, 512), (1600, 4800, 300), (6400, 1600, 257), (768, 2304, 1024)])
+@pytest.mark.parametrize("tile", [10, 11, 12, 13, 14, 15, 1, 2, 3, 4])
+@pytest.mark.parametrize("K,N,M", [(1600, 1600, 512), (1600, 4800, 300), (6400, 1600, 257), (768, 2304, 1024),
+                                   (1600, 6400, 4096)])
 def test_gemm_w8_tiles(dev, c_oracle, tile, K, N, M):
     _run_w8("tiq_gemm_w8_tile", dev, c_oracle, K, N, M, torch.bfloat16, tile + M, M % 2 == 0, tile)
 
@@ -111,7 +114,7 @@ def test_gemm_w8_tile_rejects_unknown_configuration(dev):
     s = torch.ones(64, device=dev)
     y = torch.empty(256, 64, device=dev)
     st = torch.cuda.current_stream().cuda_stream
-    for bad in (-1, 5, 9, 13):
+    for bad in (-1, 5, 9, 16):
         assert L.tiq_gemm_w8_tile(x.data_ptr(), 1, 256, 64, 64, q.data_ptr(), s.data_ptr(), None, 64, y.data_ptr(),
                                   0, 64, bad, st) == -1
 
