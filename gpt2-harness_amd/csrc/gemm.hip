@@ -89,11 +89,15 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chu
 //     y[m, n] = sum_g s[n, g] * (sum_{k in g} x[m, k] * q[n, k]) + bias[n]
 // with no rounding beyond fp32 accumulation. The last group may be short
 // (K = 1600 with group 128: twelve groups of two steps and one of one).
+// kw: the period of K in the weight matrix (the GEMM reads weight column
+// k % kw): K = 3 kw for fp32 activations split into three bf16 planes laid side
+// by side (x = hi + lo + lo2, each product exact), kw = K otherwise. Groups
+// restart with every plane.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int OCC, int FMT, typename TY>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const uint16_t* __restrict__ scale16, int group,
-    const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N, int K, int kw) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // wave tile
     constexpr int TM = WM / 32, TN = WN / 32;            // 32 x 32 MFMA tiles per wave
@@ -149,8 +153,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     // group-wise scales: this lane's output columns (one per 32-wide tile
     // column j, clamped for a partial tile), the group's partial sums, and the
     // group's scales, requested at the group's first step
-    const int steps_per_group = GROUPED ? group / BK : 1;
-    const int ngroups = GROUPED ? (K + group - 1) / group : 1;
+    const int ngroups = GROUPED ? (kw + group - 1) / group : 1;
     int64_t srow[TN];
     floatx16 part[GROUPED ? TM : 1][GROUPED ? TN : 1];
     uint16_t gsc[TN];
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
 
 #define TIQ_LOAD_TILES(k0)                                                                         \
     {                                                                                              \
-        const int kb_ = (FMT == kW8) ? (k0) : (k0) / 2;                                            \
+        const int kb_ = (FMT == kW8) ? (k0) % kw : ((k0) % kw) / 2;                                \
         _Pragma("unroll") for (int j = 0; j < A_VEC; ++j) ra[j] =                                  \
             *reinterpret_cast<const uint4*>(x + a_off[j] + (k0));                                  \
         _Pragma("unroll") for (int j = 0; j < B_VEC; ++j) rb[j] =                                  \
@@ -204,9 +207,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
         const int buf = s & 1;
         const int kn = (s + 1 < nk) ? (s + 1) * BK : s * BK;
         TIQ_LOAD_TILES(kn)
+        const int sk = (s * BK) % kw;  // the step's first weight column
         if constexpr (GROUPED) {
-            if (s % steps_per_group == 0) {  // a new group: its scales, and partial sums from zero
-                const int g = s / steps_per_group;
+            if (sk % group == 0) {  // a new group: its scales, and partial sums from zero
+                const int g = sk / group;
 #pragma unroll
                 for (int j = 0; j < TN; ++j) gsc[j] = scale16[srow[j] + g];
 #pragma unroll
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
                 }
         }
         if constexpr (GROUPED) {
-            if ((s + 1) % steps_per_group == 0 || s + 1 == nk) {  // the group's last step
+            if ((sk + BK) % group == 0 || sk + BK == kw || s + 1 == nk) {  // the group's last step
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     const float sg = f16_bits_to_f32(gsc[j]);
@@ -282,7 +286,7 @@ int run_gemm32(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     hipLaunchKernelGGL((gemm32_kernel<BM, BN, WMW, WNW, OCC, FMT, TY>), dim3((unsigned)tiles), dim3(WMW * WNW * 64),
                        0, a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.scale16, a.group,
-                       a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K);
+                       a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
     return launch_status();
 }
 
@@ -319,6 +323,7 @@ bool gemm_supported(const LinearArgs& a) {
     // group-wise int4: whole k steps per group (the GPT-2 group of 128 is two)
     if (a.fmt == kW4G && (a.group % BK != 0 || !aligned(a.scale16, 2))) return false;
     if (a.K % BK != 0) return false;
+    if (a.kw && (a.kw % BK != 0 || a.K % a.kw != 0)) return false;
     if (!aligned(a.x, 16) || a.ldx % 8 != 0) return false;
     if (!aligned(a.w, 16) || a.ldw % 16 != 0) return false;
     if (a.M > 0x7fffffff || a.N > 0x7fffffff || a.K > 0x7fffffff) return false;

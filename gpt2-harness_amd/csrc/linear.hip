@@ -83,10 +83,11 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ x, int64_t ldx, in
 
 size_t split_workspace(int64_t M, int64_t K) { return (size_t)(M * 3 * K * 2 + 255) / 256 * 256; }
 
-// fp32 activations through the matrix cores when the staged GEMM takes the
-// three-plane problem; TIQ_EUNSUPPORTED otherwise (the caller falls back).
+// fp32 activations through the matrix cores when a GEMM takes the three-plane
+// problem (the staged kernel for int8 weights, the LDS-dequant one for int4
+// and group-wise int4); TIQ_EUNSUPPORTED otherwise (the caller falls back).
 int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
-    if (a.x_dtype != TIQ_F32 || a.fmt != kW8 || a.M < kGemmMinRows || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
+    if (a.x_dtype != TIQ_F32 || a.fmt == kF32 || a.M < kGemmMinRows || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
     if (!aligned(a.x, 16) || a.ldx % 4 != 0 || a.M * 3 * a.K > 0x7fffffffLL) return TIQ_EUNSUPPORTED;
     LinearArgs g = a;
     g.x = ws;
@@ -94,13 +95,15 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     g.K = 3 * a.K;
     g.ldx = 3 * a.K;
     g.kw = a.K;
-    if (!staged_gemm_supported(g)) return TIQ_EUNSUPPORTED;
+    const bool staged = a.fmt == kW8 && staged_gemm_supported(g);
+    if (!staged && !gemm_supported(g)) return TIQ_EUNSUPPORTED;
     if (!ws || ws_bytes < split_workspace(a.M, a.K) || !aligned(ws, 16)) return TIQ_EWORKSPACE;
     const int64_t n = a.M * (a.K / 4);
     hipLaunchKernelGGL(split_bf16x3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, a.stream,
                        static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, static_cast<uint16_t*>(ws));
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
+    if (!staged) return launch_gemm(g);
     // a workspace sized by tiq_gemm_w8_workspace also holds split-K partials
     const size_t planes = split_workspace(a.M, a.K);
     rc = launch_staged_gemm_split(g, static_cast<uint8_t*>(ws) + planes, ws_bytes - planes);
@@ -281,6 +284,33 @@ extern "C" int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_
     return linear_fused(x, x_dtype, M, K, ldx, w, w_format, scale, scale_f16, group, bias, N, y, y_dtype, ldy,
                         ln_weight, ln_bias, ln_eps, activation, residual, ld_residual, workspace, workspace_bytes,
                         stream);
+}
+
+extern "C" int tiq_linear_w4_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                const uint8_t* packed, const float* scale, const float* bias, int64_t N, void* y,
+                                int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, packed, K / 2, scale, nullptr, 0, bias, N, y, y_dtype, ldy,
+                             stream, kW4);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    if (workspace && !aligned(workspace, 16)) return TIQ_EALIGN;
+    rc = run_linear_split(a, workspace, workspace_bytes);
+    if (rc != TIQ_EUNSUPPORTED) return rc;
+    return run_linear(a);
+}
+
+extern "C" int tiq_linear_w4g_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                 const uint8_t* packed, const uint16_t* scale_f16, int group, const float* bias,
+                                 int64_t N, void* y, int y_dtype, int64_t ldy, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    LinearArgs a = make_args(x, x_dtype, M, K, ldx, packed, (K + 1) / 2, nullptr, scale_f16, group, bias, N, y,
+                             y_dtype, ldy, stream, kW4G);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    if (workspace && !aligned(workspace, 16)) return TIQ_EALIGN;
+    rc = run_linear_split(a, workspace, workspace_bytes);
+    if (rc != TIQ_EUNSUPPORTED) return rc;
+    return run_linear(a);
 }
 
 extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,

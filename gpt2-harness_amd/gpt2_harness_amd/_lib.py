@@ -43,6 +43,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_gemm_w8_tile": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _i32, _vp], _i32),
     "tiq_linear_w4": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
     "tiq_linear_w4g": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64, _vp], _i32),
+    "tiq_linear_w4_ws": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i64, _vp, _sz, _vp], _i32),
+    "tiq_linear_w4g_ws": ([_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64, _vp, _sz, _vp],
+                          _i32),
     "tiq_linear_fused": ([_vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i32, _i64,
                           _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp], _i32),
     "tiq_gemm_w8_workspace": ([_i32, _i64, _i64, _i64], _sz),

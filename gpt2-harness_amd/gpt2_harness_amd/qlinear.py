@@ -114,12 +114,18 @@ def linear_into(m: QuantLinear, x2: torch.Tensor, y: torch.Tensor) -> None:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
         rc = L.tiq_linear_w8_ws(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b, N,
                                 y.data_ptr(), yd, y.stride(0), None if ws is None else ws.data_ptr(), ws_bytes, st)
-    elif m.fmt == FMT_W4:
-        rc = L.tiq_linear_w4(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b, N,
-                             y.data_ptr(), yd, y.stride(0), st)
     else:
-        rc = L.tiq_linear_w4g(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(),
-                              m.group_size, b, N, y.data_ptr(), yd, y.stride(0), st)
+        # int4 formats: fp32 activations over many rows take the matrix cores
+        # through the same three exact bf16 planes (workspace 0: none)
+        ws_bytes = int(L.tiq_linear_w8_workspace(xd, M, K))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
+        wp = None if ws is None else ws.data_ptr()
+        if m.fmt == FMT_W4:
+            rc = L.tiq_linear_w4_ws(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(), b,
+                                    N, y.data_ptr(), yd, y.stride(0), wp, ws_bytes, st)
+        else:
+            rc = L.tiq_linear_w4g_ws(x2.data_ptr(), xd, M, K, x2.stride(0), m.codes.data_ptr(), m.scale.data_ptr(),
+                                     m.group_size, b, N, y.data_ptr(), yd, y.stride(0), wp, ws_bytes, st)
     _lib.check(rc, f"quantized linear ({m.fmt}, M={M}, K={K}, N={N})")
 
 

@@ -192,6 +192,24 @@ int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx
                    const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
                    void* stream);
 
+/* tiq_linear_w4 / tiq_linear_w4g with a caller workspace of
+ * tiq_linear_w8_workspace(x_dtype, M, K) bytes: with fp32 x and M >= 128 the
+ * activations are split exactly into three bf16 planes there and the product
+ * runs on the matrix cores (every product exact, fp32 accumulation; the
+ * group-wise format scales each group's partial sum), as tiq_linear_w8_ws
+ * does for int8 -- the prefill of a model quantized to int4 (model.py:254,
+ * 319,352,355 at M = B*T). Without a workspace, or where the GEMM does not
+ * take the shape (K % 64, group % 64), they compute what tiq_linear_w4 /
+ * tiq_linear_w4g compute. */
+int tiq_linear_w4_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                     const uint8_t* packed, const float* scale, const float* bias, int64_t N,
+                     void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
+                     void* stream);
+int tiq_linear_w4g_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                      const uint8_t* packed, const uint16_t* scale_f16, int group,
+                      const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------- decode step
  * Kernels of one GPT-2 decode step (one token per sequence) over a
  * preallocated KV cache whose fill level `pos` is a device int64 scalar, so

@@ -355,6 +355,49 @@ def test_gemm_w4_groupwise_widths_and_partial_tiles(dev, c_oracle, K, N, M, grou
     _run_w4g(dev, c_oracle, K, N, M, group, seed=M + group)
 
 
+# fp32 activations with int4 weights (reference nibbles, group-wise g128) at
+# prefill sizes: three exact bf16 planes through the LDS-dequant MFMA GEMM
+# (the weight read at column k % K), the contract bound and fp32-level
+# accuracy against float64 as for int8.
+@pytest.mark.parametrize("fmt", ["int4", "int4_g128"])
+@pytest.mark.parametrize("K,N,M", [(1600, 4800, 256), (6400, 1600, 300), (1600, 1600, 4096), (768, 3072, 128)])
+def test_linear_w4_fp32_matrix_cores(dev, c_oracle, fmt, K, N, M):
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, seed=M + K + 7)
+    if fmt == "int4":
+        q, s = c_oracle.quantize_per_channel(w.numpy(), 4)
+        w_hat = OL.dequantize(q, s)
+        codes, sc = torch.from_numpy(c_oracle.pack_int4(q)).to(dev), torch.from_numpy(s.reshape(-1)).to(dev)
+    else:
+        packed, s16 = c_oracle.quantize_groupwise_int4(w.numpy(), 128)
+        w_hat = torch.from_numpy(OQ.dequantize_groupwise_int4(packed, s16, K, 128))
+        codes, sc = torch.from_numpy(packed).to(dev), torch.from_numpy(s16.view(np.uint16).copy()).to(dev)
+    xd, bd = x.to(dev), b.to(dev)
+    ws_bytes = int(L.tiq_linear_w8_workspace(_lib.F32, M, K))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    y = torch.empty(M, N, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def call(nbytes):
+        if fmt == "int4":
+            return L.tiq_linear_w4_ws(xd.data_ptr(), _lib.F32, M, K, K, codes.data_ptr(), sc.data_ptr(),
+                                      bd.data_ptr(), N, y.data_ptr(), _lib.F32, N, ws.data_ptr(), nbytes, st)
+        return L.tiq_linear_w4g_ws(xd.data_ptr(), _lib.F32, M, K, K, codes.data_ptr(), sc.data_ptr(), 128,
+                                   bd.data_ptr(), N, y.data_ptr(), _lib.F32, N, ws.data_ptr(), nbytes, st)
+
+    assert call(ws_bytes - 256) == -5  # too small a workspace is refused before any work
+    _lib.check(call(ws_bytes), f"tiq_linear_{fmt}_ws")
+    torch.cuda.synchronize()
+    y_ref = OL.linear_ref(x, w_hat, b)
+    ok, err, bound = OL.within_tolerance(y, y_ref, TOL)
+    assert ok, f"max err {err:.3g} > {bound:.3g}"
+    y64 = x.double() @ w_hat.double().T + b.double()
+    err_gpu = float((y.cpu().double() - y64).abs().max())
+    err_cpu = float((y_ref.double() - y64).abs().max())
+    floor = 2.0 ** -24 * float(y64.abs().max())
+    assert err_gpu <= 8 * max(err_cpu, floor), f"error {err_gpu:.3g} vs fp32 oracle {err_cpu:.3g}"
+
+
 def test_zero_rows_is_a_no_op(dev):
     L = _lib.lib()
     y = torch.full((1, 4), 3.0, device=dev)
