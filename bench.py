@@ -222,8 +222,9 @@ def hbm_stream_section(dev, reps=10):
 
 
 def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
-    """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws; with fmt="int4_g128" the
-    group-wise int4 GEMM, tiq_linear_w4g, group 128) per shape: `reps` launches back
+    """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws; fmt="int4": the reference
+    nibble layout, tiq_linear_w4; fmt="int4_g128": the group-wise int4 GEMM,
+    tiq_linear_w4g, group 128) per shape: `reps` launches back
     to back between one HIP event pair, rotating over `copies` independent
     (activation, weight, output) sets (at M = 4096 on 1600 x 6400 the eight
     sets hold 600 MB, past the 256 MB Infinity Cache), so no launch finds its
@@ -262,6 +263,9 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
             if fmt == "int8":
                 q, s = g.quantize_tensor(w, 8)
                 s = s.reshape(-1).contiguous()
+            elif fmt == "int4":
+                q4, s = g.quantize_tensor(w, 4)
+                q, s = g.pack_int4(q4), s.reshape(-1).contiguous()
             else:
                 q, s = g.quantize_groupwise_int4(w, 128)
             x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
@@ -273,6 +277,9 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
             if fmt == "int8":
                 rc = L.tiq_gemm_w8_ws(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1,
                                       N, ws.data_ptr(), n_ws, st)
+            elif fmt == "int4":
+                rc = L.tiq_linear_w4(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1,
+                                     N, st)
             else:
                 rc = L.tiq_linear_w4g(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), 128, None, N, y.data_ptr(),
                                       1, N, st)
@@ -755,8 +762,9 @@ def main() -> int:
         print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev) for M in (256, 1024, 4096)}))
         return 0
     if args.only == "gemm4096":
-        print(json.dumps({"int8": gemm_section(4096, XL_KN, dev), "int4_g128": gemm_section(4096, XL_KN, dev,
-                                                                                          fmt="int4_g128")}))
+        print(json.dumps({"int8": gemm_section(4096, XL_KN, dev),
+                          "int4": gemm_section(4096, XL_KN, dev, fmt="int4"),
+                          "int4_g128": gemm_section(4096, XL_KN, dev, fmt="int4_g128")}))
         return 0
     if args.only == "gemm_g128":
         print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev, fmt="int4_g128") for M in (256, 1024, 4096)}))
@@ -793,6 +801,7 @@ def main() -> int:
             detail[f"gemm_xl_M{M}"] = gemm_section(M, XL_KN, dev)
         for M in (256, 1024, 4096):
             detail[f"gemm_xl_g128_M{M}"] = gemm_section(M, XL_KN, dev, fmt="int4_g128")
+        detail["gemm_xl_int4_M4096"] = gemm_section(4096, XL_KN, dev, fmt="int4")
         print("# gemm done", file=sys.stderr, flush=True)
         detail["quantize_xl"] = quantize_section(dev)
         detail["decode_gpt2_small_int8"] = decode_section(dev)

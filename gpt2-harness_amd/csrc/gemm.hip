@@ -309,7 +309,7 @@ int dispatch_tile(const LinearArgs& a, int tile) {
 
 template <int FMT>
 int dispatch_gemm(const LinearArgs& a, int tile) {
-    if (FMT == kW8 && (tile == 0 || tile >= 10) && staged_gemm_supported(a))
+    if ((tile == 0 || tile >= 10) && staged_gemm_supported(a))
         return launch_staged_gemm(a, tile >= 10 ? tile - 10 : staged_gemm_choice(a));
     if (a.y_dtype == TIQ_F32) return dispatch_tile<FMT, float>(a, tile);
     return dispatch_tile<FMT, uint16_t>(a, tile);

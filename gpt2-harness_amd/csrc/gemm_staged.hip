@@ -74,11 +74,26 @@ __device__ __forceinline__ uint32_t bf16x2_of_bytes_perm(uint32_t d, int sh) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-template <int BM, int BN, int WMW, typename TY>
-__global__ __launch_bounds__(256, 1) void gemm_w8_staged(
-    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+// the two biased nibbles of byte sh / 8 of d (low = even column) -> two bf16
+// in one dword (exact)
+__device__ __forceinline__ uint32_t bf16x2_of_nibbles_perm(uint32_t d, int sh) {
+    const float lo = (float)((int32_t)((d >> sh) & 0xfu) - 8);
+    const float hi = (float)((int32_t)((d >> (sh + 4)) & 0xfu) - 8);
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// FMT: kW8 (int8 codes) or kW4 (the reference's nibbles), per-row scale.
+// Nibble rows are staged 8 bytes a thread per k64 step into the same bf16
+// LDS layout as int8 rows. (Group-wise int4 runs on gemm32_kernel: folding a
+// group's partial tiles into the sums every two k steps drains the MFMA
+// pipeline of a 4-wavefront workgroup, and the partial tiles beside the sums
+// halve the workgroups a CU holds -- measured slower than that kernel.)
+template <int BM, int BN, int WMW, int FMT, typename TY>
+__global__ __launch_bounds__(256, 1) void gemm_staged(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
     int K, int kw) {
+    static_assert(FMT == kW8 || FMT == kW4, "int8 or reference-layout int4 weights");
     constexpr int NT = 256;
     constexpr int WNW = 4 / WMW;
     constexpr int WM = BM / WMW, WN = BN / WNW;
@@ -119,8 +134,14 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
             sx[p][q] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(x) + 2 * k0 + off);
         } else {
             const int j = q - XL;
-            const uint32_t off = (uint32_t)min(n_blk + wrow + 64 * j, N - 1) * ldw1 + wch * 16;
-            sw[p][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + (k0 % kw) + off);
+            if constexpr (FMT == kW8) {
+                const uint32_t off = (uint32_t)min(n_blk + wrow + 64 * j, N - 1) * ldw1 + wch * 16;
+                sw[p][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + (k0 % kw) + off);
+            } else {  // 16 nibbles: 8 bytes
+                const uint32_t off = (uint32_t)min(n_blk + wrow + 64 * j, N - 1) * ldw1 + wch * 8;
+                const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(w) + (k0 % kw) / 2 + off);
+                sw[p][j] = u32x4{v.x, v.y, 0u, 0u};
+            }
         }
     };
     auto lstore = [&](uint8_t* base, int p, int q) {
@@ -129,10 +150,18 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
         } else {
             const int j = q - XL;
             const u32x4 v = sw[p][j];
-            const u32x4 lo = {bf16x2_of_bytes_perm(v.x, 0), bf16x2_of_bytes_perm(v.x, 16),
-                              bf16x2_of_bytes_perm(v.y, 0), bf16x2_of_bytes_perm(v.y, 16)};
-            const u32x4 hi = {bf16x2_of_bytes_perm(v.z, 0), bf16x2_of_bytes_perm(v.z, 16),
-                              bf16x2_of_bytes_perm(v.w, 0), bf16x2_of_bytes_perm(v.w, 16)};
+            u32x4 lo, hi;
+            if constexpr (FMT == kW8) {
+                lo = u32x4{bf16x2_of_bytes_perm(v.x, 0), bf16x2_of_bytes_perm(v.x, 16),
+                           bf16x2_of_bytes_perm(v.y, 0), bf16x2_of_bytes_perm(v.y, 16)};
+                hi = u32x4{bf16x2_of_bytes_perm(v.z, 0), bf16x2_of_bytes_perm(v.z, 16),
+                           bf16x2_of_bytes_perm(v.w, 0), bf16x2_of_bytes_perm(v.w, 16)};
+            } else {
+                lo = u32x4{bf16x2_of_nibbles_perm(v.x, 0), bf16x2_of_nibbles_perm(v.x, 8),
+                           bf16x2_of_nibbles_perm(v.x, 16), bf16x2_of_nibbles_perm(v.x, 24)};
+                hi = u32x4{bf16x2_of_nibbles_perm(v.y, 0), bf16x2_of_nibbles_perm(v.y, 8),
+                           bf16x2_of_nibbles_perm(v.y, 16), bf16x2_of_nibbles_perm(v.y, 24)};
+            }
             *reinterpret_cast<u32x4*>(base + ws00 + j * 64 * 128) = lo;
             *reinterpret_cast<u32x4*>(base + ws01 + j * 64 * 128) = hi;
         }
@@ -293,26 +322,25 @@ __global__ __launch_bounds__(256, 1) void gemm_w8_staged(
     }
 }
 
-template <int BM, int BN, int WMW, typename TY>
+template <int BM, int BN, int WMW, int FMT, typename TY>
 int run_staged(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_w8_staged<BM, BN, WMW, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
-                       static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
-                       a.scale, a.bias, static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K,
-                       (int)(a.kw ? a.kw : a.K));
+    hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
+                       static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, static_cast<TY*>(a.y),
+                       a.ldy, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
     return launch_status();
 }
 
 bool staged_supported_impl(const LinearArgs& a) {
-    if (a.fmt != kW8 || a.x_dtype != TIQ_BF16 || a.K % BK != 0) return false;
+    if ((a.fmt != kW8 && a.fmt != kW4) || a.x_dtype != TIQ_BF16 || a.K % BK != 0) return false;
     if (a.kw && (a.kw % BK != 0 || a.K % a.kw != 0)) return false;
+    const int64_t kw = a.kw ? a.kw : a.K;
     const int unit = a.y_dtype == TIQ_F32 ? 4 : 8;
     if (a.N % unit != 0 || a.ldy % unit != 0 || !aligned(a.y, 16)) return false;
     if (!aligned(a.scale, 16) || (a.bias && !aligned(a.bias, 16))) return false;
     if (!aligned(a.x, 16) || a.ldx % 8 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
     // 32-bit byte offsets from the base pointers
-    if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + (a.kw ? a.kw : a.K) > 0xffffffffLL)
-        return false;
+    if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + kw > 0xffffffffLL) return false;
     return true;
 }
 
@@ -405,22 +433,24 @@ size_t staged_split_workspace(int64_t M, int64_t N, int64_t K) {
     return S > 1 ? (size_t)((S * M * N * 4 + 255) / 256 * 256) : 0;
 }
 
+template <int FMT>
 int dispatch_staged_f32(const LinearArgs& a, int choice) {
     switch (choice) {
-        case 0: return run_staged<256, 256, 2, float>(a);
-        case 1: return run_staged<256, 128, 2, float>(a);
-        default: return run_staged<128, 128, 2, float>(a);
+        case 0: return run_staged<256, 256, 2, FMT, float>(a);
+        case 1: return run_staged<256, 128, 2, FMT, float>(a);
+        default: return run_staged<128, 128, 2, FMT, float>(a);
     }
 }
 
+template <int FMT>
 int dispatch_staged_bf16(const LinearArgs& a, int choice) {
     switch (choice) {
-        case 0: return run_staged<256, 256, 2, uint16_t>(a);
-        case 1: return run_staged<256, 128, 2, uint16_t>(a);
-        case 3: return run_staged<224, 256, 1, uint16_t>(a);
-        case 4: return run_staged<160, 256, 1, uint16_t>(a);
-        case 5: return run_staged<224, 128, 1, uint16_t>(a);
-        default: return run_staged<128, 128, 2, uint16_t>(a);
+        case 0: return run_staged<256, 256, 2, FMT, uint16_t>(a);
+        case 1: return run_staged<256, 128, 2, FMT, uint16_t>(a);
+        case 3: return run_staged<224, 256, 1, FMT, uint16_t>(a);
+        case 4: return run_staged<160, 256, 1, FMT, uint16_t>(a);
+        case 5: return run_staged<224, 128, 1, FMT, uint16_t>(a);
+        default: return run_staged<128, 128, 2, FMT, uint16_t>(a);
     }
 }
 
@@ -431,21 +461,21 @@ int staged_gemm_choice(const LinearArgs& a) { return staged_choice(a.M, a.N, a.K
 
 int launch_staged_gemm(const LinearArgs& a, int choice) {
     if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
-    if (a.y_dtype == TIQ_F32) return dispatch_staged_f32(a, choice);
-    return dispatch_staged_bf16(a, choice);
+    if (a.fmt == kW4) return a.y_dtype == TIQ_F32 ? dispatch_staged_f32<kW4>(a, choice) : dispatch_staged_bf16<kW4>(a, choice);
+    return a.y_dtype == TIQ_F32 ? dispatch_staged_f32<kW8>(a, choice) : dispatch_staged_bf16<kW8>(a, choice);
 }
 
 int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
-    if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
+    if (a.fmt != kW8 || !staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
     const int64_t S = staged_splits(a.M, a.N, a.K);
     const size_t need = staged_split_workspace(a.M, a.N, a.K);
     if (S <= 1 || !ws || ws_bytes < need || !aligned(ws, 16)) return TIQ_EUNSUPPORTED;
     float* part = static_cast<float*>(ws);
     const int64_t tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
     // the products: raw fp32 slices [S][M][N] (unit scale, no bias in the kernel)
-    hipLaunchKernelGGL((gemm_w8_staged<128, 128, 2, float>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
-                       a.stream, static_cast<const uint16_t*>(a.x), a.ldx, reinterpret_cast<const int8_t*>(a.w), a.ldw,
-                       a.scale, a.bias, part, (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
+    hipLaunchKernelGGL((gemm_staged<128, 128, 2, kW8, float>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
+                       a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, part,
+                       (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
     const int64_t quads = a.M * a.N / 4;

@@ -84,8 +84,8 @@ __global__ void split_bf16x3_kernel(const float* __restrict__ x, int64_t ldx, in
 size_t split_workspace(int64_t M, int64_t K) { return (size_t)(M * 3 * K * 2 + 255) / 256 * 256; }
 
 // fp32 activations through the matrix cores when a GEMM takes the three-plane
-// problem (the staged kernel for int8 weights, the LDS-dequant one for int4
-// and group-wise int4); TIQ_EUNSUPPORTED otherwise (the caller falls back).
+// problem (the staged kernel, else the LDS-dequant one); TIQ_EUNSUPPORTED
+// otherwise (the caller falls back).
 int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     if (a.x_dtype != TIQ_F32 || a.fmt == kF32 || a.M < kGemmMinRows || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
     if (!aligned(a.x, 16) || a.ldx % 4 != 0 || a.M * 3 * a.K > 0x7fffffffLL) return TIQ_EUNSUPPORTED;
@@ -95,7 +95,7 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     g.K = 3 * a.K;
     g.ldx = 3 * a.K;
     g.kw = a.K;
-    const bool staged = a.fmt == kW8 && staged_gemm_supported(g);
+    const bool staged = staged_gemm_supported(g);
     if (!staged && !gemm_supported(g)) return TIQ_EUNSUPPORTED;
     if (!ws || ws_bytes < split_workspace(a.M, a.K) || !aligned(ws, 16)) return TIQ_EWORKSPACE;
     const int64_t n = a.M * (a.K / 4);

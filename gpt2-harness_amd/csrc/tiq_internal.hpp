@@ -81,9 +81,10 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
 size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N);
 size_t decode_planes_bytes(int64_t M, int64_t K);
 
-// The register-staged int8 GEMM (gemm_staged.hip): whether it takes these
-// arguments, its tile choice (0: 256 x 256, 1: 256 x 128, 2: 128 x 128; bf16
-// output also 3: 224 x 256, 4: 160 x 256, 5: 224 x 128) and its launch.
+// The register-staged GEMM (gemm_staged.hip; int8 and reference-layout int4
+// weights): whether it takes these arguments, its tile choice (0: 256 x 256,
+// 1: 256 x 128, 2: 128 x 128; bf16 output also 3: 224 x 256, 4: 160 x 256,
+// 5: 224 x 128) and its launch.
 bool staged_gemm_supported(const LinearArgs& a);
 int staged_gemm_choice(const LinearArgs& a);
 int launch_staged_gemm(const LinearArgs& a, int choice);

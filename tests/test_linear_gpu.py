@@ -295,17 +295,27 @@ def test_strided_activations_and_outputs(dev, c_oracle):
     assert torch.all(ys[:, N:] == 7.0), "kernel wrote outside its output rows"
 
 
-@pytest.mark.parametrize("KN", [(768, 2304), (1600, 6400), (6400, 1600)])
-@pytest.mark.parametrize("M", [1, 4, 256])
+# int4 in the reference's nibble layout: the GEMV at decode sizes, the staged
+# MFMA GEMM (nibbles staged into bf16 tiles) at prefill sizes, every XL shape
+# at M = 4096 and partial tiles; bf16 output exactly the RNE of the fp32 one.
+@pytest.mark.parametrize("KN,M", [((768, 2304), 1), ((768, 2304), 4), ((1600, 6400), 1), ((6400, 1600), 4),
+                                  ((768, 2304), 256), ((1600, 6400), 256), ((6400, 1600), 300),
+                                  ((1600, 4800), 4096), ((1600, 1600), 4096), ((1600, 6400), 4096),
+                                  ((6400, 1600), 4096), ((3072, 768), 1000)])
 def test_linear_w4_reference_layout(dev, c_oracle, KN, M):
     K, N = KN
     w, x, b = _inputs(K, N, M, M + K, torch.bfloat16 if M >= 16 else torch.float32)
     q, s = c_oracle.quantize_per_channel(w.numpy(), 4)
     packed = torch.from_numpy(c_oracle.pack_int4(q)).to(dev)
+    sd, bd, xd = torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
     y = torch.empty(M, N, device=dev)
-    _call("tiq_linear_w4", x.to(dev), packed, torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), N, y)
+    _call("tiq_linear_w4", xd, packed, sd, bd, N, y)
     ok, err, bound = OL.within_tolerance(y, OL.linear_ref(x, OL.dequantize(q, s), b))
     assert ok, (err, bound)
+    if M >= 16:
+        ybf = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        _call("tiq_linear_w4", xd, packed, sd, bd, N, ybf)
+        assert torch.equal(ybf.cpu(), y.cpu().to(torch.bfloat16)), "bf16 output is not RNE of the fp32 output"
 
 
 @pytest.mark.parametrize("KN", [(768, 2304), (1600, 4800), (6400, 1600)])
