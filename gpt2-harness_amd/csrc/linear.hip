@@ -124,7 +124,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 112; }
+extern "C" int tiq_version(void) { return 113; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
@@ -321,10 +321,16 @@ extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, 
 }
 
 extern "C" size_t tiq_decode_linear_workspace(int w_format, int64_t M, int64_t K, int64_t N) {
-    if ((w_format != TIQ_WF_INT8 && w_format != TIQ_WF_F32) || M < kSkinnyMinRows || M > 64 || K <= 0 ||
+    if ((w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT8_TILED && w_format != TIQ_WF_F32) ||
+        M < kSkinnyMinRows || M > 64 || K <= 0 ||
         K % 32 != 0 || N <= 0)
         return 0;
     return decode_linear_workspace(M, K, N);
+}
+
+extern "C" int tiq_tile_int8(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* tiles, void* stream) {
+    return launch_tile_int8(reinterpret_cast<const uint8_t*>(w), N, K, ldw, reinterpret_cast<uint8_t*>(tiles),
+                            as_stream(stream));
 }
 
 extern "C" size_t tiq_decode_planes_bytes(int64_t M, int64_t K) {
@@ -388,18 +394,18 @@ extern "C" int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_
                                  int activation, const float* residual, int64_t ld_residual,
                                  const float* next_ln_weight, const float* next_ln_bias, float next_ln_eps,
                                  uint16_t* planes_out, void* workspace, size_t workspace_bytes, void* stream) {
-    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_F32) return TIQ_EUNSUPPORTED;
+    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT8_TILED && w_format != TIQ_WF_F32) return TIQ_EUNSUPPORTED;
     if (activation != TIQ_ACT_NONE && activation != TIQ_ACT_GELU_TANH) return TIQ_EINVAL;
     if ((ln_weight == nullptr) != (ln_bias == nullptr)) return TIQ_EINVAL;
     if (M < 0 || K < 0 || N < 0) return TIQ_EINVAL;
     if (M == 0 || N == 0) return TIQ_OK;
-    if (!w || (w_format == TIQ_WF_INT8 && !scale)) return TIQ_EINVAL;
+    if (!w || (w_format != TIQ_WF_F32 && !scale)) return TIQ_EINVAL;
     if (x_planes && ln_weight) return TIQ_EINVAL;  // planes already carry their LayerNorm
     if (!x_planes && (!x || ldx < K)) return TIQ_EINVAL;
     if (y && ldy < N) return TIQ_EINVAL;
     if (residual && (!y || ld_residual < N)) return TIQ_EINVAL;
     const WFormat fmt = (WFormat)w_format;
-    LinearArgs a = make_args(x, TIQ_F32, M, K, ldx, static_cast<const uint8_t*>(w), fmt == kW8 ? K : 4 * K, scale,
+    LinearArgs a = make_args(x, TIQ_F32, M, K, ldx, static_cast<const uint8_t*>(w), fmt == kF32 ? 4 * K : K, scale,
                              nullptr, 0, bias, N, y, TIQ_F32, ldy, stream, fmt);
     a.fuse.ln_w = ln_weight;
     a.fuse.ln_b = ln_bias;

@@ -11,6 +11,7 @@ enum WFormat : int {
     kW4 = 1,   // reference nibble layout, row n at byte n * K / 2 (K even)
     kW4G = 2,  // group-wise nibbles, row n at byte n * ((K + 1) / 2), fp16 group scales
     kF32 = 3,  // fp32 weights (an unquantized Linear such as the tied lm_head), no scale
+    kW8T = 4,  // int8 codes in 32 x 32 operand tiles (tiq_tile_int8; batched decode only)
 };
 
 // Optional work fused around a decode GEMV: LayerNorm of the activation rows
@@ -80,6 +81,8 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
                       const float* next_ln_b, float next_eps, uint16_t* planes_out);
 size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N);
 size_t decode_planes_bytes(int64_t M, int64_t K);
+// int8 codes (N, K) -> the operand tiles the decode product reads with kW8T.
+int launch_tile_int8(const uint8_t* w, int64_t N, int64_t K, int64_t ldw, uint8_t* tiles, hipStream_t stream);
 
 // The register-staged GEMM (gemm_staged.hip; int8 and reference-layout int4
 // weights): whether it takes these arguments, its tile choice (0: 256 x 256,

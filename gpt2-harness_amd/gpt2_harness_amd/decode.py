@@ -244,6 +244,18 @@ class FusedDecoder(_DecoderBase):
             self.p_ln2 = torch.empty(pc, dtype=torch.uint8, device=dev)   # LayerNorm 2 planes
             self.p_hid = torch.empty(ph, dtype=torch.uint8, device=dev)   # GELU(c_fc) planes
             self.p_att = torch.empty(pc, dtype=torch.uint8, device=dev)   # attention output planes
+            # the block Linears' codes once more, in the operand tiles the
+            # batched products read as 1 KB consecutive loads (the row-major
+            # codes stay for prefill): 1x the int8 weight bytes again
+            self.tiles = {}
+            for lin in lins:
+                if lin.out_features % 32 or lin.in_features % 32:
+                    continue  # whole 32 x 32 tiles only; these keep the row-major codes
+                t = torch.empty_like(lin.codes)
+                _lib.check(L.tiq_tile_int8(lin.codes.data_ptr(), lin.out_features, lin.in_features,
+                                           lin.codes.stride(0), t.data_ptr(),
+                                           torch.cuda.current_stream(dev).cuda_stream), "tile int8 codes")
+                self.tiles[id(lin)] = t
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
@@ -266,6 +278,9 @@ class FusedDecoder(_DecoderBase):
         K = lin.in_features if hasattr(lin, "in_features") else self.cfg.n_embd
         N = lin.out_features if hasattr(lin, "out_features") else self.cfg.vocab_size
         w = lin.codes if isinstance(lin, QuantLinear) else self.head_w
+        tiles = getattr(self, "tiles", {}).get(id(lin))
+        if tiles is not None:
+            w, wf = tiles, _lib.WF_INT8_TILED
         scale = lin.scale.data_ptr() if isinstance(lin, QuantLinear) else None
         bias = _lib.ptr(lin.bias) if isinstance(lin, QuantLinear) else None
         rc = self.L.tiq_decode_linear(

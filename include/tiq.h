@@ -42,7 +42,14 @@ enum tiq_status {
 enum tiq_dtype { TIQ_F32 = 0, TIQ_BF16 = 1 };
 
 /* Weight storage formats accepted by tiq_linear_fused. */
-enum tiq_weight_format { TIQ_WF_INT8 = 0, TIQ_WF_INT4 = 1, TIQ_WF_INT4_GROUPWISE = 2, TIQ_WF_F32 = 3 };
+enum tiq_weight_format {
+    TIQ_WF_INT8 = 0,
+    TIQ_WF_INT4 = 1,
+    TIQ_WF_INT4_GROUPWISE = 2,
+    TIQ_WF_F32 = 3,
+    /* int8 codes rearranged by tiq_tile_int8 (tiq_decode_linear only) */
+    TIQ_WF_INT8_TILED = 4,
+};
 
 /* Activations fused after a linear. */
 enum tiq_activation { TIQ_ACT_NONE = 0, TIQ_ACT_GELU_TANH = 1 };
@@ -261,7 +268,9 @@ int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_
                         size_t workspace_bytes, void* stream);
 
 /* Batched decode-step linear (5 <= M <= 64 fp32 activation rows; int8
- * weights with per-row scale, or fp32 weights) whose K range is split over
+ * weights with per-row scale -- row-major (TIQ_WF_INT8) or in the operand
+ * tiles of tiq_tile_int8 (TIQ_WF_INT8_TILED, N % 32 == 0) -- or fp32
+ * weights) whose K range is split over
  * workgroups: the matrix-core products write fp32 partial sums to the
  * workspace, a second kernel sums them in a fixed order and applies
  *     y = act(LayerNorm(x) @ W^T * scale + bias) + residual
@@ -281,6 +290,19 @@ int tiq_linear_fused_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_
  * No counterpart in the reference (its decode runs one torch op per step). */
 size_t tiq_decode_linear_workspace(int w_format, int64_t M, int64_t K, int64_t N);
 size_t tiq_decode_planes_bytes(int64_t M, int64_t K);
+
+/* The int8 codes of an (N, K) weight (leading dimension ldw bytes, 16-byte
+ * aligned rows) rearranged for tiq_decode_linear with w_format
+ * TIQ_WF_INT8_TILED: N * K bytes in 1 KB blocks, block t * (K / 32) + u
+ * holding rows 32 t .. 32 t + 31 and columns 32 u .. 32 u + 31 in the order a
+ * wavefront's matrix-core operands take them (byte 16 l + j of the block is
+ * w[32 t + l % 32][32 u + 16 (l / 32) + j]), so each 64-lane load of the
+ * product reads 1 KB of consecutive memory. Needs N % 32 == 0, K % 32 == 0,
+ * ldw % 16 == 0 and 16-byte aligned pointers. The scale, results and every
+ * other argument of tiq_decode_linear are those of the row-major codes
+ * (TIQ_WF_INT8): the products are the same, in the same order. No
+ * counterpart in the reference (a device layout of this library). */
+int tiq_tile_int8(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* tiles, void* stream);
 int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M, int64_t K, const void* w,
                       int w_format, const float* scale, const float* bias, int64_t N, float* y, int64_t ldy,
                       const float* ln_weight, const float* ln_bias, float ln_eps, int activation,

@@ -623,3 +623,85 @@ def test_gelu_tanh_pass(dev, n):
     assert torch.equal(gelu_tanh(xd).cpu(), y.cpu())
     torch_chain = 0.5 * xd * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd.pow(3))))
     assert torch.allclose(y, torch_chain, rtol=1e-5, atol=1e-6)
+
+
+# ---- operand-tiled int8 codes (tiq_tile_int8, TIQ_WF_INT8_TILED) -----------
+
+@pytest.mark.parametrize("N,K,ldw", [(64, 96, 96), (96, 64, 80), (4800, 1600, 1600)])
+def test_tile_int8_layout(dev, N, K, ldw):
+    """Byte 16 l + j of block t * (K / 32) + u is w[32 t + l % 32][32 u +
+    16 (l / 32) + j]: the expected bytes are rearranged here on the CPU."""
+    gen = torch.Generator().manual_seed(N + K + ldw)
+    full = torch.randint(-127, 128, (N, ldw), generator=gen, dtype=torch.int8)
+    w = full[:, :K]
+    tiles = torch.empty(N * K, dtype=torch.int8, device=dev)
+    _lib.check(_lib.lib().tiq_tile_int8(full.to(dev).data_ptr(), N, K, ldw, tiles.data_ptr(), _st()), "tile")
+    torch.cuda.synchronize()
+    # (t, r, u, h, j) -> (t, u, h, r, j)
+    want = w.reshape(N // 32, 32, K // 32, 2, 16).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert torch.equal(tiles.cpu(), want)
+
+
+def test_tile_int8_rejects_partial_tiles(dev):
+    L = _lib.lib()
+    w = torch.zeros(48, 64, dtype=torch.int8, device=dev)
+    t = torch.empty_like(w)
+    assert L.tiq_tile_int8(w.data_ptr(), 48, 64, 64, t.data_ptr(), _st()) == -4
+    assert L.tiq_tile_int8(w.data_ptr(), 32, 48, 64, t.data_ptr(), _st()) == -4
+    assert L.tiq_tile_int8(w.data_ptr(), 32, 64, 40, t.data_ptr(), _st()) == -1  # ldw < K
+    # the decode linear refuses tiled codes with a partial row tile
+    n_ws = int(L.tiq_decode_linear_workspace(_lib.WF_INT8_TILED, 8, 64, 48))
+    ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=dev)
+    x = torch.zeros(8, 64, device=dev)
+    y = torch.empty(8, 48, device=dev)
+    s = torch.ones(48, device=dev)
+    rc = L.tiq_decode_linear(x.data_ptr(), 64, None, 8, 64, w.data_ptr(), _lib.WF_INT8_TILED, s.data_ptr(), None, 48,
+                             y.data_ptr(), 48, None, None, 1e-5, 0, None, 0, None, None, 1e-5, None, ws.data_ptr(),
+                             n_ws, _st())
+    assert rc == -4
+
+
+@pytest.mark.parametrize("M", [5, 32, 64])
+@pytest.mark.parametrize("K,N", [(1600, 4800), (1600, 1600), (6400, 1600), (768, 2304), (3072, 768)])
+def test_decode_linear_tiled_equals_row_major(dev, c_oracle, M, K, N):
+    """The tiled codes feed the same products in the same order: every output
+    of the decode chain (fp32 rows with LayerNorm in, GELU, planes out; then
+    planes in, residual in place, next LayerNorm planes out) is bit-identical
+    to the row-major call's."""
+    gen = torch.Generator().manual_seed(M * 7 + K + N)
+    qd, sd, _ = _w8(c_oracle, N, K, gen, dev)
+    tiles = torch.empty_like(qd)
+    _lib.check(_lib.lib().tiq_tile_int8(qd.data_ptr(), N, K, qd.stride(0), tiles.data_ptr(), _st()), "tile")
+    b = (0.1 * torch.randn(N, generator=gen)).to(dev)
+    x = (torch.randn(M, K, generator=gen) * 2 + 0.5).to(dev)
+    lw, lb = (1 + 0.1 * torch.randn(K, generator=gen)).to(dev), (0.1 * torch.randn(K, generator=gen)).to(dev)
+    nw, nb = (1 + 0.1 * torch.randn(N, generator=gen)).to(dev), (0.1 * torch.randn(N, generator=gen)).to(dev)
+    L = _lib.lib()
+    outs = {}
+    for wf, wd in ((_lib.WF_INT8, qd), (_lib.WF_INT8_TILED, tiles)):
+        y = torch.empty(M, N, device=dev)
+        pl = torch.zeros(int(L.tiq_decode_planes_bytes(M, N)), dtype=torch.uint8, device=dev)
+        _lib.check(_dl(x, None, M, K, wd, wf, sd, b, N, y, ln=(lw, lb), act=_lib.ACT_GELU_TANH, planes=pl), "rows in")
+        r = torch.randn(M, N, generator=torch.Generator().manual_seed(M)).to(dev)
+        y2 = r.clone()
+        pl2 = torch.zeros_like(pl)
+        _lib.check(_dl(None, _split_planes(x, dev), M, K, wd, wf, sd, b, N, y2, res=y2, nln=(nw, nb), planes=pl2),
+                   "planes in")
+        outs[wf] = (y, pl, y2, pl2)
+    for a, c in zip(outs[_lib.WF_INT8], outs[_lib.WF_INT8_TILED]):
+        assert torch.equal(a, c)
+
+
+def _split_planes(x, dev):
+    """Operand planes of fp32 rows x, made by the library's own split (a decode
+    linear with planes out and no product work kept: the planes of y = x come
+    from the reduction with one slice)."""
+    M, K = x.shape
+    L = _lib.lib()
+    pl = torch.zeros(int(L.tiq_decode_planes_bytes(M, K)), dtype=torch.uint8, device=dev)
+    # identity weights: y = x exactly (int8 codes 1 on the diagonal, scale 1),
+    # planes of y out
+    eye = torch.eye(K, dtype=torch.int8, device=dev)
+    one = torch.ones(K, device=dev)
+    _lib.check(_dl(x, None, M, K, eye, _lib.WF_INT8, one, None, K, None, planes=pl), "identity planes")
+    return pl
