@@ -150,8 +150,9 @@ __global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__
     }
 }
 
-// The end of a split-K decode linear, one workgroup of 1024 threads per
-// activation row m, thread t owning the 8 consecutive columns 8 t .. 8 t + 7:
+// The end of a split-K decode linear, one workgroup of NT threads per
+// activation row m (256 for rows of up to 2048 columns, else 1024), thread t
+// owning the 8 consecutive columns 8 t .. 8 t + 7:
 // the S partial rows (row m of slice s at part + (s M + m) ldp) are summed in
 // a fixed order (the result does not depend on timing), then scale, bias,
 // GELU(tanh) and the residual (which may alias y: every element is read and
@@ -159,31 +160,26 @@ __global__ __launch_bounds__(256) void ln_split_kernel(const float* __restrict__
 // With PLANES the row is also written as the next linear's operand planes
 // (ln_split_kernel's layout, K' = N), after LayerNorm when LN. With S = 1,
 // no epilogue and part = fp32 rows, the kernel is a LayerNorm + split pass.
-// Every load is issued before any is used and none sits behind a branch
-// (the optional operands are compile-time flags).
+// Every load is issued before any is used (the slices eight at a time, after
+// the epilogue operands) and none sits behind a branch (the optional operands
+// are compile-time flags): one trip to memory for up to eight slices.
 constexpr int kRedThreads = 1024;
 constexpr int kRedMaxCols = kRedThreads * 8;
-template <bool LN, bool PLANES, bool SC, bool BI, bool RS>
-__global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* __restrict__ part, int64_t ldp,
-                                                                  int S, int M, int N,
-                                                                  const float* __restrict__ scale,
-                                                                  const float* __restrict__ bias, int act,
-                                                                  const float* res, int64_t ldr, float* y,
-                                                                  int64_t ldy, const float* __restrict__ ln_w,
-                                                                  const float* __restrict__ ln_b, float ln_eps,
-                                                                  uint16_t* __restrict__ x3) {
-    __shared__ float red[kRedThreads / 64];
+template <bool LN, bool PLANES, bool SC, bool BI, bool RS, int NT>
+__global__ __launch_bounds__(NT) void reduce_rows_kernel(const float* __restrict__ part, int64_t ldp, int S, int M,
+                                                         int N, const float* __restrict__ scale,
+                                                         const float* __restrict__ bias, int act, const float* res,
+                                                         int64_t ldr, float* y, int64_t ldy,
+                                                         const float* __restrict__ ln_w,
+                                                         const float* __restrict__ ln_b, float ln_eps,
+                                                         uint16_t* __restrict__ x3) {
+    __shared__ float red[NT / 64];
     const int m = blockIdx.x, tid = threadIdx.x;
     const int NC8 = N / 8;
     const bool own = tid < NC8;
     const int n = 8 * min(tid, NC8 - 1);  // a thread past the row repeats its last chunk, unused
-    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int si = 0; si < S; ++si) {
-        const float* pr = part + ((int64_t)si * M + m) * ldp + n;
-        const float4 p0 = reinterpret_cast<const float4*>(pr)[0], p1 = reinterpret_cast<const float4*>(pr)[1];
-        a[0] += p0.x; a[1] += p0.y; a[2] += p0.z; a[3] += p0.w;
-        a[4] += p1.x; a[5] += p1.y; a[6] += p1.z; a[7] += p1.w;
-    }
+    // the epilogue operands first, then the slices (indices clamped, the
+    // repeats not added), summed in slice order
     float4 sc[2], bi[2], rs[2], gw[2], gb[2];
     if constexpr (SC) sc[0] = reinterpret_cast<const float4*>(scale + n)[0], sc[1] = reinterpret_cast<const float4*>(scale + n)[1];
     if constexpr (BI) bi[0] = reinterpret_cast<const float4*>(bias + n)[0], bi[1] = reinterpret_cast<const float4*>(bias + n)[1];
@@ -193,6 +189,24 @@ __global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* _
     }
     if constexpr (LN) gw[0] = reinterpret_cast<const float4*>(ln_w + n)[0], gw[1] = reinterpret_cast<const float4*>(ln_w + n)[1];
     if constexpr (LN) gb[0] = reinterpret_cast<const float4*>(ln_b + n)[0], gb[1] = reinterpret_cast<const float4*>(ln_b + n)[1];
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int z0 = 0; z0 < S; z0 += 8) {
+        float4 p[8][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float* pr = part + ((int64_t)min(z0 + j, S - 1) * M + m) * ldp + n;
+            p[j][0] = reinterpret_cast<const float4*>(pr)[0];
+            p[j][1] = reinterpret_cast<const float4*>(pr)[1];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool use = z0 + j < S;
+            a[0] = use ? a[0] + p[j][0].x : a[0]; a[1] = use ? a[1] + p[j][0].y : a[1];
+            a[2] = use ? a[2] + p[j][0].z : a[2]; a[3] = use ? a[3] + p[j][0].w : a[3];
+            a[4] = use ? a[4] + p[j][1].x : a[4]; a[5] = use ? a[5] + p[j][1].y : a[5];
+            a[6] = use ? a[6] + p[j][1].z : a[6]; a[7] = use ? a[7] + p[j][1].w : a[7];
+        }
+    }
     auto lane8 = [](const float4 (&f)[2], int i) { const float4 q = f[i >> 2]; return (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w; };
     float v[8];
 #pragma unroll
@@ -223,7 +237,7 @@ __global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* _
         __syncthreads();
         float tot = 0.f;
 #pragma unroll
-        for (int w = 0; w < kRedThreads / 64; ++w) tot += red[w];
+        for (int w = 0; w < NT / 64; ++w) tot += red[w];
         mu = tot / (float)N;
         __syncthreads();
         float d = 0.f;
@@ -234,7 +248,7 @@ __global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* _
         __syncthreads();
         tot = 0.f;
 #pragma unroll
-        for (int w = 0; w < kRedThreads / 64; ++w) tot += red[w];
+        for (int w = 0; w < NT / 64; ++w) tot += red[w];
         rstd = 1.0f / sqrtf(tot / (float)N + ln_eps);
     }
     if (!own) return;
@@ -267,24 +281,31 @@ __global__ __launch_bounds__(kRedThreads) void reduce_rows_kernel(const float* _
 // The reduction kernel instance for these operands.
 using ReduceFn = void (*)(const float*, int64_t, int, int, int, const float*, const float*, int, const float*,
                           int64_t, float*, int64_t, const float*, const float*, float, uint16_t*);
-template <bool LN, bool PLANES>
+template <bool LN, bool PLANES, int NT>
 ReduceFn reduce_fn(bool sc, bool bi, bool rs) {
     const int k = (sc ? 4 : 0) | (bi ? 2 : 0) | (rs ? 1 : 0);
     switch (k) {
-        case 0: return reduce_rows_kernel<LN, PLANES, false, false, false>;
-        case 1: return reduce_rows_kernel<LN, PLANES, false, false, true>;
-        case 2: return reduce_rows_kernel<LN, PLANES, false, true, false>;
-        case 3: return reduce_rows_kernel<LN, PLANES, false, true, true>;
-        case 4: return reduce_rows_kernel<LN, PLANES, true, false, false>;
-        case 5: return reduce_rows_kernel<LN, PLANES, true, false, true>;
-        case 6: return reduce_rows_kernel<LN, PLANES, true, true, false>;
-        default: return reduce_rows_kernel<LN, PLANES, true, true, true>;
+        case 0: return reduce_rows_kernel<LN, PLANES, false, false, false, NT>;
+        case 1: return reduce_rows_kernel<LN, PLANES, false, false, true, NT>;
+        case 2: return reduce_rows_kernel<LN, PLANES, false, true, false, NT>;
+        case 3: return reduce_rows_kernel<LN, PLANES, false, true, true, NT>;
+        case 4: return reduce_rows_kernel<LN, PLANES, true, false, false, NT>;
+        case 5: return reduce_rows_kernel<LN, PLANES, true, false, true, NT>;
+        case 6: return reduce_rows_kernel<LN, PLANES, true, true, false, NT>;
+        default: return reduce_rows_kernel<LN, PLANES, true, true, true, NT>;
     }
 }
 
-ReduceFn pick_reduce(bool ln, bool planes, bool sc, bool bi, bool rs) {
-    if (!planes) return reduce_fn<false, false>(sc, bi, rs);
-    return ln ? reduce_fn<true, true>(sc, bi, rs) : reduce_fn<false, true>(sc, bi, rs);
+// threads of the reduction workgroup for rows of N columns (8 a thread)
+int red_threads(int64_t N) { return N <= 2048 ? 256 : 1024; }
+
+ReduceFn pick_reduce(bool ln, bool planes, bool sc, bool bi, bool rs, int64_t N) {
+    if (N <= 2048) {
+        if (!planes) return reduce_fn<false, false, 256>(sc, bi, rs);
+        return ln ? reduce_fn<true, true, 256>(sc, bi, rs) : reduce_fn<false, true, 256>(sc, bi, rs);
+    }
+    if (!planes) return reduce_fn<false, false, 1024>(sc, bi, rs);
+    return ln ? reduce_fn<true, true, 1024>(sc, bi, rs) : reduce_fn<false, true, 1024>(sc, bi, rs);
 }
 
 // WF: kW8 (int8 codes, per-row scale), kW8T (the same codes in the operand
@@ -675,6 +696,104 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     }
 }
 
+// The product of a split batched decode linear whose output the reduction
+// kernel finishes: int8 weights (row-major or operand tiles), the activation
+// planes of the previous call in, raw fp32 partial sums out (slice z of
+// `part` holds K units [z U / S, (z + 1) U / S) of every output; scale, bias
+// and the rest are applied by the reduction). A workgroup of 8 wavefronts owns
+// RT 32-row weight tiles (N rows 32 t0 .. 32 (t0 + RT) - 1) and 32 activation
+// rows; its wavefronts split its K units, at most MU each, and every
+// activation operand a wavefront loads feeds the MFMAs of all RT tiles. All
+// loads are issued at once; the wavefronts' partial tiles are summed through
+// LDS in wavefront order (results do not depend on timing).
+template <int WF, int RT, int MU>
+__global__ __launch_bounds__(kWaves * 64, 1) void split_product_kernel(const uint16_t* __restrict__ x3, int M, int K,
+                                                                      const uint8_t* __restrict__ w, int64_t ldw,
+                                                                      int N, float* __restrict__ part) {
+    static_assert(WF == kW8 || WF == kW8T, "int8 codes");
+    __shared__ float red[kWaves][RT * 32][33];  // partial tiles, rows padded
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+    const int t0 = blockIdx.x * RT, m0 = blockIdx.y * 32;
+    const int U = K / 32;
+    const int ub = blockIdx.z * U / gridDim.z, Us = (blockIdx.z + 1) * U / gridDim.z - ub;
+    const int u0 = ub + wave * Us / kWaves, cnt = ub + (wave + 1) * Us / kWaves - u0;  // <= MU (host checks)
+    const bool xrow_ok = m0 + r < M;
+    const uint16_t* x3t = x3 + (int64_t)blockIdx.y * U * 6 * 64 * 8 + lane * 8;
+    u32x4 wreg[MU][RT];
+#pragma unroll
+    for (int c = 0; c < MU; ++c)
+        if (c < cnt) {
+#pragma unroll
+            for (int j = 0; j < RT; ++j) {
+                if constexpr (WF == kW8T) {  // 1 KB of consecutive codes per instruction, read once
+                    wreg[c][j] = __builtin_nontemporal_load(
+                        reinterpret_cast<const u32x4*>(w + ((int64_t)(t0 + j) * U + u0 + c) * 1024 + lane * 16));
+                } else {  // lane (r, h): 16 codes of row 32 (t0 + j) + r (clamped for a partial tile)
+                    wreg[c][j] = *reinterpret_cast<const u32x4*>(w + (int64_t)min(32 * (t0 + j) + r, N - 1) * ldw +
+                                                                 32 * (u0 + c) + 16 * h);
+                }
+            }
+        }
+    u32x4 xv[MU][3][2];
+#pragma unroll
+    for (int c = 0; c < MU; ++c)
+        if (c < cnt) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    xv[c][q][e] = *reinterpret_cast<const u32x4*>(x3t + (((int64_t)(u0 + c) * 3 + q) * 2 + e) * 64 * 8);
+        }
+    floatx16 acc[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[j][q] = 0.f;
+#pragma unroll
+    for (int c = 0; c < MU; ++c)
+        if (c < cnt) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                bf16x8 xq[3];
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    u32x4 t = xv[c][q][e];
+                    if (!xrow_ok) t = u32x4{0u, 0u, 0u, 0u};
+                    xq[q] = __builtin_bit_cast(bf16x8, t);
+                }
+#pragma unroll
+                for (int j = 0; j < RT; ++j) {
+                    const u32x4 d = wreg[c][j];
+                    const uint32_t s0 = e == 0 ? d.x : d.z, s1 = e == 0 ? d.y : d.w;
+                    const u32x4 wq = {bf16x2_of_bytes(s0, 0), bf16x2_of_bytes(s0, 16), bf16x2_of_bytes(s1, 0),
+                                      bf16x2_of_bytes(s1, 16)};
+                    const bf16x8 wf = __builtin_bit_cast(bf16x8, wq);
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xq[0], acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xq[1], acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xq[2], acc[j], 0, 0, 0);
+                }
+            }
+        }
+    // register q of lane (r, h) in tile j: output row n = 32 (t0 + j) + 8 (q / 4)
+    // + 4 h + q % 4, activation row m = m0 + r
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) red[wave][32 * j + r][8 * (q >> 2) + 4 * h + (q & 3)] = acc[j][q];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2 * RT; ++t) {  // 1024 outputs a tile, two per thread and tile
+        const int o = threadIdx.x + kWaves * 64 * t;
+        const int j = o >> 10, m = (o >> 5) & 31, nn = o & 31;
+        float v = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) v += red[i][32 * j + m][nn];
+        const int gm = m0 + m, gn = 32 * (t0 + j) + nn;
+        if (gm < M && gn < N) part[((int64_t)blockIdx.z * M + gm) * N + gn] = v;
+    }
+}
+
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 // Workspace: the split activation planes, row tiles x 32 x 3K bf16 in operand order.
@@ -717,13 +836,12 @@ int run_skinny(const LinearArgs& a) {
     return launch_status();
 }
 
-// Splits of a batched decode linear's K range: about 512 workgroups in all,
-// at least one 32-column unit per wavefront of a split.
+// Splits of a batched decode linear's K range when nothing but the split
+// needs the reduction kernel (y rows out, or planes out without LayerNorm or
+// residual): about six 32-column units per wavefront, so a split pays for its
+// partial sums and the reduction launch only on long rows (6400 columns: four
+// splits); with at most 64 output tiles (N <= 2048) two splits.
 int64_t decode_splits(int64_t M, int64_t K, int64_t N) {
-    // about six 32-column units per wavefront: a split pays for its partial
-    // sums and the reduction only on long rows (6400 columns: four splits);
-    // with at most 64 output tiles (N <= 2048) two splits, so that twice the
-    // CUs stream the weights (GPT-2-XL attn.c_proj: 50 tiles, 10.3 -> 9.1 us)
     (void)M;
     int64_t S = (K / 32) / (kWaves * 6);
     if (S <= 1 && (N + 31) / 32 <= 64 && K / 32 >= 2 * kWaves) S = 2;
@@ -731,13 +849,50 @@ int64_t decode_splits(int64_t M, int64_t K, int64_t N) {
     return std::max<int64_t>(1, std::min<int64_t>(S, 32));
 }
 
-size_t partials_bytes(int64_t M, int64_t K, int64_t N) {
-    return round256((size_t)(decode_splits(M, K, N) * M * N) * 4);
+// The split of an int8 product whose output the reduction kernel finishes in
+// any case (LayerNorm'd planes or a residual follow): split_product_kernel
+// with RT weight tiles a workgroup -- two on long rows (K >= 4096, an even
+// tile count), so each activation operand serves twice the weights -- and K
+// split until about 256 workgroups stream the weights, at least one 32-column
+// unit and at most kSplitMaxUnits a wavefront, at most 16 splits.
+// GPT-2-XL at batch 32: attn.c_proj 50 tiles x 5 splits, mlp.c_proj 25 tile
+// pairs x 10 splits.
+constexpr int kSplitMaxUnits = 4;
+struct SplitPlan { int64_t S; int RT; };
+SplitPlan reduce_plan(int64_t M, int64_t K, int64_t N) {
+    const int64_t U = K / 32, tiles = (N + 31) / 32, rows = (M + 31) / 32;
+    const int RT = (U >= 128 && tiles % 2 == 0) ? 2 : 1;
+    const int64_t groups = tiles / RT * rows;
+    int64_t S = std::min<int64_t>(std::max<int64_t>(256 / groups, 1), std::max<int64_t>(U / kWaves, 1));
+    S = std::max<int64_t>(S, (U + kWaves * kSplitMaxUnits - 1) / (kWaves * kSplitMaxUnits));
+    return {std::min<int64_t>(S, 16), RT};
 }
 
+size_t partials_bytes(int64_t M, int64_t K, int64_t N) {
+    const int64_t S = std::max<int64_t>(decode_splits(M, K, N), reduce_plan(M, K, N).S);
+    return round256((size_t)(S * M * N) * 4);
+}
+
+template <int WF, int RT>
+int launch_split_product(const LinearArgs& a, const uint16_t* x3, float* part, int64_t S) {
+    const dim3 grid((unsigned)((a.N + 31) / 32 / RT), (unsigned)((a.M + 31) / 32), (unsigned)S);
+    const int64_t per_wave = ((a.K / 32 + S - 1) / S + kWaves - 1) / kWaves;
+    if (per_wave <= 2)
+        hipLaunchKernelGGL((split_product_kernel<WF, RT, 2>), grid, dim3(kWaves * 64), 0, a.stream, x3, (int)a.M,
+                           (int)a.K, a.w, a.ldw, (int)a.N, part);
+    else
+        hipLaunchKernelGGL((split_product_kernel<WF, RT, kSplitMaxUnits>), grid, dim3(kWaves * 64), 0, a.stream, x3,
+                           (int)a.M, (int)a.K, a.w, a.ldw, (int)a.N, part);
+    return launch_status();
+}
+
+// plan.RT > 0: split_product_kernel with that many tiles a workgroup (int8
+// weights, the reduction follows); else skinny_kernel (its own epilogue
+// without `part`, raw partial slices with it)
 template <int WF>
 int run_decode_t(const LinearArgs& a, const uint16_t* x3, const float* next_ln_w, const float* next_ln_b,
-                 float next_eps, uint16_t* planes_out, float* part, int64_t S) {
+                 float next_eps, uint16_t* planes_out, float* part, SplitPlan plan) {
+    const int64_t S = plan.S;
     const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)((a.M + 31) / 32), (unsigned)S);
     const float* xp = reinterpret_cast<const float*>(x3);
     if (!part) {  // one split: the product kernel's own epilogue writes y and / or the planes
@@ -747,15 +902,23 @@ int run_decode_t(const LinearArgs& a, const uint16_t* x3, const float* next_ln_w
                            a.fuse.ldr, nullptr, planes_out);
         return launch_status();
     }
-    hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, float>), grid, dim3(kWaves * 64), 0, a.stream, xp, (int64_t)0,
-                       (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N, static_cast<float*>(nullptr),
-                       (int64_t)0, nullptr, nullptr, 0.f, 0, nullptr, (int64_t)0, part, nullptr);
-    int rc = launch_status();
+    int rc = TIQ_OK;
+    if constexpr (is_w8<WF>()) {
+        if (plan.RT == 2) rc = launch_split_product<WF, 2>(a, x3, part, S);
+        else if (plan.RT == 1) rc = launch_split_product<WF, 1>(a, x3, part, S);
+    }
+    if (plan.RT == 0) {
+        hipLaunchKernelGGL((skinny_kernel<WF, kXPlanes, float>), grid, dim3(kWaves * 64), 0, a.stream, xp,
+                           (int64_t)0, (int)a.M, (int)a.K, a.w, a.ldw, a.scale, a.bias, (int)a.N,
+                           static_cast<float*>(nullptr), (int64_t)0, nullptr, nullptr, 0.f, 0, nullptr, (int64_t)0,
+                           part, nullptr);
+        rc = launch_status();
+    }
     if (rc != TIQ_OK) return rc;
     const float* sc = is_w8<WF>() ? a.scale : nullptr;
     ReduceFn red = pick_reduce(next_ln_w != nullptr, planes_out != nullptr, sc != nullptr, a.bias != nullptr,
-                               a.fuse.res != nullptr);
-    hipLaunchKernelGGL(red, dim3((unsigned)a.M), dim3(kRedThreads), 0, a.stream, part, (int64_t)a.N, (int)S,
+                               a.fuse.res != nullptr, a.N);
+    hipLaunchKernelGGL(red, dim3((unsigned)a.M), dim3(red_threads(a.N)), 0, a.stream, part, (int64_t)a.N, (int)S,
                        (int)a.M, (int)a.N, sc, a.bias, a.fuse.act, a.fuse.res, a.fuse.ldr, static_cast<float*>(a.y),
                        a.ldy, next_ln_w, next_ln_b, next_eps, planes_out);
     return launch_status();
@@ -783,7 +946,16 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
     // a row the reduction cannot take (N % 8, N > 8192) without planes out:
     // one split, the product kernel's own epilogue
     const bool red_ok = a.N % 8 == 0 && a.N <= kRedMaxCols;
-    const int64_t S = (red_ok || planes_out) ? decode_splits(a.M, a.K, a.N) : 1;
+    // LayerNorm'd planes or a residual after the product: the reduction kernel
+    // runs whatever the split, so int8 products split to fill the GPU
+    const bool must_reduce = planes_out && (next_ln_w || a.fuse.res || a.N % 32 != 0);
+    SplitPlan plan{(red_ok || planes_out) ? decode_splits(a.M, a.K, a.N) : 1, 0};
+    if (w8 && must_reduce && red_ok) {
+        const SplitPlan p = reduce_plan(a.M, a.K, a.N);
+        const int64_t per_wave = ((a.K / 32 + p.S - 1) / p.S + kWaves - 1) / kWaves;
+        if (per_wave <= kSplitMaxUnits && ((a.N + 31) / 32) % p.RT == 0) plan = p;
+    }
+    const int64_t S = plan.S;
     // planes without a LayerNorm or residual from one split: the product
     // kernel writes them itself (its 32 columns are one unit of the next
     // linear's K), no reduction launch
@@ -791,7 +963,7 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
     const bool reduce = !product_planes && (S > 1 || planes_out);
     // every wavefront's share of K fits its weight registers
     const int64_t units = ((a.K / 32 + S - 1) / S + kWaves - 1) / kWaves;
-    if (units > (w8 ? max_units<kW8>() : max_units<kF32>())) return TIQ_EUNSUPPORTED;
+    if (plan.RT == 0 && units > (w8 ? max_units<kW8>() : max_units<kF32>())) return TIQ_EUNSUPPORTED;
     if (!aligned(a.w, 16) || a.ldw % 16 != 0) return TIQ_EALIGN;
     if (x_planes ? !aligned(x_planes, 16)
                  : (!a.x || !aligned(a.x, 16) || a.ldx % 4 != 0 ||
@@ -817,8 +989,8 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
     if (!x3) {
         uint16_t* xs = reinterpret_cast<uint16_t*>(ws);
         if (a.K <= kRedMaxCols) {  // LayerNorm + split: the reduction kernel with one slice, no epilogue
-            ReduceFn f = pick_reduce(a.fuse.ln_w != nullptr, true, false, false, false);
-            hipLaunchKernelGGL(f, dim3((unsigned)a.M), dim3(kRedThreads), 0, a.stream,
+            ReduceFn f = pick_reduce(a.fuse.ln_w != nullptr, true, false, false, false, a.K);
+            hipLaunchKernelGGL(f, dim3((unsigned)a.M), dim3(red_threads(a.K)), 0, a.stream,
                                static_cast<const float*>(a.x), a.ldx, 1, (int)a.M, (int)a.K, nullptr, nullptr, 0,
                                nullptr, (int64_t)0, nullptr, (int64_t)0, a.fuse.ln_w, a.fuse.ln_b, a.fuse.ln_eps, xs);
         } else if (a.fuse.ln_w) {
@@ -835,9 +1007,10 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
         ws += planes_bytes(a.M, a.K);
     }
     float* part = reduce ? reinterpret_cast<float*>(ws) : nullptr;
-    if (a.fmt == kW8) return run_decode_t<kW8>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, S);
-    if (a.fmt == kW8T) return run_decode_t<kW8T>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, S);
-    return run_decode_t<kF32>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, S);
+    if (!part) plan.RT = 0;
+    if (a.fmt == kW8) return run_decode_t<kW8>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, plan);
+    if (a.fmt == kW8T) return run_decode_t<kW8T>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, plan);
+    return run_decode_t<kF32>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, plan);
 }
 
 // One thread per 16 bytes of a tile: block b = (t, u) of (N / 32, K / 32),
