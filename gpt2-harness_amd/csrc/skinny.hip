@@ -392,13 +392,13 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
                 if (ep_m + 16 * t < M) ep_res[t] = res[(int64_t)(ep_m + 16 * t) * ldr + ep_n];
         }
     }
-    // planes out: thread t < 128 finishes row t / 4, columns n0 + 8 (t % 4) + 0..7
-    float4 pe_scale[2] = {make_float4(1.f, 1.f, 1.f, 1.f), make_float4(1.f, 1.f, 1.f, 1.f)};
-    float4 pe_bias[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    // planes out: thread t finishes row t / 16, columns n0 + 2 (t % 16) + 0..1
+    // (every wavefront takes a share of the GELU)
+    float2 pe_scale = make_float2(1.f, 1.f), pe_bias = make_float2(0.f, 0.f);
     if (x3o) {
-        const int c8 = n0 + 8 * (threadIdx.x & 3);  // N % 32 == 0 (the host checks): in range
-        if (W8) pe_scale[0] = reinterpret_cast<const float4*>(scale + c8)[0], pe_scale[1] = reinterpret_cast<const float4*>(scale + c8)[1];
-        if (bias) pe_bias[0] = reinterpret_cast<const float4*>(bias + c8)[0], pe_bias[1] = reinterpret_cast<const float4*>(bias + c8)[1];
+        const int c2 = n0 + 2 * (threadIdx.x & 15);  // N % 32 == 0 (the host checks): in range
+        if (W8) pe_scale = *reinterpret_cast<const float2*>(scale + c2);
+        if (bias) pe_bias = *reinterpret_cast<const float2*>(bias + c2);
     }
     // LayerNorm statistics of the 32 activation rows (two-pass); its weight
     // and bias go to LDS (read there, they add no global loads to the unit
@@ -628,39 +628,33 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
     if (x3o) {
         // The tile as the next linear's operand planes: its 32 columns are
         // unit u = n0 / 32 of that linear's K (= this N), row tile blockIdx.y;
-        // rows past M are not written (the consumer zeroes them).
-        if (threadIdx.x < 128) {
-            const int m = threadIdx.x >> 2, g = threadIdx.x & 3, gm = m0 + m;
-            float v[8];
+        // rows past M are not written (the consumer zeroes them). Thread t:
+        // row m = t / 16, columns 2 c, 2 c + 1 (c = t % 16) -- 4 bytes of the
+        // 16-byte operand chunk (8 columns) of each plane.
+        const int m = threadIdx.x >> 4, c = threadIdx.x & 15, gm = m0 + m;
+        float v[2];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float t = 0.f;
+        for (int i = 0; i < 2; ++i) {
+            float t = 0.f;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) t += red[w][m][8 * g + i];
-                const float4 sc4 = pe_scale[i >> 2], bi4 = pe_bias[i >> 2];
-                const float sc1 = (i & 3) == 0 ? sc4.x : (i & 3) == 1 ? sc4.y : (i & 3) == 2 ? sc4.z : sc4.w;
-                const float bi1 = (i & 3) == 0 ? bi4.x : (i & 3) == 1 ? bi4.y : (i & 3) == 2 ? bi4.z : bi4.w;
-                v[i] = t * sc1 + bi1;
+            for (int w = 0; w < kWaves; ++w) t += red[w][m][2 * c + i];
+            v[i] = t * (i ? pe_scale.y : pe_scale.x) + (i ? pe_bias.y : pe_bias.x);
+        }
+        apply_act<2>(v, act);
+        if (gm < M) {
+            if constexpr (sizeof(TY) == 4) {  // fp32 rows too when asked for
+                if (y) *reinterpret_cast<float2*>(y + (int64_t)gm * ldy + n0 + 2 * c) = make_float2(v[0], v[1]);
             }
-            apply_act<8>(v, act);
-            if (gm < M) {
-                if constexpr (sizeof(TY) == 4) {  // fp32 rows too when asked for
-                    if (y) {
-                        float* yr = y + (int64_t)gm * ldy + n0 + 8 * g;
-                        reinterpret_cast<float4*>(yr)[0] = make_float4(v[0], v[1], v[2], v[3]);
-                        reinterpret_cast<float4*>(yr)[1] = make_float4(v[4], v[5], v[6], v[7]);
-                    }
-                }
-                uint32_t pl[3][4];
-                split3_words(v, pl);
-                const int64_t Uo = N / 32, u = blockIdx.x;
-                const int hh = g >> 1, e = g & 1;
+            const uint32_t hi = pk_bf16(v[0], v[1]);
+            const float r0 = v[0] - bf_lo(hi), r1 = v[1] - bf_hi(hi);
+            const uint32_t lo = pk_bf16(r0, r1);
+            const uint32_t pl[3] = {hi, lo, pk_bf16(r0 - bf_lo(lo), r1 - bf_hi(lo))};
+            const int64_t Uo = N / 32, u = blockIdx.x;
+            const int g = c >> 2, hh = g >> 1, e = g & 1;
 #pragma unroll
-                for (int q = 0; q < 3; ++q) {
-                    const int64_t blk = (((int64_t)blockIdx.y * Uo + u) * 3 + q) * 2 + e;
-                    *reinterpret_cast<uint4*>(x3o + (blk * 64 + 32 * hh + m) * 8) =
-                        make_uint4(pl[q][0], pl[q][1], pl[q][2], pl[q][3]);
-                }
+            for (int q = 0; q < 3; ++q) {
+                const int64_t blk = (((int64_t)blockIdx.y * Uo + u) * 3 + q) * 2 + e;
+                *reinterpret_cast<uint32_t*>(x3o + (blk * 64 + 32 * hh + m) * 8 + 2 * (c & 3)) = pl[q];
             }
         }
         return;
