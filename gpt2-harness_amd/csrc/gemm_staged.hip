@@ -40,6 +40,17 @@ constexpr int kXcds = 8;
 //     with sched_barrier and an empty asm memory clobber so that neither the
 //     scheduler nor the IR passes regroup them. One barrier per step, placed
 //     before the last k16 group, whose fragments are already in registers.
+//   * k order: MFMA block b (0..3) of a k64 step takes, in lane (r, h), the 8
+//     columns 32 (b / 2) + 16 h + 8 (b % 2) .. + 7 of its row, for both
+//     operands (every staged tile sums the same column groups in the same
+//     order, so a bf16 result is the rounding of any tile's fp32 result). A
+//     lane's 16 consecutive bytes of a row then feed two MFMA blocks.
+//   * Weights in registers (WMW = 1, int8): each wavefront owns its weight
+//     rows, so it loads them straight from memory in that operand order (16
+//     bytes a lane, two k64 steps ahead) and widens them to bf16 one k16 group
+//     before their MFMAs; only the activations pass through LDS, which halves
+//     the LDS traffic of a step (GPT-2-XL shapes at M = 4096 with K = 1600:
+//     5-7% faster; at K = 6400 the 2 x 2 layout stays ahead).
 //   * Output through LDS: the accumulators are scaled, biased and converted,
 //     written to an XOR-swizzled LDS tile, then stored as whole 16-byte row
 //     chunks (a wavefront writes contiguous rows), which costs a few
@@ -94,21 +105,26 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
     int K, int kw) {
     static_assert(FMT == kW8 || FMT == kW4, "int8 or reference-layout int4 weights");
+    constexpr bool WD = WMW == 1 && FMT == kW8;  // weights straight into registers
     constexpr int NT = 256;
     constexpr int WNW = 4 / WMW;
     constexpr int WM = BM / WMW, WN = BN / WNW;
     constexpr int TMm = WM / 32, TNn = WN / 32;
-    constexpr int XS = BM * 128, WS = BN * 128, STAGE = XS + WS;
-    constexpr int XL = BM * 8 / NT, WL = BN * 4 / NT, NL = XL + WL;  // staging loads per thread per step
-    constexpr int NMF = TMm * TNn, NRD = TMm + TNn;                  // per k16
+    constexpr int XS = BM * 128, WS = WD ? 0 : BN * 128, STAGE = XS + WS;
+    constexpr int XL = BM * 8 / NT, WL = WD ? 0 : BN * 4 / NT, NL = XL + WL;  // staging loads per thread per step
+    constexpr int WLD = WD ? 2 * TNn : 0;                                     // direct weight loads per step
+    constexpr int NMF = TMm * TNn, NRD = TMm + (WD ? 0 : TNn);                // per k16
     static_assert((WMW == 1 || WMW == 2) && WM % 32 == 0 && WN % 32 == 0, "wave layout");
-    static_assert(XL * NT == BM * 8 && WL * NT == BN * 4, "staging split");
-    static_assert(NL <= 3 * NMF && NRD <= 2 * NMF, "staging ops and fragment reads per bundle");
+    static_assert(XL * NT == BM * 8 && WL * NT == (WD ? 0 : BN * 4), "staging split");
+    static_assert(NL <= 3 * NMF && NRD <= 2 * NMF && WLD <= NMF, "staging ops and fragment reads per bundle");
     constexpr int UNIT = 16 / (int)sizeof(TY);  // output elements per 16-byte chunk
     constexpr int UNITS = BN / UNIT;            // chunks per output row
-    constexpr int PASSES = (BM * BN * (int)sizeof(TY) + 2 * STAGE - 1) / (2 * STAGE);
+    constexpr int OUTB = BM * BN * (int)sizeof(TY);
+    // with the weights out of LDS the whole output tile fits in one pass
+    constexpr int SMEM = WD && OUTB > 2 * STAGE ? OUTB : 2 * STAGE;
+    constexpr int PASSES = (OUTB + SMEM - 1) / SMEM;
     static_assert(PASSES == 1 || (PASSES == 2 && WMW == 2), "output tile passes");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
     __shared__ __attribute__((aligned(16))) float sb_s[2][BN];  // the tile's scale and bias
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -167,15 +183,42 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
         }
     };
 
-    // fragments: lane (r, h) reads row base + r, chunk (2 kk + h) of a k16 step
+    // fragments: lane (r, h) reads row base + r, chunk 4 (kk / 2) + 2 h + kk % 2
+    // of k16 block kk (the k order above)
     const int r = lane & 31, h = lane >> 5;
     int fo[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) fo[kk] = r * 128 + (((2 * kk + h) ^ swz8(r)) * 16);
+    for (int kk = 0; kk < 4; ++kk) fo[kk] = r * 128 + (((4 * (kk >> 1) + 2 * h + (kk & 1)) ^ swz8(r)) * 16);
     bf16x8 FW[2][TNn], FX[2][TMm];
+    constexpr int FWR = WD ? 0 : TNn;  // weight fragments read from LDS
     auto fread = [&](const uint8_t* base, int kk, int set, int q) {
-        if (q < TNn) FW[set][q] = *reinterpret_cast<const bf16x8*>(base + XS + (wn + 32 * q) * 128 + fo[kk]);
-        else FX[set][q - TNn] = *reinterpret_cast<const bf16x8*>(base + (wm + 32 * (q - TNn)) * 128 + fo[kk]);
+        if (q < FWR) FW[set][q] = *reinterpret_cast<const bf16x8*>(base + XS + (wn + 32 * q) * 128 + fo[kk]);
+        else FX[set][q - FWR] = *reinterpret_cast<const bf16x8*>(base + (wm + 32 * (q - FWR)) * 128 + fo[kk]);
+    };
+    // WD: lane (r, h) of tile i holds bytes 32 j + 16 h .. + 15 (j = 0, 1) of
+    // the step's 64 columns of weight row n_blk + wn + 32 i + r (clamped), in
+    // two raw sets; block b widens 8 of them to bf16
+    u32x4 wr[2][WD ? TNn : 1][2];
+    uint32_t wdrow[TNn];
+#pragma unroll
+    for (int i = 0; i < TNn; ++i) wdrow[i] = (uint32_t)min(n_blk + wn + 32 * i + r, N - 1) * ldw1 + 16 * h;
+    auto wload = [&](int k0, int p, int q) {
+        if constexpr (WD) {
+            const int i = q >> 1, j = q & 1;
+            wr[p][i][j] =
+                *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + (k0 % kw) + wdrow[i] + 32 * j);
+        }
+    };
+    auto wfrag = [&](int p, int i, int b) {
+        if constexpr (WD) {
+            const u32x4 v = wr[p][i][b >> 1];
+            const uint32_t s0 = (b & 1) ? v.z : v.x, s1 = (b & 1) ? v.w : v.y;
+            const u32x4 t = {bf16x2_of_bytes_perm(s0, 0), bf16x2_of_bytes_perm(s0, 16),
+                             bf16x2_of_bytes_perm(s1, 0), bf16x2_of_bytes_perm(s1, 16)};
+            return __builtin_bit_cast(bf16x8, t);
+        } else {
+            return FW[0][0];
+        }
     };
     // D[n][m] = sum_k w[n][k] x[m][k]: result register q of lane (r, h) holds
     // n = 8 (q / 4) + 4 h + q % 4, m = r of its 32 x 32 tile
@@ -202,6 +245,10 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     for (int q = 0; q < NL; ++q) gload(kbase, 0, q);
 #pragma unroll
     for (int q = 0; q < NL; ++q) gload(kbase + min(1, nk - 1) * BK, 1, q);
+#pragma unroll
+    for (int q = 0; q < WLD; ++q) wload(kbase, 0, q);
+#pragma unroll
+    for (int q = 0; q < WLD; ++q) wload(kbase + min(1, nk - 1) * BK, 1, q);
     // the epilogue's per-column scale and bias, read once here, behind the
     // first tiles' loads (after the last k step they would cost another trip
     // to memory); columns past N repeat the last one
@@ -215,11 +262,18 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < NRD; ++q) fread(smem, 0, 0, q);
+    if constexpr (WD) {
+#pragma unroll
+        for (int i = 0; i < TNn; ++i) FW[0][i] = wfrag(0, i, 0);
+    }
 
     // Step s: MFMAs on buffer s % 2; stage s + 1 (register set (s + 1) % 2)
     // is stored to the other buffer over the first three k16 groups; stage
     // s + 2 is loaded into set s % 2 over all four. Past the last stage the
-    // loads repeat it (clamped k), which keeps the loop body one path.
+    // loads repeat it (clamped k), which keeps the loop body one path. WD:
+    // raw weight set p (this step's) is widened one k16 group ahead; by the
+    // end of the third group it is free and takes step s + 2's weights in the
+    // fourth, whose end widens block 0 of raw set p ^ 1 (step s + 1's).
     auto step = [&](int s, int p) {
         uint8_t* cur = smem + (s & 1) * STAGE;
         uint8_t* nxt = smem + ((s + 1) & 1) * STAGE;
@@ -235,6 +289,9 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
                 } else {  // more fragments than MFMAs: spread over the bundles
 #pragma unroll
                     for (int q = t * NRD / NMF; q < (t + 1) * NRD / NMF; ++q) fread(cur, kk + 1, set ^ 1, q);
+                }
+                if constexpr (WD) {
+                    if (t < TNn) FW[set ^ 1][t] = wfrag(p, t, kk + 1);
                 }
                 const int b = kk * NMF + t;
                 if ((b + 1) * NL / (3 * NMF) > b * NL / (3 * NMF)) lstore(nxt, p ^ 1, b * NL / (3 * NMF));
@@ -255,6 +312,13 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
             }
             const int b = 3 * NMF + t;
             if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
+            if constexpr (WD) {
+                if ((t + 1) * WLD / NMF > t * WLD / NMF) wload(k2, p, t * WLD / NMF);
+                if (t == NMF - 1) {
+#pragma unroll
+                    for (int i = 0; i < TNn; ++i) FW[0][i] = wfrag(p ^ 1, i, 0);
+                }
+            }
             asm volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
         }
