@@ -60,13 +60,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// Bijective workgroup -> tile map: the tiles are split into 8 contiguous
-// ranges, one per XCD (dispatch round-robins workgroups over the XCDs), and
-// each range is walked in groups of 4 row tiles so that concurrently running
+// Bijective tile index -> tile map: the tiles are split into 8 contiguous
+// ranges, one per XCD (dispatch round-robins workgroups over the XCDs, and a
+// persistent workgroup's later indices differ by a multiple of 8), and each
+// range is walked in groups of 4 row tiles so that concurrently running
 // workgroups of an XCD share x and weight panels in its L2.
-__device__ __forceinline__ void staged_tile_of(int& tm, int& tn, int tiles_m, int tiles_n) {
+__device__ __forceinline__ void staged_tile_of(int i, int& tm, int& tn, int tiles_m, int tiles_n) {
     const int total = tiles_m * tiles_n;
-    const int i = blockIdx.x;
     const int q = total / kXcds, r = total % kXcds;
     const int xcd = i % kXcds, local = i / kXcds;
     const int id = (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
@@ -124,13 +124,18 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     constexpr int SMEM = WD && OUTB > 2 * STAGE ? OUTB : 2 * STAGE;
     constexpr int PASSES = (OUTB + SMEM - 1) / SMEM;
     static_assert(PASSES == 1 || (PASSES == 2 && WMW == 2), "output tile passes");
+    // a persistent grid (several tiles a workgroup) only where the next tile's
+    // first loads fit beside the accumulators without spilling
+    constexpr bool PERSIST = NMF * 16 <= 192;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
     __shared__ __attribute__((aligned(16))) float sb_s[2][BN];  // the tile's scale and bias
 
+    // Tiles blockIdx.x, blockIdx.x + gridDim.x, ... (one unless the grid is
+    // persistent: fewer workgroups than tiles, one per CU)
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    int tm, tn;
-    staged_tile_of(tm, tn, tiles_m, tiles_n);
-    const int m_blk = tm * BM, n_blk = tn * BN;
+    int tile = blockIdx.x, tm, tn;
+    staged_tile_of(tile, tm, tn, tiles_m, tiles_n);
+    int m_blk = tm * BM, n_blk = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave / WNW) * WM, wn = (wave % WNW) * WN;
@@ -223,12 +228,6 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     // D[n][m] = sum_k w[n][k] x[m][k]: result register q of lane (r, h) holds
     // n = 8 (q / 4) + 4 h + q % 4, m = r of its 32 x 32 tile
     floatx16 acc[TNn][TMm];
-#pragma unroll
-    for (int i = 0; i < TNn; ++i)
-#pragma unroll
-        for (int j = 0; j < TMm; ++j)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
     auto mfma_set = [&](int set, int t) {
         const int i = t / TMm, j = t % TMm;
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FW[set][i], FX[set][j], acc[i][j], 0, 0, 0);
@@ -241,22 +240,35 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     const int nk = ((int)blockIdx.z + 1) * NK / (int)gridDim.z - s0;
     const int kbase = s0 * BK;
     const bool split = gridDim.z > 1;
+    // A tile's first stage and its epilogue's per-column scale and bias
+    // (columns past N repeat the last one), requested together; for the next
+    // tile of a persistent workgroup this runs before the current tile's
+    // epilogue, so those loads and the epilogue's stores overlap. The second
+    // stage follows after the epilogue (its registers would otherwise be live
+    // beside the accumulators).
+    constexpr int SBN = (BN + NT - 1) / NT;
+    float sbr[2][SBN];
+    auto begin_tile = [&]() {
 #pragma unroll
-    for (int q = 0; q < NL; ++q) gload(kbase, 0, q);
+        for (int q = 0; q < NL; ++q) gload(kbase, 0, q);
+#pragma unroll
+        for (int q = 0; q < WLD; ++q) wload(kbase, 0, q);
+#pragma unroll
+        for (int c = 0; c < SBN; ++c) {
+            const int n = min(n_blk + min(tid + NT * c, BN - 1), N - 1);
+            sbr[0][c] = split ? 1.f : scale[n];
+            sbr[1][c] = (bias && !split) ? bias[n] : 0.f;
+        }
+    };
+    begin_tile();
+    for (;;) {  // the workgroup's tiles
 #pragma unroll
     for (int q = 0; q < NL; ++q) gload(kbase + min(1, nk - 1) * BK, 1, q);
 #pragma unroll
-    for (int q = 0; q < WLD; ++q) wload(kbase, 0, q);
-#pragma unroll
     for (int q = 0; q < WLD; ++q) wload(kbase + min(1, nk - 1) * BK, 1, q);
-    // the epilogue's per-column scale and bias, read once here, behind the
-    // first tiles' loads (after the last k step they would cost another trip
-    // to memory); columns past N repeat the last one
-    for (int c = tid; c < BN; c += NT) {
-        const int n = min(n_blk + c, N - 1);
-        sb_s[0][c] = split ? 1.f : scale[n];
-        sb_s[1][c] = (bias && !split) ? bias[n] : 0.f;
-    }
+#pragma unroll
+    for (int c = 0; c < SBN; ++c)
+        if (tid + NT * c < BN) sb_s[0][tid + NT * c] = sbr[0][c], sb_s[1][tid + NT * c] = sbr[1][c];
 #pragma unroll
     for (int q = 0; q < NL; ++q) lstore(smem, 0, q);
     __syncthreads();
@@ -266,6 +278,12 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
 #pragma unroll
         for (int i = 0; i < TNn; ++i) FW[0][i] = wfrag(0, i, 0);
     }
+#pragma unroll
+    for (int i = 0; i < TNn; ++i)
+#pragma unroll
+        for (int j = 0; j < TMm; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
 
     // Step s: MFMAs on buffer s % 2; stage s + 1 (register set (s + 1) % 2)
     // is stored to the other buffer over the first three k16 groups; stage
@@ -330,6 +348,20 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     }
     if (s < nk) step(s, 0);
     __syncthreads();
+    // the next tile's first loads, then this tile's epilogue
+    const int em_blk = m_blk, en_blk = n_blk;
+    tile += gridDim.x;
+    const bool more = PERSIST && tile < tiles_m * tiles_n;
+    if (more) {
+        staged_tile_of(tile, tm, tn, tiles_m, tiles_n);
+        m_blk = tm * BM;
+        n_blk = tn * BN;
+        if constexpr (WD) {
+#pragma unroll
+            for (int i = 0; i < TNn; ++i) wdrow[i] = (uint32_t)min(n_blk + wn + 32 * i + r, N - 1) * ldw1 + 16 * h;
+        }
+        begin_tile();
+    }
 
     // epilogue: scale, bias, convert; LDS tile [rows of the pass][UNITS chunks],
     // chunk u of row m at position u ^ (m % UNITS)
@@ -375,7 +407,7 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
         for (int c = 0; c < CH; ++c) {
             const int idx = tid + NT * c;
             const int ml = idx / UNITS, u = idx % UNITS;
-            const int m = m_blk + pass * ROWS + ml, n = n_blk + u * UNIT;
+            const int m = em_blk + pass * ROWS + ml, n = en_blk + u * UNIT;
             const u32x4 v = *reinterpret_cast<const u32x4*>(smem + ml * ROW_BYTES + ((u ^ (ml & (UNITS - 1))) * 16));
             // nontemporal: the output is written once and read by a later kernel
             if (m < M && n < N)
@@ -384,12 +416,25 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
         }
         if (pass + 1 < PASSES) __syncthreads();
     }
+    if (!more) break;
+    __syncthreads();  // the epilogue's LDS reads are done before the next tile's stores
+    }
+}
+
+// The kernel's PERSIST condition, on the host: tiles whose accumulators leave
+// room for the next tile's first loads run on a persistent grid of one
+// workgroup per tile slot (256 CUs x the workgroups a CU holds).
+template <int BM, int BN, int WMW>
+constexpr bool staged_persist() {
+    return (BM / WMW / 32) * (BN * WMW / 4 / 32) * 16 <= 192;
 }
 
 template <int BM, int BN, int WMW, int FMT, typename TY>
 int run_staged(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY>), dim3((unsigned)tiles), dim3(256), 0, a.stream,
+    const int64_t slots = 256 * (BM * BN <= 128 * 128 ? 2 : 1);
+    const int64_t grid = staged_persist<BM, BN, WMW>() ? std::min(tiles, slots) : tiles;
+    hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY>), dim3((unsigned)grid), dim3(256), 0, a.stream,
                        static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, static_cast<TY*>(a.y),
                        a.ldy, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
     return launch_status();
