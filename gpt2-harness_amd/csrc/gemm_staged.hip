@@ -459,13 +459,15 @@ bool staged_supported_impl(const LinearArgs& a) {
 // duration of one round, modelled as step_us per k64 step plus a fixed term
 // (prologue, epilogue, launch), both least-squares fits to MI355X timings of
 // every tile at the GPT-2-XL Linear shapes with M = 256 / 1024 / 4096 (bf16
-// output, operands rotated over six copies; within 12% of every timing but
-// one, and choosing the fastest tile or one within 1% of it at all twelve).
+// output, operands rotated over six copies, the current kernels: register-fed
+// weights in the WMW = 1 tiles, persistent grids; within 16% of every timing
+// but the 128x128 tile's at M = 4096, up to 26%), which picks the fastest
+// tile at all twelve.
 int staged_choice(int64_t M, int64_t N, int64_t K, bool bf16_out) {
     struct Opt { int bm, bn, per_cu; double step_us, fixed_us; };
     // 3-5: the WMW = 1 tiles (bf16 output only)
-    static const Opt opts[] = {{256, 256, 1, 1.180, 14.14}, {256, 128, 1, 0.704, 7.60}, {128, 128, 2, 1.033, 2.49},
-                               {224, 256, 1, 1.072, 12.94}, {160, 256, 1, 0.880, 9.58}, {224, 128, 1, 0.739, 5.83}};
+    static const Opt opts[] = {{256, 256, 1, 1.218, 13.39}, {256, 128, 1, 0.716, 8.16}, {128, 128, 2, 1.029, 3.29},
+                               {224, 256, 1, 1.029, 12.40}, {160, 256, 1, 0.862, 9.06}, {224, 128, 1, 0.674, 6.92}};
     const double nk = (double)(K / BK);
     int best = 0;
     double best_t = 1e30;
