@@ -12,7 +12,9 @@ the K timed steps (HIP events on the launch stream; one step is one replay
 of a captured HIP graph of the 48 launches).
 
 ``roofline`` also carries a 1 GiB device copy timed in the same run as the
-measured-achievable HBM rate. ``detail`` adds the other configurations:
+measured-achievable HBM rate; ``detail["platform_bf16_gemm"]`` is the
+matching measured-achievable bf16 matrix-core rate (an 8192^3 platform GEMM).
+``detail`` adds the other configurations:
 M = 4 / 16 at the same shapes, GPT-2-XL layer shapes at M = 1 (per shape),
 the int8->bf16 MFMA GEMM at GPT-2-XL shapes with M = 256 / 1024 / 4096, the
 quantize kernels at GPT-2-XL shapes (a graph of calls over cold weight
@@ -219,6 +221,32 @@ def hbm_stream_section(dev, reps=10):
         ts.append(a.elapsed_time(b))
     del src, dst
     return {"copy": {"GB/s": 8 * n / (statistics.median(ts) * 1e-3) / 1e9, "bytes": 8 * n}}
+
+
+def mfma_platform_section(dev, n=8192, reps=10):
+    """Measured-achievable bf16 matrix-core rate beside the 2.5 PFLOP/s
+    datasheet figure: the platform GEMM (torch.matmul -> hipBLASLt) on an
+    n x n x n bf16 product, the median of `reps` launches between HIP events.
+    Under a full-chip matrix load the MI355X clock settles well below its 2.4 GHz
+    peak, so this, not the datasheet, is the ceiling the GEMM rows sit under."""
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(3)
+    a = torch.randn(n, n, generator=gen, device=dev).bfloat16()
+    b = torch.randn(n, n, generator=gen, device=dev).bfloat16()
+    c = torch.matmul(a, b)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.matmul(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    del a, b, c
+    tf = 2 * n ** 3 / (statistics.median(ts) * 1e-3) / 1e12
+    return {"shape": f"{n}x{n}x{n} bf16", "TFLOP/s": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS}
 
 
 def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
@@ -764,7 +792,8 @@ def main() -> int:
     if args.only == "gemm4096":
         print(json.dumps({"int8": gemm_section(4096, XL_KN, dev),
                           "int4": gemm_section(4096, XL_KN, dev, fmt="int4"),
-                          "int4_g128": gemm_section(4096, XL_KN, dev, fmt="int4_g128")}))
+                          "int4_g128": gemm_section(4096, XL_KN, dev, fmt="int4_g128"),
+                          "platform_bf16_gemm": mfma_platform_section(dev)}))
         return 0
     if args.only == "gemm_g128":
         print(json.dumps({f"M{M}": gemm_section(M, XL_KN, dev, fmt="int4_g128") for M in (256, 1024, 4096)}))
@@ -802,6 +831,7 @@ def main() -> int:
         for M in (256, 1024, 4096):
             detail[f"gemm_xl_g128_M{M}"] = gemm_section(M, XL_KN, dev, fmt="int4_g128")
         detail["gemm_xl_int4_M4096"] = gemm_section(4096, XL_KN, dev, fmt="int4")
+        detail["platform_bf16_gemm"] = mfma_platform_section(dev)
         print("# gemm done", file=sys.stderr, flush=True)
         detail["quantize_xl"] = quantize_section(dev)
         detail["decode_gpt2_small_int8"] = decode_section(dev)
