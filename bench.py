@@ -252,7 +252,8 @@ def mfma_platform_section(dev, n=8192, reps=10):
 def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
     """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws; fmt="int4": the reference
     nibble layout, tiq_linear_w4; fmt="int4_g128": the group-wise int4 GEMM,
-    tiq_linear_w4g, group 128) per shape: `reps` launches back
+    tiq_linear_w4g_ws, group 128, split over K where the tiles are few) per
+    shape: `reps` launches back
     to back between one HIP event pair, rotating over `copies` independent
     (activation, weight, output) sets (at M = 4096 on 1600 x 6400 the eight
     sets hold 600 MB, past the 256 MB Infinity Cache), so no launch finds its
@@ -309,8 +310,8 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8"):
                 rc = L.tiq_linear_w4(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1,
                                      N, st)
             else:
-                rc = L.tiq_linear_w4g(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), 128, None, N, y.data_ptr(),
-                                      1, N, st)
+                rc = L.tiq_linear_w4g_ws(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), 128, None, N,
+                                         y.data_ptr(), 1, N, ws.data_ptr(), n_ws, st)
             if rc:
                 raise RuntimeError(f"{fmt} GEMM status {rc}")
 

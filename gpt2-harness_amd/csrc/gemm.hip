@@ -22,6 +22,7 @@
 //     weight panel they share stay in that XCD's L2;
 //   * the epilogue multiplies the fp32 accumulators by the per-channel scale
 //     and adds the bias, exactly once per output.
+#include <algorithm>
 #include <cstdlib>
 
 #include "tiq_internal.hpp"
@@ -93,6 +94,10 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chu
 // k % kw): K = 3 kw for fp32 activations split into three bf16 planes laid side
 // by side (x = hi + lo + lo2, each product exact), kw = K otherwise. Groups
 // restart with every plane.
+// Split over K (gridDim.z = S > 1, group-wise int4 with kw = K only): workgroup
+// z takes the whole groups [z G / S, (z + 1) G / S) of the G groups and writes
+// its fp32 sums (groups already scaled) to slice z of y, without bias; the
+// split-K reduction adds the slices in order and the bias.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int OCC, int FMT, typename TY>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
@@ -166,6 +171,14 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
 
     const int frag_row = lane & 31, frag_c = lane >> 5;  // row in the tile, chunk within a k16 step
     const int nk = K / BK;
+    // this workgroup's k steps [s_begin, s_end): all of K, or whole groups of a split
+    int s_begin = 0, s_end = nk;
+    if (GROUPED && gridDim.z > 1) {
+        const int gsteps = group / BK, G = (nk + gsteps - 1) / gsteps;
+        s_begin = (int)blockIdx.z * G / (int)gridDim.z * gsteps;
+        s_end = min(((int)blockIdx.z + 1) * G / (int)gridDim.z * gsteps, nk);
+    }
+    TY* const yz = y + (int64_t)blockIdx.z * M * ldy;
     uint4 ra[A_VEC], rb[B_VEC];
 
 #define TIQ_LOAD_TILES(k0)                                                                         \
@@ -200,12 +213,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
         }                                                                                          \
     }
 
-    TIQ_LOAD_TILES(0)
+    TIQ_LOAD_TILES(s_begin * BK)
     TIQ_STORE_TILES(0)
     __syncthreads();
-    for (int s = 0; s < nk; ++s) {
-        const int buf = s & 1;
-        const int kn = (s + 1 < nk) ? (s + 1) * BK : s * BK;
+    for (int s = s_begin; s < s_end; ++s) {
+        const int buf = (s - s_begin) & 1;
+        const int kn = (s + 1 < s_end) ? (s + 1) * BK : s * BK;
         TIQ_LOAD_TILES(kn)
         const int sk = (s * BK) % kw;  // the step's first weight column
         if constexpr (GROUPED) {
@@ -242,7 +255,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
                 }
         }
         if constexpr (GROUPED) {
-            if ((sk + BK) % group == 0 || sk + BK == kw || s + 1 == nk) {  // the group's last step
+            if ((sk + BK) % group == 0 || sk + BK == kw || s + 1 == s_end) {  // the group's last step
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     const float sg = f16_bits_to_f32(gsc[j]);
@@ -272,8 +285,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
                 const int m = m_blk + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < M) {
                     const float v = fmaf(acc[i][j][r], s, b);
-                    if constexpr (sizeof(TY) == 4) y[(int64_t)m * ldy + n] = v;
-                    else y[(int64_t)m * ldy + n] = f32_to_bf16_bits(v);
+                    if constexpr (sizeof(TY) == 4) yz[(int64_t)m * ldy + n] = v;
+                    else yz[(int64_t)m * ldy + n] = f32_to_bf16_bits(v);
                 }
             }
         }
@@ -339,5 +352,27 @@ int launch_gemm_tile(const LinearArgs& a, int tile) {
 }
 
 int launch_gemm(const LinearArgs& a) { return launch_gemm_tile(a, 0); }
+
+int launch_gemm_w4g_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
+    if (a.fmt != kW4G || a.x_dtype != TIQ_BF16 || (a.kw && a.kw != a.K) || !gemm_supported(a))
+        return TIQ_EUNSUPPORTED;
+    // the reduction's 16-byte accesses of y and the bias
+    const int unit = a.y_dtype == TIQ_F32 ? 4 : 8;
+    if (a.N % unit != 0 || a.ldy % unit != 0 || !aligned(a.y, 16) || (a.bias && !aligned(a.bias, 16)))
+        return TIQ_EUNSUPPORTED;
+    const int64_t gsteps = a.group / BK, G = (a.K / BK + gsteps - 1) / gsteps;
+    const int64_t S = std::min<int64_t>(staged_splits(a.M, a.N, a.K), G);  // at least one group a split
+    if (S <= 1) return TIQ_EUNSUPPORTED;
+    const size_t need = (size_t)(S * a.M * a.N) * 4;
+    if (!ws || ws_bytes < need || !aligned(ws, 16) || a.M * a.N * S > 0x7fffffffLL) return TIQ_EUNSUPPORTED;
+    float* part = static_cast<float*>(ws);
+    const int64_t tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+    hipLaunchKernelGGL((gemm32_kernel<128, 128, 2, 2, 2, kW4G, float>), dim3((unsigned)tiles, 1, (unsigned)S),
+                       dim3(256), 0, a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale,
+                       a.scale16, a.group, nullptr, part, (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)a.K);
+    const int rc = launch_status();
+    if (rc != TIQ_OK) return rc;
+    return launch_splitk_reduce(a, part, S, nullptr);
+}
 
 }  // namespace tiq

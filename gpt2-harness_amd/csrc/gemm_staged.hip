@@ -483,7 +483,8 @@ int staged_choice(int64_t M, int64_t N, int64_t K, bool bf16_out) {
 }
 
 // The end of a split-K product: y[m][n] = scale[n] * sum_z part[z][m][n] +
-// bias[n], the S slices summed in a fixed order; 4 consecutive outputs a thread.
+// bias[n] (scale 1 when null: the group-wise slices are scaled already), the
+// S slices summed in a fixed order; 4 consecutive outputs a thread.
 template <typename TY>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
                                                             const float* __restrict__ scale,
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
             a.w = use ? a.w + v[j].w : a.w;
         }
     }
-    const float4 sc = *reinterpret_cast<const float4*>(scale + n);
+    const float4 sc = scale ? *reinterpret_cast<const float4*>(scale + n) : make_float4(1.f, 1.f, 1.f, 1.f);
     float4 bi = make_float4(0.f, 0.f, 0.f, 0.f);
     if (bias) bi = *reinterpret_cast<const float4*>(bias + n);
     const float o0 = fmaf(a.x, sc.x, bi.x), o1 = fmaf(a.y, sc.y, bi.y);
@@ -589,14 +590,18 @@ int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
                        (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K));
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
+    return launch_splitk_reduce(a, part, S, a.scale);
+}
+
+int launch_splitk_reduce(const LinearArgs& a, const float* part, int64_t S, const float* scale) {
     const int64_t quads = a.M * a.N / 4;
     const dim3 grid((unsigned)((quads + 255) / 256));
     if (a.y_dtype == TIQ_F32)
         hipLaunchKernelGGL(splitk_reduce_kernel<float>, grid, dim3(256), 0, a.stream, part, (int)S, (int)a.M,
-                           (int)a.N, a.scale, a.bias, static_cast<float*>(a.y), a.ldy);
+                           (int)a.N, scale, a.bias, static_cast<float*>(a.y), a.ldy);
     else
         hipLaunchKernelGGL(splitk_reduce_kernel<uint16_t>, grid, dim3(256), 0, a.stream, part, (int)S, (int)a.M,
-                           (int)a.N, a.scale, a.bias, static_cast<uint16_t*>(a.y), a.ldy);
+                           (int)a.N, scale, a.bias, static_cast<uint16_t*>(a.y), a.ldy);
     return launch_status();
 }
 

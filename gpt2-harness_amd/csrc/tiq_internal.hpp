@@ -98,5 +98,12 @@ int launch_staged_gemm(const LinearArgs& a, int choice);
 int64_t staged_splits(int64_t M, int64_t N, int64_t K);
 size_t staged_split_workspace(int64_t M, int64_t N, int64_t K);
 int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes);
+// y = scale * (sum of the S fp32 slices part[S][M][N], in slice order) + bias
+// (scale null: 1), with a's output, bias and stream; N % 4 == 0.
+int launch_splitk_reduce(const LinearArgs& a, const float* part, int64_t S, const float* scale);
+// Group-wise int4 with bf16 activations split over K (whole groups a split)
+// when the 128 x 128 tiles are too few to fill the GPU; the partial slices in
+// ws (staged_split_workspace bytes). TIQ_EUNSUPPORTED: no split planned.
+int launch_gemm_w4g_split(const LinearArgs& a, void* ws, size_t ws_bytes);
 
 }  // namespace tiq

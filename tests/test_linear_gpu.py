@@ -356,6 +356,38 @@ def test_gemm_w4_groupwise_prefill(dev, c_oracle, KN, M):
     _run_w4g(dev, c_oracle, *KN, M, 128, seed=M + KN[0], bias=M != 1024)
 
 
+# Group-wise int4 with bf16 rows and the GEMM workspace: products with few
+# 128 x 128 tiles split over K, whole groups a split, the fp32 slices summed in
+# order (6400x1600 at M = 256: 26 tiles, eight splits of 6-7 groups; group
+# widths of one, three and sixteen k steps; partial tiles). The result is held
+# to the oracle's bound, and the bf16 output to the rounding of the fp32 one.
+@pytest.mark.parametrize("K,N,M,group", [(6400, 1600, 256, 128), (1600, 4800, 256, 128), (1600, 1600, 1024, 128),
+                                         (6400, 1600, 1024, 128), (1600, 4800, 300, 64), (1600, 1600, 257, 192),
+                                         (3072, 768, 129, 1024)])
+def test_gemm_w4_groupwise_split_k(dev, c_oracle, K, N, M, group):
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, M + group + K, torch.bfloat16)
+    packed, s16 = c_oracle.quantize_groupwise_int4(w.numpy(), group)
+    pd, sd = torch.from_numpy(packed).to(dev), torch.from_numpy(s16.view(np.uint16).copy()).to(dev)
+    bd, xd = b.to(dev), x.to(dev)
+    n_ws = int(L.tiq_gemm_w8_workspace(_lib.BF16, M, K, N))
+    assert n_ws > 0, "the shape should plan a split"
+    ws = torch.empty(n_ws, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for dt in (torch.float32, torch.bfloat16):
+        y = torch.full((M, N), 7.0, device=dev, dtype=dt)
+        rc = L.tiq_linear_w4g_ws(xd.data_ptr(), _lib.BF16, M, K, K, pd.data_ptr(), sd.data_ptr(), group, bd.data_ptr(),
+                                 N, y.data_ptr(), _lib.dtype_code(dt), N, ws.data_ptr(), n_ws, st)
+        _lib.check(rc, "tiq_linear_w4g_ws")
+        torch.cuda.synchronize()
+        outs[dt] = y.cpu()
+    w_hat = torch.from_numpy(OQ.dequantize_groupwise_int4(packed, s16, K, group))
+    ok, err, bound = OL.within_tolerance(outs[torch.float32], OL.linear_ref(x, w_hat, b))
+    assert ok, f"w4g split M={M} K={K} N={N} group={group}: max err {err:.3g} > {bound:.3g}"
+    assert torch.equal(outs[torch.bfloat16], outs[torch.float32].to(torch.bfloat16)), "bf16 not RNE of fp32"
+
+
 # other group widths (multiples of the 64-column k step, a last group of one
 # step), partial row and column tiles, and a width the GEMM does not take
 # (32: the vector-ALU kernel serves it)
