@@ -12,7 +12,9 @@ the K timed steps (HIP events on the launch stream; one step is one replay
 of a captured HIP graph of the 48 launches).
 
 ``roofline`` also carries a 1 GiB device copy timed in the same run as the
-measured-achievable HBM rate; ``detail["platform_bf16_gemm"]`` is the
+measured-achievable HBM rate and the per-launch floor of a HIP graph (an
+all-but-empty kernel, and this library's GEMV on a 4 KB matrix, back to back:
+the fixed cost every decode GEMV launch pays); ``detail["platform_bf16_gemm"]`` is the
 matching measured-achievable bf16 matrix-core rate (an 8192^3 platform GEMM).
 ``detail`` adds the other configurations:
 M = 4 / 16 at the same shapes, GPT-2-XL layer shapes at M = 1 (per shape),
@@ -221,6 +223,56 @@ def hbm_stream_section(dev, reps=10):
         ts.append(a.elapsed_time(b))
     del src, dst
     return {"copy": {"GB/s": 8 * n / (statistics.median(ts) * 1e-3) / 1e9, "bytes": 8 * n}}
+
+
+def launch_floor_section(dev, launches=240, reps=5):
+    """What one launch costs inside a HIP graph, the floor a decode GEMV sits
+    on: back-to-back graph replays of `launches` launches of (a) a one-element
+    torch fill (an all-but-empty kernel) and (b) this library's M = 1 GEMV on
+    a 64 x 64 int8 matrix (its own argument path, one 4 KB read); HIP events
+    around each replay, the median over `reps` replays, per launch."""
+    import torch
+
+    import gpt2_harness_amd as g
+    from gpt2_harness_amd import _lib
+
+    L = _lib.lib()
+    t = torch.zeros(1, device=dev)
+    q, sc = g.quantize_tensor(torch.randn(64, 64, device=dev) * 0.02, 8)
+    sc = sc.reshape(-1).contiguous()
+    x = torch.randn(1, 64, device=dev).to(torch.bfloat16)
+    y = torch.empty(1, 64, device=dev, dtype=torch.bfloat16)
+
+    def gemv():
+        rc = L.tiq_linear_w8(x.data_ptr(), 1, 1, 64, 64, q.data_ptr(), sc.data_ptr(), None, 64, y.data_ptr(), 1, 64,
+                             torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"tiq_linear_w8 status {rc}")
+
+    out = {}
+    cases = (("torch_fill_1_element", lambda i: t.fill_(1.0)), ("tiq_linear_w8_64x64_M1", lambda i: gemv()))
+    for name, fn in cases:
+        s_cap = torch.cuda.Stream()
+        with torch.cuda.stream(s_cap):
+            fn(0)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s_cap):
+                for i in range(launches):
+                    fn(i)
+        gr.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            gr.replay()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / launches)
+        out[name] = {"us_per_launch": statistics.median(ts), "launches_per_graph": launches}
+        del gr
+    return out
 
 
 def mfma_platform_section(dev, n=8192, reps=10):
@@ -755,7 +807,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
-    ap.add_argument("--only", choices=["headline", "gemv", "gemv_xl", "gemm", "gemm4096", "gemm_g128", "quantize", "decode", "decode_xl", "eval", "schemes", "copy"],
+    ap.add_argument("--only", choices=["headline", "gemv", "gemv_xl", "gemm", "gemm4096", "gemm_g128", "quantize", "decode", "decode_xl", "eval", "schemes", "copy", "floor"],
                     default=None,
                     help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
                          "used to calibrate the HBM byte counters")
@@ -779,6 +831,9 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 5}))
+        return 0
+    if args.only == "floor":
+        print(json.dumps(launch_floor_section(dev)))
         return 0
     if args.only == "headline":  # the timed headline replays alone (what its kernel profile covers)
         h = gemv_section(1, SMALL_KN, 12, 6, args.steps, args.warmup, dev, seed=0, per_shape=False)
@@ -826,6 +881,7 @@ def main() -> int:
         detail["gemv_xl_M1"] = gemv_section(1, XL_KN, 12, 3, 10, 2, dev, seed=7)
         print("# gemv detail done", file=sys.stderr, flush=True)
     hbm = hbm_stream_section(dev)
+    floor = launch_floor_section(dev)
     if not args.quick and args.only is None:
         for M in (256, 1024, 4096):
             detail[f"gemm_xl_M{M}"] = gemm_section(M, XL_KN, dev)
@@ -888,9 +944,10 @@ def main() -> int:
             "avg_launch_us": head["avg_launch_us"],
             "measured_hbm_GBs": {k: v["GB/s"] for k, v in hbm.items()},
             "frac_of_measured_copy": achieved / hbm["copy"]["GB/s"],
+            "graph_launch_floor_us": {k: v["us_per_launch"] for k, v in floor.items()},
         },
         "cpu_baseline": cpu,
-        "detail": {"gemv_small_M1": head, "hbm_measured": hbm, **detail},
+        "detail": {"gemv_small_M1": head, "hbm_measured": hbm, "launch_floor": floor, **detail},
     }
     print(json.dumps(line))
     return 0
