@@ -24,6 +24,7 @@
 //     and adds the bias, exactly once per output.
 #include <algorithm>
 #include <cstdlib>
+#include <utility>
 
 #include "tiq_internal.hpp"
 
@@ -32,6 +33,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 bytes in flight, as plain loads
 
 constexpr int BK = 64;
 constexpr int kXcds = 8;
@@ -98,6 +100,13 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chu
 // z takes the whole groups [z G / S, (z + 1) G / S) of the G groups and writes
 // its fp32 sums (groups already scaled) to slice z of y, without bias; the
 // split-K reduction adds the slices in order and the bias.
+// f(integral_constant<int, J>) for J = 0 .. sizeof...(J) - 1, in order: a
+// register array indexed by J stays in registers whatever the loop passes do.
+template <int... J, typename F>
+__device__ __forceinline__ void for_each_index(std::integer_sequence<int, J...>, F&& f) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int OCC, int FMT, typename TY>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
@@ -156,17 +165,14 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     // group-wise scales: this lane's output columns (one per 32-wide tile
-    // column j, clamped for a partial tile), the group's partial sums, and the
-    // group's scales, requested at the group's first step
+    // column j, clamped for a partial tile) and the group's partial sums
     const int ngroups = GROUPED ? (kw + group - 1) / group : 1;
     int64_t srow[TN];
     floatx16 part[GROUPED ? TM : 1][GROUPED ? TN : 1];
-    uint16_t gsc[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = n_blk + wn + j * 32 + (lane & 31);
         srow[j] = (int64_t)(n < N ? n : N - 1) * ngroups;
-        gsc[j] = 0;
     }
 
     const int frag_row = lane & 31, frag_c = lane >> 5;  // row in the tile, chunk within a k16 step
@@ -179,59 +185,74 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
         s_end = min(((int)blockIdx.z + 1) * G / (int)gridDim.z * gsteps, nk);
     }
     TY* const yz = y + (int64_t)blockIdx.z * M * ldy;
-    uint4 ra[A_VEC], rb[B_VEC];
+    // A ring of NS register sets: step t's tiles (and, group-wise, its
+    // group's scales) are loaded into set (t - s_begin) % NS during step
+    // t - NS + 1 and go to LDS at the end of step t - 1, so each load has
+    // NS - 2 steps of MFMA work to arrive behind (a 128 x 128 tile's step is
+    // short against a trip to HBM). No load sits under a branch inside the
+    // unrolled ring: the compiler's wait counts stay exact only where every
+    // path issues the same loads.
+    constexpr int NS = (OCC >= 2 || BM * BN > 128 * 128) ? 3 : 4;  // within the register budget
+    u32x4 ra[NS][A_VEC], rb[NS][B_VEC];
+    uint16_t rs[NS][GROUPED ? TN : 1];
+    auto load_tiles = [&](auto set_c, int step) __attribute__((always_inline)) {
+        constexpr int set = decltype(set_c)::value;
+        const int k0 = min(step, s_end - 1) * BK;  // past the end: repeat the last step
+        const int kb = (FMT == kW8) ? k0 % kw : (k0 % kw) / 2;
+#pragma unroll
+        for (int j = 0; j < A_VEC; ++j) ra[set][j] = *reinterpret_cast<const u32x4*>(x + a_off[j] + k0);
+#pragma unroll
+        for (int j = 0; j < B_VEC; ++j) rb[set][j] = *reinterpret_cast<const u32x4*>(w + b_off[j] + kb);
+        if constexpr (GROUPED) {
+            const int g = (k0 % kw) / group;
+#pragma unroll
+            for (int jj = 0; jj < TN; ++jj) rs[set][jj] = scale16[srow[jj] + g];
+        }
+    };
+    auto store_tiles = [&](auto set_c, int buf) __attribute__((always_inline)) {
+        constexpr int set = decltype(set_c)::value;
+#pragma unroll
+        for (int j = 0; j < A_VEC; ++j) *reinterpret_cast<u32x4*>(&As[buf][a_dst[j]]) = ra[set][j];
+#pragma unroll
+        for (int j = 0; j < B_VEC; ++j) {
+            uint16_t* base = &Bs[buf][0];
+            const int r_ = b_row[j], c_ = b_c8[j];
+            const u32x4 v = rb[set][j];
+            if constexpr (FMT == kW8) {
+                *reinterpret_cast<uint4*>(base + swz(r_, c_)) =
+                    make_uint4(bf16x2_of_bytes(v.x, 0), bf16x2_of_bytes(v.x, 16), bf16x2_of_bytes(v.y, 0),
+                               bf16x2_of_bytes(v.y, 16));
+                *reinterpret_cast<uint4*>(base + swz(r_, c_ + 1)) =
+                    make_uint4(bf16x2_of_bytes(v.z, 0), bf16x2_of_bytes(v.z, 16), bf16x2_of_bytes(v.w, 0),
+                               bf16x2_of_bytes(v.w, 16));
+            } else {
+                const uint32_t d_[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<uint4*>(base + swz(r_, c_ + q)) =
+                        make_uint4(bf16x2_of_nibbles(d_[q], 0), bf16x2_of_nibbles(d_[q], 8),
+                                   bf16x2_of_nibbles(d_[q], 16), bf16x2_of_nibbles(d_[q], 24));
+            }
+        }
+    };
 
-#define TIQ_LOAD_TILES(k0)                                                                         \
-    {                                                                                              \
-        const int kb_ = (FMT == kW8) ? (k0) % kw : ((k0) % kw) / 2;                                \
-        _Pragma("unroll") for (int j = 0; j < A_VEC; ++j) ra[j] =                                  \
-            *reinterpret_cast<const uint4*>(x + a_off[j] + (k0));                                  \
-        _Pragma("unroll") for (int j = 0; j < B_VEC; ++j) rb[j] =                                  \
-            *reinterpret_cast<const uint4*>(w + b_off[j] + kb_);                                   \
-    }
-#define TIQ_STORE_TILES(buf)                                                                       \
-    {                                                                                              \
-        _Pragma("unroll") for (int j = 0; j < A_VEC; ++j)                                          \
-            *reinterpret_cast<uint4*>(&As[buf][a_dst[j]]) = ra[j];                                 \
-        _Pragma("unroll") for (int j = 0; j < B_VEC; ++j) {                                        \
-            uint16_t* base = &Bs[buf][0];                                                          \
-            const int r_ = b_row[j], c_ = b_c8[j];                                                 \
-            if (FMT == kW8) {                                                                      \
-                *reinterpret_cast<uint4*>(base + swz(r_, c_)) =                                    \
-                    make_uint4(bf16x2_of_bytes(rb[j].x, 0), bf16x2_of_bytes(rb[j].x, 16),          \
-                               bf16x2_of_bytes(rb[j].y, 0), bf16x2_of_bytes(rb[j].y, 16));         \
-                *reinterpret_cast<uint4*>(base + swz(r_, c_ + 1)) =                                \
-                    make_uint4(bf16x2_of_bytes(rb[j].z, 0), bf16x2_of_bytes(rb[j].z, 16),          \
-                               bf16x2_of_bytes(rb[j].w, 0), bf16x2_of_bytes(rb[j].w, 16));         \
-            } else {                                                                               \
-                const uint32_t d_[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};                       \
-                _Pragma("unroll") for (int q = 0; q < 4; ++q)                                      \
-                    *reinterpret_cast<uint4*>(base + swz(r_, c_ + q)) =                            \
-                        make_uint4(bf16x2_of_nibbles(d_[q], 0), bf16x2_of_nibbles(d_[q], 8),       \
-                                   bf16x2_of_nibbles(d_[q], 16), bf16x2_of_nibbles(d_[q], 24));    \
-            }                                                                                      \
-        }                                                                                          \
-    }
-
-    TIQ_LOAD_TILES(s_begin * BK)
-    TIQ_STORE_TILES(0)
-    __syncthreads();
-    for (int s = s_begin; s < s_end; ++s) {
+    // step s (register set j = (s - s_begin) % NS): the loads of step
+    // s + NS - 1 go out into set (j + NS - 1) % NS, whose tiles (step s - 1)
+    // are in LDS already; step s's MFMAs run on LDS buffer (s - s_begin) % 2;
+    // step s + 1's tiles go from set (j + 1) % NS to the other buffer.
+    auto iteration = [&](int s, auto j_c) __attribute__((always_inline)) {
+        constexpr int j = decltype(j_c)::value;
         const int buf = (s - s_begin) & 1;
-        const int kn = (s + 1 < s_end) ? (s + 1) * BK : s * BK;
-        TIQ_LOAD_TILES(kn)
+        load_tiles(std::integral_constant<int, (j + NS - 1) % NS>{}, s + NS - 1);
         const int sk = (s * BK) % kw;  // the step's first weight column
         if constexpr (GROUPED) {
-            if (sk % group == 0) {  // a new group: its scales, and partial sums from zero
-                const int g = sk / group;
-#pragma unroll
-                for (int j = 0; j < TN; ++j) gsc[j] = scale16[srow[j] + g];
+            if (sk % group == 0) {  // a new group: partial sums from zero
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j)
+                    for (int jj = 0; jj < TN; ++jj)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) part[i][j][r] = 0.f;
+                        for (int r = 0; r < 16; ++r) part[i][jj][r] = 0.f;
             }
         }
 #pragma unroll
@@ -242,35 +263,43 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, OCC) void gemm32_kernel(
             for (int i = 0; i < TM; ++i)
                 af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][swz(wm + i * 32 + frag_row, c)]);
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][swz(wn + j * 32 + frag_row, c)]);
+            for (int jj = 0; jj < TN; ++jj)
+                bfr[jj] = *reinterpret_cast<const bf16x8*>(&Bs[buf][swz(wn + jj * 32 + frag_row, c)]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
+                for (int jj = 0; jj < TN; ++jj) {
                     if constexpr (GROUPED)
-                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], part[i][j], 0, 0, 0);
+                        part[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[jj], part[i][jj], 0, 0, 0);
                     else
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[jj], acc[i][jj], 0, 0, 0);
                 }
         }
         if constexpr (GROUPED) {
             if ((sk + BK) % group == 0 || sk + BK == kw || s + 1 == s_end) {  // the group's last step
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const float sg = f16_bits_to_f32(gsc[j]);
+                for (int jj = 0; jj < TN; ++jj) {
+                    const float sg = f16_bits_to_f32(rs[j][jj]);
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(part[i][j][r], sg, acc[i][j][r]);
+                        for (int r = 0; r < 16; ++r) acc[i][jj][r] = fmaf(part[i][jj][r], sg, acc[i][jj][r]);
                 }
             }
         }
-        TIQ_STORE_TILES(buf ^ 1)
+        store_tiles(std::integral_constant<int, (j + 1) % NS>{}, buf ^ 1);
         __syncthreads();
-    }
-#undef TIQ_LOAD_TILES
-#undef TIQ_STORE_TILES
+    };
+
+    for_each_index(std::make_integer_sequence<int, NS - 1>{}, [&](auto j) __attribute__((always_inline)) { load_tiles(j, s_begin + j); });
+    store_tiles(std::integral_constant<int, 0>{}, 0);
+    __syncthreads();
+    int s0 = s_begin;
+    for (; s0 + NS <= s_end; s0 += NS)
+        for_each_index(std::make_integer_sequence<int, NS>{}, [&](auto j) __attribute__((always_inline)) { iteration(s0 + j, j); });
+    for_each_index(std::make_integer_sequence<int, NS - 1>{}, [&](auto j) __attribute__((always_inline)) {
+        if (s0 + j < s_end) iteration(s0 + j, j);
+    });
 
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
