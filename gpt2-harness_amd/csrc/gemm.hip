@@ -351,6 +351,9 @@ int dispatch_tile(const LinearArgs& a, int tile) {
 
 template <int FMT>
 int dispatch_gemm(const LinearArgs& a, int tile) {
+    if constexpr (FMT == kW4G) {
+        if (tile == 0 && staged_w4g_supported(a)) return launch_staged_w4g(a, nullptr, 0);
+    }
     if ((tile == 0 || tile >= 10) && staged_gemm_supported(a))
         return launch_staged_gemm(a, tile >= 10 ? tile - 10 : staged_gemm_choice(a));
     if (a.y_dtype == TIQ_F32) return dispatch_tile<FMT, float>(a, tile);

@@ -1,0 +1,72 @@
+// Group-wise int4 prefill GEMM on the register-staged kernel (gfx950): the
+// library's own group-wise format (nibbles as the reference's int4 rows,
+// quantization.py:132-149, one fp16 scale per row and group of 128 columns)
+// behind the reference's quantized Linears over a whole prompt
+// (model.py:254,319,352,355 with M = B*T):
+//     y[m, n] = sum_g s[n, g] * sum_{k in g} x[m, k] * q[n, k] + bias[n]
+// Built without -amdgpu-mfma-vgpr-form: the MFMAs accumulate a group's
+// partial tiles in AGPRs, and the scaled sums, which only vector instructions
+// touch, stay in VGPRs.
+#include <algorithm>
+
+#include "tiq_internal.hpp"
+
+namespace tiq {
+namespace {
+
+#include "gemm_staged_kernel.hpp"
+
+constexpr int kGroup = 128;  // two k64 steps
+constexpr int kBM = 224, kBN = 128;
+
+// One workgroup per tile (the group-wise kernel does not run persistent);
+// gridDim.z = S splits of whole groups, fp32 slices without bias when S > 1.
+template <typename TY>
+int run_w4g(const LinearArgs& a, TY* y, int64_t ldy, const float* bias, int64_t S) {
+    const int64_t tiles = ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
+    const int ngroups = (int)((a.K + kGroup - 1) / kGroup);
+    hipLaunchKernelGGL((gemm_staged<kBM, kBN, 1, kW4G, TY>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
+                       a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, nullptr, bias, y, ldy,
+                       (int)a.M, (int)a.N, (int)a.K, (int)a.K, a.scale16, ngroups);
+    return launch_status();
+}
+
+}  // namespace
+
+bool staged_w4g_supported(const LinearArgs& a) {
+    if (a.fmt != kW4G || a.x_dtype != TIQ_BF16 || a.group != kGroup || (a.kw && a.kw != a.K)) return false;
+    if (a.K % BK != 0 || a.ldw != a.K / 2) return false;
+    const int unit = a.y_dtype == TIQ_F32 ? 4 : 8;
+    if (a.N % unit != 0 || a.ldy % unit != 0 || !aligned(a.y, 16)) return false;
+    if ((a.bias && !aligned(a.bias, 16)) || !aligned(a.scale16, 2)) return false;
+    if (!aligned(a.x, 16) || a.ldx % 8 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
+    // 32-bit byte offsets from the base pointers, 32-bit scale offsets
+    if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + a.K / 2 > 0xffffffffLL) return false;
+    if (a.N * ((a.K + kGroup - 1) / kGroup) > 0x7fffffffLL) return false;
+    return true;
+}
+
+// Splits of whole groups when the 224 x 128 tiles fill less than a round of
+// 256 CUs (at most 8, at most one a group, within the workspace); 1: none.
+int64_t staged_w4g_splits(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
+    const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    const int64_t groups = (K + kGroup - 1) / kGroup;
+    int64_t S = std::min<int64_t>(std::min<int64_t>(256 / std::max<int64_t>(tiles, 1), groups), 8);
+    S = std::min<int64_t>(S, (int64_t)(ws_bytes / (size_t)(M * N * 4)));
+    return std::max<int64_t>(S, 1);
+}
+
+int launch_staged_w4g(const LinearArgs& a, void* ws, size_t ws_bytes) {
+    if (!staged_w4g_supported(a)) return TIQ_EUNSUPPORTED;
+    const int64_t S = (ws && aligned(ws, 16)) ? staged_w4g_splits(a.M, a.N, a.K, ws_bytes) : 1;
+    if (S > 1 && a.M * a.N * S <= 0x7fffffffLL) {
+        float* part = static_cast<float*>(ws);
+        int rc = run_w4g<float>(a, part, a.N, nullptr, S);
+        if (rc != TIQ_OK) return rc;
+        return launch_splitk_reduce(a, part, S, nullptr);
+    }
+    if (a.y_dtype == TIQ_F32) return run_w4g<float>(a, static_cast<float*>(a.y), a.ldy, a.bias, 1);
+    return run_w4g<uint16_t>(a, static_cast<uint16_t*>(a.y), a.ldy, a.bias, 1);
+}
+
+}  // namespace tiq

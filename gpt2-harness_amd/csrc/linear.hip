@@ -311,6 +311,8 @@ extern "C" int tiq_linear_w4g_ws(const void* x, int x_dtype, int64_t M, int64_t 
     rc = run_linear_split(a, workspace, workspace_bytes);
     if (rc != TIQ_EUNSUPPORTED) return rc;
     if (x_dtype == TIQ_BF16 && M >= kGemmMinRows) {  // bf16 rows: split over K when planned
+        rc = launch_staged_w4g(a, workspace, workspace_bytes);
+        if (rc != TIQ_EUNSUPPORTED) return rc;
         rc = launch_gemm_w4g_split(a, workspace, workspace_bytes);
         if (rc != TIQ_EUNSUPPORTED) return rc;
     }

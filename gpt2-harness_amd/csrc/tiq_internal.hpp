@@ -105,5 +105,11 @@ int launch_splitk_reduce(const LinearArgs& a, const float* part, int64_t S, cons
 // when the 128 x 128 tiles are too few to fill the GPU; the partial slices in
 // ws (staged_split_workspace bytes). TIQ_EUNSUPPORTED: no split planned.
 int launch_gemm_w4g_split(const LinearArgs& a, void* ws, size_t ws_bytes);
+// Group-wise int4 (groups of 128) with bf16 activations on the register-staged
+// kernel (gemm_grouped.hip): whether it takes these arguments, and the launch,
+// split over K (whole groups, fp32 slices in ws) when its tiles are few and ws
+// holds them. TIQ_EUNSUPPORTED when it does not take them.
+bool staged_w4g_supported(const LinearArgs& a);
+int launch_staged_w4g(const LinearArgs& a, void* ws, size_t ws_bytes);
 
 }  // namespace tiq

@@ -362,7 +362,8 @@ def test_gemm_w4_groupwise_prefill(dev, c_oracle, KN, M):
 # widths of one, three and sixteen k steps; partial tiles). The result is held
 # to the oracle's bound, and the bf16 output to the rounding of the fp32 one.
 @pytest.mark.parametrize("K,N,M,group", [(6400, 1600, 256, 128), (1600, 4800, 256, 128), (1600, 1600, 1024, 128),
-                                         (6400, 1600, 1024, 128), (1600, 4800, 300, 64), (1600, 1600, 257, 192),
+                                         (6400, 1600, 1024, 128), (1600, 4800, 300, 128), (768, 2304, 129, 128),
+                                         (1600, 4800, 300, 64), (1600, 1600, 257, 192),
                                          (3072, 768, 129, 1024)])
 def test_gemm_w4_groupwise_split_k(dev, c_oracle, K, N, M, group):
     L = _lib.lib()
