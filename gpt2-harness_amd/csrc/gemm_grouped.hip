@@ -38,11 +38,12 @@ bool staged_w4g_supported(const LinearArgs& a) {
     if (a.K % BK != 0 || a.ldw != a.K / 2) return false;
     const int unit = a.y_dtype == TIQ_F32 ? 4 : 8;
     if (a.N % unit != 0 || a.ldy % unit != 0 || !aligned(a.y, 16)) return false;
+    if (a.N % 32 != 0) return false;  // a 32-column tile is all inside N or all outside
     if ((a.bias && !aligned(a.bias, 16)) || !aligned(a.scale16, 2)) return false;
     if (!aligned(a.x, 16) || a.ldx % 8 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
     // 32-bit byte offsets from the base pointers, 32-bit scale offsets
     if ((a.M - 1) * a.ldx * 2 + a.K * 2 > 0xffffffffLL || (a.N - 1) * a.ldw + a.K / 2 > 0xffffffffLL) return false;
-    if (a.N * ((a.K + kGroup - 1) / kGroup) > 0x7fffffffLL) return false;
+    if (a.N * ((a.K + kGroup - 1) / kGroup) * 2 > 0xffffffffLL) return false;
     return true;
 }
 

@@ -79,11 +79,22 @@ __device__ __forceinline__ uint32_t bf16x2_of_bytes_perm(uint32_t d, int sh) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// the two biased nibbles of byte sh / 8 of d (low = even column) -> two bf16
-// in one dword (exact)
-__device__ __forceinline__ uint32_t bf16x2_of_nibbles_perm(uint32_t d, int sh) {
-    const float lo = (float)((int32_t)((d >> sh) & 0xfu) - 8);
-    const float hi = (float)((int32_t)((d >> (sh + 4)) & 0xfu) - 8);
+// Nibbles as bf16 times 16: d holds 8 biased nibbles (column 2j in the low
+// nibble of byte j, code n - 8); e (even columns) and o (odd columns) get
+// each nibble in the high half of a byte with its top bit flipped, which as
+// a signed byte is 16 (n - 8). A byte becomes a float in one instruction
+// (sub-dword operand select with sign extension), and 16 (n - 8) is exact in
+// bf16; the factor 16 is taken out in the epilogue (an exact power of two:
+// every partial sum is 16 times the unscaled one, rounded the same way).
+__device__ __forceinline__ void nibbles_x16(uint32_t d, uint32_t& e, uint32_t& o) {
+    e = ((d << 4) & 0xf0f0f0f0u) ^ 0x80808080u;
+    o = (d & 0xf0f0f0f0u) ^ 0x80808080u;
+}
+
+// byte k of e and o -> two bf16 in one dword (even column low)
+__device__ __forceinline__ uint32_t bf16x2_of_x16(uint32_t e, uint32_t o, int k) {
+    const float lo = (float)(int8_t)(e >> (8 * k));
+    const float hi = (float)(int8_t)(o >> (8 * k));
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
@@ -183,10 +194,13 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
                 hi = u32x4{bf16x2_of_bytes_perm(v.z, 0), bf16x2_of_bytes_perm(v.z, 16),
                            bf16x2_of_bytes_perm(v.w, 0), bf16x2_of_bytes_perm(v.w, 16)};
             } else {
-                lo = u32x4{bf16x2_of_nibbles_perm(v.x, 0), bf16x2_of_nibbles_perm(v.x, 8),
-                           bf16x2_of_nibbles_perm(v.x, 16), bf16x2_of_nibbles_perm(v.x, 24)};
-                hi = u32x4{bf16x2_of_nibbles_perm(v.y, 0), bf16x2_of_nibbles_perm(v.y, 8),
-                           bf16x2_of_nibbles_perm(v.y, 16), bf16x2_of_nibbles_perm(v.y, 24)};
+                uint32_t e0, o0, e1, o1;
+                nibbles_x16(v.x, e0, o0);
+                nibbles_x16(v.y, e1, o1);
+                lo = u32x4{bf16x2_of_x16(e0, o0, 0), bf16x2_of_x16(e0, o0, 1), bf16x2_of_x16(e0, o0, 2),
+                           bf16x2_of_x16(e0, o0, 3)};
+                hi = u32x4{bf16x2_of_x16(e1, o1, 0), bf16x2_of_x16(e1, o1, 1), bf16x2_of_x16(e1, o1, 2),
+                           bf16x2_of_x16(e1, o1, 3)};
             }
             *reinterpret_cast<u32x4*>(base + ws00 + j * 64 * 128) = lo;
             *reinterpret_cast<u32x4*>(base + ws01 + j * 64 * 128) = hi;
@@ -229,8 +243,10 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
         if constexpr (GROUPED) {
             const u32x4 v = wr[p][i][0];
             const uint32_t d = b == 0 ? v.x : b == 1 ? v.y : b == 2 ? v.z : v.w;
-            const u32x4 t = {bf16x2_of_nibbles_perm(d, 0), bf16x2_of_nibbles_perm(d, 8),
-                             bf16x2_of_nibbles_perm(d, 16), bf16x2_of_nibbles_perm(d, 24)};
+            uint32_t e, o;
+            nibbles_x16(d, e, o);
+            const u32x4 t = {bf16x2_of_x16(e, o, 0), bf16x2_of_x16(e, o, 1), bf16x2_of_x16(e, o, 2),
+                             bf16x2_of_x16(e, o, 3)};
             return __builtin_bit_cast(bf16x8, t);
         } else if constexpr (WD) {
             const u32x4 v = wr[p][i][b >> 1];
@@ -251,7 +267,7 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     floatx16 part[GROUPED ? TNn : 1][GROUPED ? TMm : 1];
     uint16_t sgr[GROUPED ? TNn : 1][16];
     float scf[GROUPED ? TNn : 1][16];
-    int soff[GROUPED ? TNn : 1][16];
+    uint32_t sbase[GROUPED ? TNn : 1];
     auto mfma_set = [&](int set, int t, bool fresh) {
         const int i = t / TMm, j = t % TMm;
         if constexpr (GROUPED) {
@@ -280,7 +296,10 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
 #pragma unroll
             for (int i = 0; i < TNn; ++i)
 #pragma unroll
-                for (int q = 0; q < 16; ++q) sgr[i][q] = scale16[soff[i][q] + g];
+                for (int q = 0; q < 16; ++q)
+                    sgr[i][q] = *reinterpret_cast<const uint16_t*>(
+                        reinterpret_cast<const char*>(scale16) + 2 * (g + (8 * (q >> 2) + (q & 3)) * ngroups) +
+                        sbase[i]);
         }
     };
     auto sconvert = [&]() {
@@ -320,7 +339,9 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
 #pragma unroll
         for (int c = 0; c < SBN; ++c) {
             const int n = min(n_blk + min(tid + NT * c, BN - 1), N - 1);
-            sbr[0][c] = (split || GROUPED) ? 1.f : scale[n];
+            // nibble codes enter the MFMAs times 16
+            constexpr float unit = FMT == kW8 ? 1.f : 0.0625f;
+            sbr[0][c] = (split || GROUPED) ? unit : scale[n] * unit;
             sbr[1][c] = (bias && !split) ? bias[n] : 0.f;
         }
     };
@@ -350,14 +371,14 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
     if constexpr (GROUPED) {
         // result register q of lane (r, h) holds column 8 (q / 4) + 4 h + q % 4
-        // of its 32-column tile; the first fold adds zero partial tiles
+        // of its 32-column tile (N % 32 == 0: a tile's columns are all inside
+        // or all outside; an outside one reads the last tile's scales); the
+        // first fold adds zero partial tiles
 #pragma unroll
         for (int i = 0; i < TNn; ++i) {
+            sbase[i] = (uint32_t)(min(n_blk + wn + 32 * i, N - 32) + 4 * h) * (uint32_t)ngroups * 2u;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                soff[i][q] = min(n_blk + wn + 32 * i + 8 * (q >> 2) + 4 * h + (q & 3), N - 1) * ngroups;
-                sgr[i][q] = 0;
-            }
+            for (int q = 0; q < 16; ++q) sgr[i][q] = 0;
 #pragma unroll
             for (int j = 0; j < TMm; ++j)
 #pragma unroll
