@@ -162,16 +162,22 @@ int launch_staged_gemm(const LinearArgs& a, int choice) {
 }
 
 int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
-    if (a.fmt != kW8 || !staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
+    if ((a.fmt != kW8 && a.fmt != kW4) || !staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
     const int64_t S = staged_splits(a.M, a.N, a.K);
     const size_t need = staged_split_workspace(a.M, a.N, a.K);
     if (S <= 1 || !ws || ws_bytes < need || !aligned(ws, 16)) return TIQ_EUNSUPPORTED;
     float* part = static_cast<float*>(ws);
     const int64_t tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
     // the products: raw fp32 slices [S][M][N] (unit scale, no bias in the kernel)
-    hipLaunchKernelGGL((gemm_staged<128, 128, 2, kW8, float>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
-                       a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, part,
-                       (int64_t)a.N, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0);
+    const dim3 grid((unsigned)tiles, 1, (unsigned)S);
+    if (a.fmt == kW4)
+        hipLaunchKernelGGL((gemm_staged<128, 128, 2, kW4, float>), grid, dim3(256), 0, a.stream,
+                           static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, part, (int64_t)a.N,
+                           (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0);
+    else
+        hipLaunchKernelGGL((gemm_staged<128, 128, 2, kW8, float>), grid, dim3(256), 0, a.stream,
+                           static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, part, (int64_t)a.N,
+                           (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0);
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
     return launch_splitk_reduce(a, part, S, a.scale);

@@ -296,6 +296,10 @@ extern "C" int tiq_linear_w4_ws(const void* x, int x_dtype, int64_t M, int64_t K
     if (workspace && !aligned(workspace, 16)) return TIQ_EALIGN;
     rc = run_linear_split(a, workspace, workspace_bytes);
     if (rc != TIQ_EUNSUPPORTED) return rc;
+    if (x_dtype == TIQ_BF16 && M >= kGemmMinRows) {  // bf16 rows: split over K when planned
+        rc = launch_staged_gemm_split(a, workspace, workspace_bytes);
+        if (rc != TIQ_EUNSUPPORTED) return rc;
+    }
     return run_linear(a);
 }
 

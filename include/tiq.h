@@ -205,10 +205,10 @@ int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx
  * runs on the matrix cores (every product exact, fp32 accumulation; the
  * group-wise format scales each group's partial sum), as tiq_linear_w8_ws
  * does for int8 -- the prefill of a model quantized to int4 (model.py:254,
- * 319,352,355 at M = B*T). tiq_linear_w4g_ws with bf16 x, M >= 128 and a
- * workspace of tiq_gemm_w8_workspace(TIQ_BF16, M, K, N) bytes splits a product
- * with few output tiles over K (whole groups a split, fp32 slices summed in a
- * fixed order). Without a workspace, or where the GEMM does not take the
+ * 319,352,355 at M = B*T). With bf16 x, M >= 128 and a workspace of
+ * tiq_gemm_w8_workspace(TIQ_BF16, M, K, N) bytes both split a product with few
+ * output tiles over K (group-wise: whole groups a split), the fp32 slices
+ * summed in a fixed order. Without a workspace, or where the GEMM does not take the
  * shape (K % 64, group % 64), they compute what tiq_linear_w4 /
  * tiq_linear_w4g compute. */
 int tiq_linear_w4_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,

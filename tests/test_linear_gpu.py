@@ -318,6 +318,34 @@ def test_linear_w4_reference_layout(dev, c_oracle, KN, M):
         assert torch.equal(ybf.cpu(), y.cpu().to(torch.bfloat16)), "bf16 output is not RNE of the fp32 output"
 
 
+# int4 in the reference's nibble layout with bf16 rows and the GEMM workspace:
+# products with few 128 x 128 tiles split over K (6400x1600 at M = 256: 26
+# tiles, eight splits), the fp32 slices summed in order, scaled and biased
+# after; the oracle's bound, the bf16 output the rounding of the fp32 one.
+@pytest.mark.parametrize("K,N,M", [(6400, 1600, 256), (1600, 4800, 300), (768, 2304, 129)])
+def test_linear_w4_split_k(dev, c_oracle, K, N, M):
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, M + K + 7, torch.bfloat16)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 4)
+    packed = torch.from_numpy(c_oracle.pack_int4(q)).to(dev)
+    sd, bd, xd = torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
+    n_ws = int(L.tiq_gemm_w8_workspace(_lib.BF16, M, K, N))
+    assert n_ws > 0, "the shape should plan a split"
+    ws = torch.empty(n_ws, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for dt in (torch.float32, torch.bfloat16):
+        y = torch.full((M, N), 7.0, device=dev, dtype=dt)
+        rc = L.tiq_linear_w4_ws(xd.data_ptr(), _lib.BF16, M, K, K, packed.data_ptr(), sd.data_ptr(), bd.data_ptr(),
+                                N, y.data_ptr(), _lib.dtype_code(dt), N, ws.data_ptr(), n_ws, st)
+        _lib.check(rc, "tiq_linear_w4_ws")
+        torch.cuda.synchronize()
+        outs[dt] = y.cpu()
+    ok, err, bound = OL.within_tolerance(outs[torch.float32], OL.linear_ref(x, OL.dequantize(q, s), b))
+    assert ok, f"w4 split M={M} K={K} N={N}: max err {err:.3g} > {bound:.3g}"
+    assert torch.equal(outs[torch.bfloat16], outs[torch.float32].to(torch.bfloat16)), "bf16 not RNE of fp32"
+
+
 @pytest.mark.parametrize("KN", [(768, 2304), (1600, 4800), (6400, 1600)])
 @pytest.mark.parametrize("M", [1, 4, 64])
 def test_linear_w4_groupwise(dev, c_oracle, KN, M):
