@@ -1,6 +1,10 @@
 // Prefill GEMM on the matrix cores (gfx950), for the reference's quantized
 // Linears over a whole prompt (model.py:254,319,352,355 with M = B*T):
 //     y[m, n] = scale[n] * sum_k x[m, k] * q[n, k] + bias[n]
+// This LDS-dequant kernel takes the group-wise int4 products the staged
+// kernels (gemm_staged.hip, gemm_grouped.hip) do not: groups other than 128
+// columns, and the three-plane fp32-activation path; and, through
+// tiq_gemm_w8_tile's tiles 1-4, int8 and reference int4 for tests.
 //
 //   * workgroup tile BM x BN over (M, N), BK = 64 columns of K per step;
 //     WAVES_M x WAVES_N wavefronts, each owning a (BM/WAVES_M) x (BN/WAVES_N)

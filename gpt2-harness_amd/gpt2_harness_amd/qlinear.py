@@ -116,11 +116,9 @@ def linear_into(m: QuantLinear, x2: torch.Tensor, y: torch.Tensor) -> None:
                                 y.data_ptr(), yd, y.stride(0), None if ws is None else ws.data_ptr(), ws_bytes, st)
     else:
         # int4 formats: fp32 activations over many rows take the matrix cores
-        # through the same three exact bf16 planes; group-wise int4 with bf16
-        # rows may also split over K (workspace 0: none)
-        ws_bytes = int(L.tiq_linear_w8_workspace(xd, M, K))
-        if m.fmt != FMT_W4:
-            ws_bytes = max(ws_bytes, int(L.tiq_gemm_w8_workspace(xd, M, K, N)))
+        # through the same three exact bf16 planes; with bf16 rows a product
+        # with few output tiles splits over K (workspace 0: none)
+        ws_bytes = max(int(L.tiq_linear_w8_workspace(xd, M, K)), int(L.tiq_gemm_w8_workspace(xd, M, K, N)))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
         wp = None if ws is None else ws.data_ptr()
         if m.fmt == FMT_W4:
