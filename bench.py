@@ -910,6 +910,14 @@ def main() -> int:
         t = json.loads(tfile.read_text())
         if t.get("tiq_version") == _lib.lib().tiq_version():
             traffic = t["traffic_bytes_per_launch"]
+    launch_model_us = (floor["tiq_linear_w8_64x64_M1"]["us_per_launch"]
+                       + head["bytes_per_step"] / head["launches_per_step"] / (hbm["copy"]["GB/s"] * 1e3))
+    if "gemv_xl_M1" in detail:
+        xl = detail["gemv_xl_M1"]
+        xl_model = (floor["tiq_linear_w8_64x64_M1"]["us_per_launch"]
+                    + xl["bytes_per_step"] / xl["launches_per_step"] / (hbm["copy"]["GB/s"] * 1e3))
+        xl["launch_model_us"] = xl_model
+        xl["frac_of_launch_model"] = xl_model / xl["avg_launch_us"]
     avg_launch_s = head["avg_launch_us"] * 1e-6
     bytes_per_launch = head["bytes_per_step"] / head["launches_per_step"]
     achieved = bytes_per_launch / avg_launch_s / 1e9
@@ -945,6 +953,11 @@ def main() -> int:
             "measured_hbm_GBs": {k: v["GB/s"] for k, v in hbm.items()},
             "frac_of_measured_copy": achieved / hbm["copy"]["GB/s"],
             "graph_launch_floor_us": {k: v["us_per_launch"] for k, v in floor.items()},
+            # what one launch of this size could cost at best: the library's
+            # own minimal GEMV launch in a graph plus the bytes at the measured
+            # copy rate; frac_of_launch_model = that / the measured launch
+            "launch_model_us": launch_model_us,
+            "frac_of_launch_model": launch_model_us / head["avg_launch_us"],
         },
         "cpu_baseline": cpu,
         "detail": {"gemv_small_M1": head, "hbm_measured": hbm, "launch_floor": floor, **detail},
