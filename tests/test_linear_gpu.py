@@ -419,9 +419,13 @@ def test_gemm_w4_groupwise_split_k(dev, c_oracle, K, N, M, group):
 
 # other group widths (multiples of the 64-column k step, a last group of one
 # step), partial row and column tiles, and a width the GEMM does not take
-# (32: the vector-ALU kernel serves it)
+# (32: the vector-ALU kernel serves it); groups of 128 at K of one half group,
+# one group and one and a half (the staged kernel), and with N % 32 != 0 (the
+# LDS-dequant kernel takes it)
 @pytest.mark.parametrize("K,N,M,group", [(1600, 4800, 300, 64), (1600, 1600, 257, 192), (768, 2304, 513, 256),
-                                         (3072, 768, 129, 1024), (1600, 1000, 256, 32), (6400, 1600, 384, 6400)])
+                                         (3072, 768, 129, 1024), (1600, 1000, 256, 32), (6400, 1600, 384, 6400),
+                                         (64, 256, 130, 128), (128, 512, 224, 128), (192, 512, 200, 128),
+                                         (1600, 1000, 256, 128)])
 def test_gemm_w4_groupwise_widths_and_partial_tiles(dev, c_oracle, K, N, M, group):
     _run_w4g(dev, c_oracle, K, N, M, group, seed=M + group)
 
