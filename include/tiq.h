@@ -149,10 +149,11 @@ int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
                      void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
                      void* stream);
 
-/* Workspace bytes with which tiq_gemm_w8_ws (and tiq_linear_w8_ws) run a
- * product with few output tiles split over K (fp32 partial slices, summed
- * in a fixed order by a second kernel), plus, for fp32 activations, their
- * bf16 planes. 0 when none is needed. */
+/* Workspace bytes with which tiq_gemm_w8_ws (and tiq_linear_w8_ws, and with
+ * bf16 activations tiq_linear_w4_ws / tiq_linear_w4g_ws) run a product with
+ * few output tiles split over K (fp32 partial slices, summed in a fixed order
+ * by a second kernel), plus, for fp32 activations, their bf16 planes. 0 when
+ * none is needed. */
 size_t tiq_gemm_w8_workspace(int x_dtype, int64_t M, int64_t K, int64_t N);
 /* tiq_gemm_w8 with a caller workspace (see tiq_gemm_w8_workspace): the
  * prefill product of the reference's Linears (model.py:254,319,352,355 at
