@@ -63,15 +63,23 @@ __device__ __forceinline__ void store_planes(uint16_t* x3, int64_t m, int64_t Kc
 // pos filled ones, so the first loads need not wait for pos -- for small caches
 // (batch 1), where the unused tail costs less than that wait; the slots past
 // pos are dropped where they are used either way.
+// SL: qkv holds the n_sl raw partial slices of the q, k, v projection
+// (slice z at qkv + z sl_stride, rows of ld_qkv; launch_decode_slices), which
+// the kernel finishes for its head: (sum of the slices in slice order) *
+// scale + bias, the reduction kernel's arithmetic.
 // Grid (head, sequence). The arguments up to t_max are the ones the loads
 // need, in the 14 dwords preloaded into SGPRs.
-template <int NCH, bool WHOLE>
-__global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
+// Eight wavefronts a SIMD (at most 64 VGPRs): four workgroups a CU, so the
+// 800 of a GPT-2-XL batch-32 layer are resident at once.
+template <int NCH, bool WHOLE, bool SL>
+__global__ __launch_bounds__(64 * kAttWaves) __attribute__((amdgpu_waves_per_eu(8))) void decode_attention_kernel(
     const float* __restrict__ qkv, const int64_t* __restrict__ pos_p, float* __restrict__ kc, float* __restrict__ vc,
     int ld_qkv, int H, int Hkv, int group, int t_max, float* __restrict__ y, int64_t ldy,
-    uint16_t* __restrict__ x3) {
+    uint16_t* __restrict__ x3, int n_sl, int64_t sl_stride, const float* __restrict__ sl_scale,
+    const float* __restrict__ sl_bias) {
     constexpr int W = kAttWaves, NI = kLoadsPerChunk;
-    __shared__ float qn[kHeadDim], kn[kHeadDim], vn[kHeadDim];
+    __shared__ __align__(16) float qn[kHeadDim];  // read as float4 with slices
+    __shared__ float kn[kHeadDim], vn[kHeadDim];
     __shared__ float sc[kMaxSlots];
     __shared__ float red[W];
     __shared__ float4 part[W][4][16];
@@ -104,13 +112,30 @@ __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
 #pragma unroll
         for (int i = 0; i < NI; ++i) vr[0][i] = cache_load(rv, slot_off(0, i));
     }
-    const float4 q4 = *reinterpret_cast<const float4*>(qr + h * kHeadDim + d4);
+    float4 q4;  // with slices, from the finished row in LDS below
+    if constexpr (!SL) q4 = *reinterpret_cast<const float4*>(qr + h * kHeadDim + d4);
     if constexpr (WHOLE) pos_in = *pos_p;  // read behind the loads, which do not need it
     // A position outside the cache computes on slot 0, writes nothing to the
     // cache and stores NaN: no branch, so no load is sunk behind the read of pos.
     const bool ok = pos_in >= 0 && pos_in < t_max;
     const int64_t pos = ok ? pos_in : 0;
-    if (tid < kHeadDim) {
+    if constexpr (SL) {
+        if (wave < 3) {  // wavefront 0 the query, 1 the key, 2 the value; every slice requested at once
+            const int col = (wave == 0 ? h * kHeadDim : wave == 1 ? C + hk * kHeadDim : C + KV + hk * kHeadDim) + lane;
+            float p[kMaxSlices];
+#pragma unroll
+            for (int z = 0; z < kMaxSlices; ++z) p[z] = qr[(int64_t)min(z, n_sl - 1) * sl_stride + col];
+            const float f_sc = sl_scale[col], f_bi = sl_bias ? sl_bias[col] : 0.f;
+            float a = 0.f;
+#pragma unroll
+            for (int z = 0; z < kMaxSlices; ++z)
+                if (z < n_sl) a += p[z];
+            const float v = a * f_sc + f_bi;
+            (wave == 0 ? qn : wave == 1 ? kn : vn)[lane] = v;
+            if (wave > 0 && ok && (group == 1 || h % group == 0))  // one writer per kv head
+                (wave == 1 ? kb : vb)[pos * kHeadDim + lane] = v;
+        }
+    } else if (tid < kHeadDim) {
         const float q_new = qr[h * kHeadDim + tid];
         const float k_new = qr[C + hk * kHeadDim + tid];
         const float v_new = qr[C + KV + hk * kHeadDim + tid];
@@ -123,6 +148,7 @@ __global__ __launch_bounds__(64 * kAttWaves) void decode_attention_kernel(
         }
     }
     __syncthreads();
+    if constexpr (SL) q4 = *reinterpret_cast<const float4*>(qn + d4);
 
     // ---- scores of slots < pos (slot pos is the new key) ----
     const float inv_div = 1.0f / sqrtf((float)kHeadDim);  // exactly 1/8
@@ -331,9 +357,12 @@ __global__ __launch_bounds__(256) void gelu_tanh_kernel(const float* x, float* y
 
 using namespace tiq;
 
+// qkv rows, or (n_sl > 0) the raw partial slices of the q, k, v projection
+// with its scale and bias
 static int decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int64_t n_head, int64_t n_kv_head,
                             int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
-                            float* y, int64_t ldy, uint16_t* planes_out, void* stream) {
+                            float* y, int64_t ldy, uint16_t* planes_out, void* stream, int64_t n_sl = 0,
+                            const float* sl_scale = nullptr, const float* sl_bias = nullptr) {
     if (batch < 0 || n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head) return TIQ_EINVAL;
     if (batch == 0) return TIQ_OK;
     if (!qkv || !k_cache || !v_cache || !pos || !y) return TIQ_EINVAL;
@@ -347,10 +376,18 @@ static int decode_attention(const float* qkv, int64_t ld_qkv, int64_t batch, int
     const bool whole = batch * n_kv_head * t_max * kHeadDim * 4 * 2 <= (32ll << 20);
     auto launch = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, block, 0, as_stream(stream), qkv, pos, k_cache, v_cache, (int)ld_qkv,
-                           (int)n_head, (int)n_kv_head, (int)(n_head / n_kv_head), (int)t_max, y, ldy, planes_out);
+                           (int)n_head, (int)n_kv_head, (int)(n_head / n_kv_head), (int)t_max, y, ldy, planes_out,
+                           (int)n_sl, batch * ld_qkv, sl_scale, sl_bias);
     };
-    if (t_max <= 128) whole ? launch(decode_attention_kernel<1, true>) : launch(decode_attention_kernel<1, false>);
-    else whole ? launch(decode_attention_kernel<2, true>) : launch(decode_attention_kernel<2, false>);
+    if (n_sl > 0) {
+        if (t_max <= 128)
+            whole ? launch(decode_attention_kernel<1, true, true>) : launch(decode_attention_kernel<1, false, true>);
+        else whole ? launch(decode_attention_kernel<2, true, true>) : launch(decode_attention_kernel<2, false, true>);
+    } else if (t_max <= 128) {
+        whole ? launch(decode_attention_kernel<1, true, false>) : launch(decode_attention_kernel<1, false, false>);
+    } else {
+        whole ? launch(decode_attention_kernel<2, true, false>) : launch(decode_attention_kernel<2, false, false>);
+    }
     return launch_status();
 }
 
@@ -368,6 +405,50 @@ extern "C" int tiq_decode_attention_planes(const float* qkv, int64_t ld_qkv, int
     if (!planes_out) return TIQ_EINVAL;
     return decode_attention(qkv, ld_qkv, batch, n_head, n_kv_head, head_dim, k_cache, v_cache, t_max, pos, y, ldy,
                             planes_out, stream);
+}
+
+extern "C" size_t tiq_decode_qkv_attention_workspace(int64_t batch, int64_t n_embd, int64_t n_qkv) {
+    return decode_slices_bytes(batch, n_embd, n_qkv);
+}
+
+extern "C" int tiq_decode_qkv_attention(const uint16_t* x_planes, int64_t batch, int64_t n_embd, const void* w,
+                                        int w_format, const float* scale, const float* bias, int64_t n_head,
+                                        int64_t n_kv_head, int64_t head_dim, float* k_cache, float* v_cache,
+                                        int64_t t_max, const int64_t* pos, float* y, int64_t ldy,
+                                        uint16_t* planes_out, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT8_TILED) return TIQ_EUNSUPPORTED;
+    if (batch < 0 || n_embd <= 0 || n_head <= 0 || n_kv_head <= 0 || n_head % n_kv_head) return TIQ_EINVAL;
+    if (batch == 0) return TIQ_OK;
+    if (!x_planes || !w || !scale || !k_cache || !v_cache || !pos || !y) return TIQ_EINVAL;
+    if (head_dim != kHeadDim || t_max <= 0 || t_max > kMaxSlots) return TIQ_EUNSUPPORTED;
+    if (batch > 64 || n_embd % 32 != 0) return TIQ_EUNSUPPORTED;
+    if (ldy < n_head * head_dim) return TIQ_EINVAL;
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || (planes_out && !aligned(planes_out, 16))) return TIQ_EALIGN;
+    const int64_t N = (n_head + 2 * n_kv_head) * head_dim;
+    if (N > INT32_MAX) return TIQ_EUNSUPPORTED;
+    const size_t need = decode_slices_bytes(batch, n_embd, N);
+    if (need == 0) return TIQ_EUNSUPPORTED;  // K beyond the product's splits
+    if (!workspace || workspace_bytes < need) return TIQ_EWORKSPACE;
+    if (!aligned(workspace, 16)) return TIQ_EALIGN;
+    const WFormat fmt = w_format == TIQ_WF_INT8_TILED ? kW8T : kW8;
+    LinearArgs a{};
+    a.x_dtype = TIQ_F32;
+    a.M = batch;
+    a.K = n_embd;
+    a.w = static_cast<const uint8_t*>(w);
+    a.ldw = n_embd;  // row-major codes: rows of K bytes
+    a.scale = scale;
+    a.bias = bias;
+    a.N = N;
+    a.y_dtype = TIQ_F32;
+    a.stream = as_stream(stream);
+    a.fmt = fmt;
+    float* part = static_cast<float*>(workspace);
+    int rc = launch_decode_slices(a, x_planes, part);
+    if (rc != TIQ_OK) return rc;
+    return decode_attention(part, N, batch, n_head, n_kv_head, head_dim, k_cache, v_cache, t_max, pos, y, ldy,
+                            planes_out, stream, decode_slices_count(batch, n_embd, N), scale, bias);
 }
 
 extern "C" int tiq_gelu_tanh(const float* x, float* y, int64_t n, void* stream) {

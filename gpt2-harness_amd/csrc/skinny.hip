@@ -845,21 +845,42 @@ int64_t decode_splits(int64_t M, int64_t K, int64_t N) {
 
 // The split of an int8 product whose output the reduction kernel finishes in
 // any case (LayerNorm'd planes or a residual follow): split_product_kernel
-// with RT weight tiles a workgroup -- two on long rows (K >= 4096, an even
-// tile count), so each activation operand serves twice the weights -- and K
-// split until about 256 workgroups stream the weights, at least one 32-column
-// unit and at most kSplitMaxUnits a wavefront, at most 16 splits.
-// GPT-2-XL at batch 32: attn.c_proj 50 tiles x 5 splits, mlp.c_proj 25 tile
-// pairs x 10 splits.
-constexpr int kSplitMaxUnits = 4;
+// with one weight tile a workgroup and K split until about 256 workgroups
+// stream the weights, at least one 32-column unit and at most
+// kSplitMaxUnits1 a wavefront, at most 16 splits. GPT-2-XL at batch 32:
+// attn.c_proj and mlp.c_proj 50 tiles x 5 splits. (Two tiles a workgroup,
+// which halves the activation reads per weight byte, measured no faster for
+// the product at these shapes and needs twice the splits for the same
+// workgroup count, which the reduction pays for: mlp.c_proj 12.4 against
+// 11.1 us product + reduction.)
+constexpr int kSplitMaxUnits = 4;   // units a wavefront with two tiles a workgroup
+constexpr int kSplitMaxUnits1 = 8;  // with one
 struct SplitPlan { int64_t S; int RT; };
+int split_max_units(int RT) { return RT == 1 ? kSplitMaxUnits1 : kSplitMaxUnits; }
 SplitPlan reduce_plan(int64_t M, int64_t K, int64_t N) {
     const int64_t U = K / 32, tiles = (N + 31) / 32, rows = (M + 31) / 32;
-    const int RT = (U >= 128 && tiles % 2 == 0) ? 2 : 1;
+    const int64_t groups = tiles * rows;
+    int64_t S = std::min<int64_t>(std::max<int64_t>(256 / groups, 1), std::max<int64_t>(U / kWaves, 1));
+    S = std::max<int64_t>(S, (U + kWaves * kSplitMaxUnits1 - 1) / (kWaves * kSplitMaxUnits1));
+    return {std::min<int64_t>(S, 16), 1};
+}
+
+// The split of a product whose raw partial slices its consumer sums itself
+// (the q, k, v projection read by the decode attention): two weight tiles a
+// workgroup where the tile count is even (each activation operand then feeds
+// twice the weights), K split until about 256 workgroups stream the weights,
+// at least one unit and at most split_max_units(RT) a wavefront, at most
+// kMaxSlices splits (a longer K is refused). GPT-2-XL at batch 32: c_attn 75
+// tile pairs x 3 splits (5.9 us against 6.7-7.3 us for one tile a workgroup
+// and no split).
+SplitPlan slices_plan(int64_t M, int64_t K, int64_t N) {
+    const int64_t U = K / 32, tiles = (N + 31) / 32, rows = (M + 31) / 32;
+    const int RT = tiles % 2 == 0 ? 2 : 1;
     const int64_t groups = tiles / RT * rows;
     int64_t S = std::min<int64_t>(std::max<int64_t>(256 / groups, 1), std::max<int64_t>(U / kWaves, 1));
-    S = std::max<int64_t>(S, (U + kWaves * kSplitMaxUnits - 1) / (kWaves * kSplitMaxUnits));
-    return {std::min<int64_t>(S, 16), RT};
+    const int64_t mu = split_max_units(RT);
+    S = std::max<int64_t>(S, (U + kWaves * mu - 1) / (kWaves * mu));
+    return {std::min<int64_t>(S, kMaxSlices), RT};
 }
 
 size_t partials_bytes(int64_t M, int64_t K, int64_t N) {
@@ -874,8 +895,11 @@ int launch_split_product(const LinearArgs& a, const uint16_t* x3, float* part, i
     if (per_wave <= 2)
         hipLaunchKernelGGL((split_product_kernel<WF, RT, 2>), grid, dim3(kWaves * 64), 0, a.stream, x3, (int)a.M,
                            (int)a.K, a.w, a.ldw, (int)a.N, part);
-    else
+    else if (RT == 2 || per_wave <= kSplitMaxUnits)
         hipLaunchKernelGGL((split_product_kernel<WF, RT, kSplitMaxUnits>), grid, dim3(kWaves * 64), 0, a.stream, x3,
+                           (int)a.M, (int)a.K, a.w, a.ldw, (int)a.N, part);
+    else  // one tile a workgroup: up to kSplitMaxUnits1 units a wavefront
+        hipLaunchKernelGGL((split_product_kernel<WF, 1, kSplitMaxUnits1>), grid, dim3(kWaves * 64), 0, a.stream, x3,
                            (int)a.M, (int)a.K, a.w, a.ldw, (int)a.N, part);
     return launch_status();
 }
@@ -947,7 +971,7 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
     if (w8 && must_reduce && red_ok) {
         const SplitPlan p = reduce_plan(a.M, a.K, a.N);
         const int64_t per_wave = ((a.K / 32 + p.S - 1) / p.S + kWaves - 1) / kWaves;
-        if (per_wave <= kSplitMaxUnits && ((a.N + 31) / 32) % p.RT == 0) plan = p;
+        if (per_wave <= split_max_units(p.RT) && ((a.N + 31) / 32) % p.RT == 0) plan = p;
     }
     const int64_t S = plan.S;
     // planes without a LayerNorm or residual from one split: the product
@@ -1005,6 +1029,40 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
     if (a.fmt == kW8) return run_decode_t<kW8>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, plan);
     if (a.fmt == kW8T) return run_decode_t<kW8T>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, plan);
     return run_decode_t<kF32>(a, x3, next_ln_w, next_ln_b, next_eps, planes_out, part, plan);
+}
+
+int64_t decode_slices_count(int64_t M, int64_t K, int64_t N) {
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    return slices_plan(M, K, N).S;
+}
+
+// every wavefront's share of K fits its registers within kMaxSlices splits
+bool slices_fit(int64_t K, SplitPlan plan) {
+    const int64_t per_wave = ((K / 32 + plan.S - 1) / plan.S + kWaves - 1) / kWaves;
+    return per_wave <= split_max_units(plan.RT);
+}
+
+size_t decode_slices_bytes(int64_t M, int64_t K, int64_t N) {
+    if (M <= 0 || M > 64 || K <= 0 || K % 32 != 0 || N <= 0) return 0;
+    const SplitPlan plan = slices_plan(M, K, N);
+    if (!slices_fit(K, plan)) return 0;
+    return round256((size_t)(plan.S * M * N) * 4);
+}
+
+int launch_decode_slices(const LinearArgs& a, const uint16_t* x_planes, float* part) {
+    if (a.fmt != kW8 && a.fmt != kW8T) return TIQ_EUNSUPPORTED;
+    if (a.M < 1 || a.M > 64 || a.K <= 0 || a.K % 32 != 0 || a.N <= 0 || a.N > 0x7fffffff) return TIQ_EUNSUPPORTED;
+    if (a.fmt == kW8T && a.N % 32 != 0) return TIQ_EUNSUPPORTED;  // whole row tiles
+    if (!x_planes || !part || !a.w) return TIQ_EINVAL;
+    if (a.fmt == kW8 && a.ldw < a.K) return TIQ_EINVAL;
+    if (!aligned(a.w, 16) || a.ldw % 16 != 0 || !aligned(x_planes, 16) || !aligned(part, 16)) return TIQ_EALIGN;
+    const SplitPlan plan = slices_plan(a.M, a.K, a.N);
+    if (!slices_fit(a.K, plan)) return TIQ_EUNSUPPORTED;
+    if (a.fmt == kW8T)
+        return plan.RT == 2 ? launch_split_product<kW8T, 2>(a, x_planes, part, plan.S)
+                            : launch_split_product<kW8T, 1>(a, x_planes, part, plan.S);
+    return plan.RT == 2 ? launch_split_product<kW8, 2>(a, x_planes, part, plan.S)
+                        : launch_split_product<kW8, 1>(a, x_planes, part, plan.S);
 }
 
 // One thread per 16 bytes of a tile: block b = (t, u) of (N / 32, K / 32),

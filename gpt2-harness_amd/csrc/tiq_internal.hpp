@@ -79,6 +79,18 @@ size_t skinny_workspace(int64_t M, int64_t K);
 // planes of a previous call (x_planes).
 int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float* next_ln_w,
                       const float* next_ln_b, float next_eps, uint16_t* planes_out);
+
+// The product of a batched decode linear as raw fp32 partial sums, for a
+// consumer that finishes them itself (skinny.hip): slice z of `part` (M x N,
+// at part + z M N) holds K units [z U / S, (z + 1) U / S) of x W^T with no
+// scale or bias, S = decode_slices_count(M, K, N) <= kMaxSlices. int8
+// weights (kW8, kW8T), 1..64 rows, K % 32 == 0 (K <= 4096 with an even
+// count of 32-row tiles, else K <= 8192), the operand planes of a previous
+// decode linear in.
+constexpr int64_t kMaxSlices = 4;
+int64_t decode_slices_count(int64_t M, int64_t K, int64_t N);
+size_t decode_slices_bytes(int64_t M, int64_t K, int64_t N);  // 0: shape not supported
+int launch_decode_slices(const LinearArgs& a, const uint16_t* x_planes, float* part);
 size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N);
 size_t decode_planes_bytes(int64_t M, int64_t K);
 // int8 codes (N, K) -> the operand tiles the decode product reads with kW8T.

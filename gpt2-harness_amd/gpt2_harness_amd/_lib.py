@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                              _vp, _vp, ctypes.c_float, _i32, _vp, _i64, _vp, _sz, _vp], _i32),
     "tiq_decode_attention": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _i32),
     "tiq_decode_attention_planes": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp], _i32),
+    "tiq_decode_qkv_attention_workspace": ([_i64, _i64, _i64], _sz),
+    "tiq_decode_qkv_attention": ([_vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp,
+                                  _i64, _vp, _vp, _sz, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
     "tiq_gelu_tanh": ([_vp, _vp, _i64, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),

@@ -237,6 +237,12 @@ class FusedDecoder(_DecoderBase):
             cws = max(int(L.tiq_decode_linear_workspace(_lib.WF_INT8, B, k, n))
                       for k, n in ((C, qkv), (C, C), (C, hidden), (hidden, C)))
             cws = max(cws, int(L.tiq_decode_linear_workspace(head_wf, B, C, cfg.vocab_size)))
+            # c_attn's split-K slices summed by the attention kernel itself
+            # (tiq_decode_qkv_attention; 0 bytes: this shape keeps the
+            # separate product)
+            self.qkv_slices = int(L.tiq_decode_qkv_attention_workspace(B, C, qkv)) > 0
+            if self.qkv_slices:
+                cws = max(cws, int(L.tiq_decode_qkv_attention_workspace(B, C, qkv)))
             self.chain_ws = torch.empty(max(cws, 1), dtype=torch.uint8, device=dev)
             self.chain_ws_bytes = cws
             pc, ph = int(L.tiq_decode_planes_bytes(B, C)), int(L.tiq_decode_planes_bytes(B, hidden))
@@ -292,6 +298,22 @@ class FusedDecoder(_DecoderBase):
             _lib.ptr(planes_out), self.chain_ws.data_ptr(), self.chain_ws_bytes, st)
         _lib.check(rc, "decode linear")
 
+    def _qkv_attention(self, i: int, lin) -> None:
+        """c_attn on LayerNorm 1's planes as split-K slices, then the attention
+        of block i summing them (tiq_decode_qkv_attention), its output rows and
+        planes out."""
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        w, wf = lin.codes, _lib.WF_INT8
+        tiles = self.tiles.get(id(lin))
+        if tiles is not None:
+            w, wf = tiles, _lib.WF_INT8_TILED
+        rc = self.L.tiq_decode_qkv_attention(
+            self.p_ln1.data_ptr(), self.B, lin.in_features, w.data_ptr(), wf, lin.scale.data_ptr(),
+            _lib.ptr(lin.bias), self.H, self.Hkv, self.hd, self.k[i].data_ptr(), self.v[i].data_ptr(), self.T,
+            self.pos.data_ptr(), self.att.data_ptr(), self.att.stride(0), self.p_att.data_ptr(),
+            self.chain_ws.data_ptr(), self.chain_ws_bytes, st)
+        _lib.check(rc, "decode q, k, v projection and attention")
+
     def _step_chain(self) -> None:
         m, cfg, L = self.model, self.cfg, self.L
         B, C = self.B, cfg.n_embd
@@ -303,14 +325,18 @@ class FusedDecoder(_DecoderBase):
         n = len(m.h)
         for i, block in enumerate(m.h):
             attn, mlp = block.attn, block.mlp
-            if i == 0:  # the embedding rows: LayerNorm 1 here
-                self._dl(attn.c_attn, W8, y=self.qkv, x=self.x, ln=block.ln_1)
-            else:       # the previous block left LayerNorm 1's planes
-                self._dl(attn.c_attn, W8, y=self.qkv, planes_in=self.p_ln1)
-            _lib.check(L.tiq_decode_attention_planes(self.qkv.data_ptr(), self.qkv.stride(0), B, self.H, self.Hkv,
-                                                     self.hd, self.k[i].data_ptr(), self.v[i].data_ptr(), self.T,
-                                                     self.pos.data_ptr(), self.att.data_ptr(), self.att.stride(0),
-                                                     self.p_att.data_ptr(), st), "decode attention")
+            if i > 0 and self.qkv_slices:  # LayerNorm 1's planes in, c_attn's slices summed by the attention
+                self._qkv_attention(i, attn.c_attn)
+            else:
+                if i == 0:  # the embedding rows: LayerNorm 1 here
+                    self._dl(attn.c_attn, W8, y=self.qkv, x=self.x, ln=block.ln_1)
+                else:       # the previous block left LayerNorm 1's planes
+                    self._dl(attn.c_attn, W8, y=self.qkv, planes_in=self.p_ln1)
+                _lib.check(L.tiq_decode_attention_planes(self.qkv.data_ptr(), self.qkv.stride(0), B, self.H,
+                                                         self.Hkv, self.hd, self.k[i].data_ptr(),
+                                                         self.v[i].data_ptr(), self.T, self.pos.data_ptr(),
+                                                         self.att.data_ptr(), self.att.stride(0),
+                                                         self.p_att.data_ptr(), st), "decode attention")
             self._dl(attn.c_proj, W8, y=self.x, planes_in=self.p_att, res=self.x, next_ln=block.ln_2,
                      planes_out=self.p_ln2)
             self._dl(mlp.c_fc, W8, planes_in=self.p_ln2, act=_lib.ACT_GELU_TANH, planes_out=self.p_hid)

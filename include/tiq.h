@@ -356,6 +356,29 @@ int tiq_decode_attention_planes(const float* qkv, int64_t ld_qkv, int64_t batch,
                                 int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
                                 float* y, int64_t ldy, uint16_t* planes_out, void* stream);
 
+/* The q, k, v projection and self-attention of one new token per sequence
+ * in one call (model.py:254 c_attn at T = 1, then as tiq_decode_attention_planes):
+ * x_planes are the operand planes of LayerNorm 1's output (planes_out of a
+ * previous tiq_decode_linear with next_ln = ln_1, K = n_embd); w the int8
+ * codes of c_attn (TIQ_WF_INT8, rows of n_embd bytes, or TIQ_WF_INT8_TILED),
+ * scale / bias (bias may be NULL) its per-output fp32 factors, N = (n_head +
+ * 2 n_kv_head) * head_dim outputs. The product runs split over K into fp32
+ * partial slices in the workspace, and the attention kernel sums them for
+ * its head ((sum of the slices) * scale + bias) instead of a reduction
+ * launch; k, v go to the caches at slot *pos, y / planes_out as
+ * tiq_decode_attention_planes (planes_out may be NULL). batch <= 64,
+ * n_embd % 32 == 0, head_dim 64, t_max <= 1024.
+ *   workspace: tiq_decode_qkv_attention_workspace(batch, n_embd, N) bytes,
+ *   16-byte aligned, clobbered; that query returns 0 for a shape the call
+ *   does not support (then use tiq_decode_linear + tiq_decode_attention_planes).
+ * No counterpart in the reference (its attention is a chain of torch ops). */
+size_t tiq_decode_qkv_attention_workspace(int64_t batch, int64_t n_embd, int64_t n_qkv);
+int tiq_decode_qkv_attention(const uint16_t* x_planes, int64_t batch, int64_t n_embd, const void* w, int w_format,
+                             const float* scale, const float* bias, int64_t n_head, int64_t n_kv_head,
+                             int64_t head_dim, float* k_cache, float* v_cache, int64_t t_max, const int64_t* pos,
+                             float* y, int64_t ldy, uint16_t* planes_out, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) elementwise over n fp32
  * values (16-byte aligned; y may alias x): the MLP activation gelu_tanh
  * (model.py:57-75, applied at model.py:354) in one pass instead of the

@@ -705,3 +705,98 @@ def _split_planes(x, dev):
     one = torch.ones(K, device=dev)
     _lib.check(_dl(x, None, M, K, eye, _lib.WF_INT8, one, None, K, None, planes=pl), "identity planes")
     return pl
+
+
+@pytest.mark.parametrize("B,C,H,Hkv,pos,T,tiled", [(32, 1600, 25, 25, 200, 256, True), (32, 1600, 25, 25, 255, 384, False),
+                                                   (8, 768, 12, 12, 130, 256, False), (5, 1024, 16, 16, 0, 128, True),
+                                                   (40, 512, 4, 2, 99, 100, False), (6, 256, 2, 2, 63, 64, True),
+                                                   (64, 1280, 20, 20, 300, 512, True)])
+def test_qkv_attention_slices_equal_projection_then_attention(dev, c_oracle, B, C, H, Hkv, pos, T, tiled):
+    """tiq_decode_qkv_attention (c_attn as split-K slices, summed with scale
+    and bias by the attention kernel) against the two-call chain
+    (tiq_decode_linear to qkv rows, then tiq_decode_attention_planes), and
+    both against float64: the new key / value in the caches, the head outputs
+    and their planes, the untouched slots of the caches."""
+    hd = 64
+    N = (H + 2 * Hkv) * hd
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(B + C + pos)
+    qd, sd, w_hat = _w8(c_oracle, N, C, gen, dev)
+    wd, wf = qd, _lib.WF_INT8
+    if tiled:
+        wd = torch.empty_like(qd)
+        _lib.check(L.tiq_tile_int8(qd.data_ptr(), N, C, qd.stride(0), wd.data_ptr(), _st()), "tile")
+        wf = _lib.WF_INT8_TILED
+    b = 0.1 * torch.randn(N, generator=gen)
+    bd = b.to(dev)
+    x = torch.randn(B, C, generator=gen)
+    pl = _split_planes(x.to(dev), dev)
+    kc = torch.randn(B, Hkv, T, hd, generator=gen)
+    vc = torch.randn(B, Hkv, T, hd, generator=gen)
+    p = torch.tensor([pos], device=dev)
+    # the two-call chain
+    qkv = torch.empty(B, N, device=dev)
+    _lib.check(_dl(None, pl, B, C, wd, wf, sd, bd, N, qkv), "c_attn")
+    ka, va = kc.to(dev), vc.to(dev)
+    ya = torch.empty(B, H * hd, device=dev)
+    pa = torch.zeros(int(L.tiq_decode_planes_bytes(B, H * hd)), dtype=torch.uint8, device=dev)
+    _lib.check(L.tiq_decode_attention_planes(qkv.data_ptr(), N, B, H, Hkv, hd, ka.data_ptr(), va.data_ptr(), T,
+                                             p.data_ptr(), ya.data_ptr(), H * hd, pa.data_ptr(), _st()), "attention")
+    # one call
+    n_ws = int(L.tiq_decode_qkv_attention_workspace(B, C, N))
+    assert n_ws >= B * N * 4
+    ws = torch.full((n_ws,), 0xff, dtype=torch.uint8, device=dev)  # NaN bytes: every slice must be written
+    kb, vb = kc.to(dev), vc.to(dev)
+    yb = torch.empty(B, H * hd, device=dev)
+    pb = torch.zeros_like(pa)
+    _lib.check(L.tiq_decode_qkv_attention(pl.data_ptr(), B, C, wd.data_ptr(), wf, sd.data_ptr(), bd.data_ptr(), H,
+                                          Hkv, hd, kb.data_ptr(), vb.data_ptr(), T, p.data_ptr(), yb.data_ptr(),
+                                          H * hd, pb.data_ptr(), ws.data_ptr(), n_ws, _st()), "qkv attention")
+    torch.cuda.synchronize()
+    # float64 from the same inputs
+    qkv64 = x.double() @ w_hat.double().T + b.double()
+    q64 = qkv64[:, : H * hd].view(B, H, 1, hd)
+    k64 = qkv64[:, H * hd : (H + Hkv) * hd].view(B, Hkv, hd)
+    v64 = qkv64[:, (H + Hkv) * hd :].view(B, Hkv, hd)
+    qkv32 = OL.linear_ref(x, w_hat, b)
+    for got in (kb.cpu()[:, :, pos], ka.cpu()[:, :, pos]):
+        _f64_check(got, qkv32[:, H * hd : (H + Hkv) * hd].view(B, Hkv, hd), k64)
+    _f64_check(vb.cpu()[:, :, pos], qkv32[:, (H + Hkv) * hd :].view(B, Hkv, hd), v64)
+    for c, d in ((kb, kc), (vb, vc)):  # every other slot as it was
+        got = c.cpu()
+        assert torch.equal(got[:, :, :pos], d[:, :, :pos]) and torch.equal(got[:, :, pos + 1 :], d[:, :, pos + 1 :])
+    K64 = torch.cat([kc[:, :, :pos].double(), k64[:, :, None]], 2).repeat_interleave(H // Hkv, dim=1)
+    V64 = torch.cat([vc[:, :, :pos].double(), v64[:, :, None]], 2).repeat_interleave(H // Hkv, dim=1)
+    y64 = (F.softmax((q64 @ K64.transpose(-2, -1)) / math.sqrt(hd), dim=-1) @ V64).view(B, H * hd)
+    err_b = float((yb.cpu().double() - y64).abs().max())
+    err_a = float((ya.cpu().double() - y64).abs().max())
+    assert err_b <= max(2 * err_a, 2e-6), (err_b, err_a)
+    assert (yb - ya).abs().max().item() < 1e-5
+    # the planes are exactly the split of the output rows
+    qo, so, _ = _w8(c_oracle, C, H * hd, gen, dev)
+    r1, r2 = torch.empty(B, C, device=dev), torch.empty(B, C, device=dev)
+    _lib.check(_dl(None, pb, B, H * hd, qo, _lib.WF_INT8, so, None, C, r1), "from planes")
+    _lib.check(_dl(yb, None, B, H * hd, qo, _lib.WF_INT8, so, None, C, r2), "from rows")
+    assert torch.equal(r1, r2)
+
+
+def test_qkv_attention_arguments(dev):
+    """Refused shapes and arguments return before any launch: K not a multiple
+    of 32, more than 64 rows, head_dim other than 64, a workspace short of the
+    query; the query is 0 for an unsupported shape."""
+    L = _lib.lib()
+    assert L.tiq_decode_qkv_attention_workspace(65, 1600, 4800) == 0
+    assert L.tiq_decode_qkv_attention_workspace(32, 1601, 4800) == 0
+    assert L.tiq_decode_qkv_attention_workspace(32, 1600, 4800) > 0
+    buf = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    f = buf.data_ptr()
+    p = torch.zeros(1, dtype=torch.int64, device=dev)
+    args = lambda B, C, hd, ws_bytes, wf=_lib.WF_INT8: (f, B, C, f, wf, f, None, 2, 2, hd, f, f, 16, p.data_ptr(), f,
+                                                         128, None, f, ws_bytes, _st())
+    assert L.tiq_decode_qkv_attention(*args(4, 100, 64, 1 << 16)) == L.tiq_decode_qkv_attention(*args(4, 100, 64, 0))
+    assert L.tiq_decode_qkv_attention(*args(4, 100, 64, 1 << 16)) == -4  # TIQ_EUNSUPPORTED
+    assert L.tiq_decode_qkv_attention(*args(65, 128, 64, 1 << 16)) == -4
+    assert L.tiq_decode_qkv_attention(*args(4, 128, 32, 1 << 16)) == -4
+    assert L.tiq_decode_qkv_attention(*args(4, 128, 64, 16, _lib.WF_F32)) == -4
+    assert L.tiq_decode_qkv_attention(*args(4, 128, 64, 16)) == -5  # TIQ_EWORKSPACE
+    assert L.tiq_decode_qkv_attention(*args(0, 128, 64, 0)) == 0
