@@ -93,19 +93,28 @@ __global__ __launch_bounds__(64 * kAttWaves) __attribute__((amdgpu_waves_per_eu(
     float* kb = kc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
     float* vb = vc + ((int64_t)b * Hkv + hk) * t_max * kHeadDim;
 
+    const int off0 = ((kSlotsPerWave * wave + row) * kHeadDim + d4) * 4;
+    auto slot_off = [&](int base, int i) { return off0 + (base + 4 * i) * kHeadDim * 4; };
+    // The keys of the first chunk need no position: requested at launch through
+    // a descriptor over the first min(t_max, 128) slots (a key past pos gets no
+    // score stored), so the read of pos below overlaps them.
+    float4 kr[NCH][NI], vr[NCH][NI];
+    {
+        const int first = (WHOLE ? t_max : min(t_max, 128)) * kHeadDim * 4;
+        const __amdgpu_buffer_rsrc_t rk0 = __builtin_amdgcn_make_buffer_rsrc(kb, (short)0, first, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) kr[0][i] = cache_load(rk0, slot_off(0, i));
+    }
+    asm volatile("" ::: "memory");  // keep the read of pos (and its wait) behind those loads
     int64_t pos_in = 0;
-    if constexpr (!WHOLE) pos_in = *pos_p;  // the descriptors need it
+    if constexpr (!WHOLE) pos_in = *pos_p;  // the other descriptors need it
     // bytes of slots 0 .. pos - 1 (0 for a position outside the cache)
     const int valid =
         WHOLE ? t_max * kHeadDim * 4 : (pos_in < 0 || pos_in >= t_max ? 0 : (int)pos_in * kHeadDim * 4);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kb, (short)0, valid, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vb, (short)0, valid, 0x00020000);
-    const int off0 = ((kSlotsPerWave * wave + row) * kHeadDim + d4) * 4;
-    auto slot_off = [&](int base, int i) { return off0 + (base + 4 * i) * kHeadDim * 4; };
-
-    float4 kr[NCH][NI], vr[NCH][NI];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+    for (int c = 1; c < NCH; ++c)
 #pragma unroll
         for (int i = 0; i < NI; ++i) kr[c][i] = cache_load(rk, slot_off(128 * c, i));
     if constexpr (NCH == 1) {  // one chunk: its values too, one trip to memory
@@ -209,12 +218,13 @@ __global__ __launch_bounds__(64 * kAttWaves) __attribute__((amdgpu_waves_per_eu(
 
     // ---- weighted sum of values: this lane's 4 dims over its slots ----
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    auto add = [&](int t, const float4& v) {
-        const float p = t < pos ? sc[t] : 0.f;
-        acc.x = fmaf(p, v.x, acc.x);
-        acc.y = fmaf(p, v.y, acc.y);
-        acc.z = fmaf(p, v.z, acc.z);
-        acc.w = fmaf(p, v.w, acc.w);
+    auto add = [&](int t, const float4& v) {  // a slot past pos adds nothing, whatever the memory holds
+        const bool in = t < pos;
+        const float p = in ? sc[t] : 0.f;
+        acc.x = in ? fmaf(p, v.x, acc.x) : acc.x;
+        acc.y = in ? fmaf(p, v.y, acc.y) : acc.y;
+        acc.z = in ? fmaf(p, v.z, acc.z) : acc.z;
+        acc.w = in ? fmaf(p, v.w, acc.w) : acc.w;
     };
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
