@@ -306,6 +306,35 @@ def test_decode_attention(dev, B, H, Hkv, pos, T):
     assert torch.equal(kd.cpu()[:, :, pos + 1 :], kc[:, :, pos + 1 :])
 
 
+@pytest.mark.parametrize("B,H,pos,T", [(2, 4, 5, 64), (2, 4, 130, 256), (32, 25, 40, 256), (32, 25, 200, 256)])
+def test_decode_attention_ignores_memory_past_pos(dev, B, H, pos, T):
+    """Cache slots past pos hold NaN (memory never written): the output is the
+    attention over slots 0..pos only, for the whole-cache kernel (small caches
+    read every slot) and the filled-slot one (batch 32: the first 128 slots'
+    keys are requested before pos is known)."""
+    hd = 64
+    gen = torch.Generator().manual_seed(B * 1000 + pos)
+    qkv = torch.randn(B, 3 * H * hd, generator=gen)
+    kc = torch.full((B, H, T, hd), float("nan"))
+    vc = torch.full((B, H, T, hd), float("nan"))
+    kc[:, :, :pos] = torch.randn(B, H, pos, hd, generator=gen)
+    vc[:, :, :pos] = torch.randn(B, H, pos, hd, generator=gen)
+    kd, vd = kc.to(dev), vc.to(dev)
+    p = torch.tensor([pos], device=dev)
+    y = torch.empty(B, H * hd, device=dev)
+    rc = _lib.lib().tiq_decode_attention(qkv.to(dev).data_ptr(), 3 * H * hd, B, H, H, hd, kd.data_ptr(),
+                                         vd.data_ptr(), T, p.data_ptr(), y.data_ptr(), H * hd, _st())
+    _lib.check(rc, "attention")
+    q = qkv[:, : H * hd].view(B, H, 1, hd)
+    kc[:, :, pos] = qkv[:, H * hd : 2 * H * hd].view(B, H, hd)
+    vc[:, :, pos] = qkv[:, 2 * H * hd :].view(B, H, hd)
+    K, V = kc[:, :, : pos + 1], vc[:, :, : pos + 1]
+    ref = (F.softmax((q @ K.transpose(-2, -1)) / math.sqrt(hd), dim=-1) @ V).view(B, H * hd)
+    out = y.cpu()
+    assert torch.isfinite(out).all()
+    assert (out - ref).abs().max() < 2e-5
+
+
 @pytest.mark.parametrize("B,H,T", [(1, 2, 16), (32, 25, 256)])
 def test_out_of_range_position_gives_nan_without_writes(dev, B, H, T):
     """A position outside the cache writes nothing and flags every output row
