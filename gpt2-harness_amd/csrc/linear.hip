@@ -331,6 +331,7 @@ extern "C" int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, 
 }
 
 extern "C" size_t tiq_decode_linear_workspace(int w_format, int64_t M, int64_t K, int64_t N) {
+    if (w_format == TIQ_WF_F32_TILED) return 0;  // planes in only: nothing staged
     if ((w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT8_TILED && w_format != TIQ_WF_F32) ||
         M < kSkinnyMinRows || M > 64 || K <= 0 ||
         K % 32 != 0 || N <= 0)
@@ -341,6 +342,12 @@ extern "C" size_t tiq_decode_linear_workspace(int w_format, int64_t M, int64_t K
 extern "C" int tiq_tile_int8(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* tiles, void* stream) {
     return launch_tile_int8(reinterpret_cast<const uint8_t*>(w), N, K, ldw, reinterpret_cast<uint8_t*>(tiles),
                             as_stream(stream));
+}
+
+extern "C" size_t tiq_tile_f32_bytes(int64_t N, int64_t K) { return tile_f32_bytes(N, K); }
+
+extern "C" int tiq_tile_f32(const float* w, int64_t N, int64_t K, int64_t ldw, float* tiles, void* stream) {
+    return launch_tile_f32(w, N, K, ldw, tiles, as_stream(stream));
 }
 
 extern "C" size_t tiq_decode_planes_bytes(int64_t M, int64_t K) {
@@ -404,12 +411,15 @@ extern "C" int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_
                                  int activation, const float* residual, int64_t ld_residual,
                                  const float* next_ln_weight, const float* next_ln_bias, float next_ln_eps,
                                  uint16_t* planes_out, void* workspace, size_t workspace_bytes, void* stream) {
-    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT8_TILED && w_format != TIQ_WF_F32) return TIQ_EUNSUPPORTED;
+    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT8_TILED && w_format != TIQ_WF_F32 &&
+        w_format != TIQ_WF_F32_TILED)
+        return TIQ_EUNSUPPORTED;
     if (activation != TIQ_ACT_NONE && activation != TIQ_ACT_GELU_TANH) return TIQ_EINVAL;
     if ((ln_weight == nullptr) != (ln_bias == nullptr)) return TIQ_EINVAL;
     if (M < 0 || K < 0 || N < 0) return TIQ_EINVAL;
     if (M == 0 || N == 0) return TIQ_OK;
-    if (!w || (w_format != TIQ_WF_F32 && !scale)) return TIQ_EINVAL;
+    const bool f32w = w_format == TIQ_WF_F32 || w_format == TIQ_WF_F32_TILED;
+    if (!w || (!f32w && !scale)) return TIQ_EINVAL;
     if (x_planes && ln_weight) return TIQ_EINVAL;  // planes already carry their LayerNorm
     if (!x_planes && (!x || ldx < K)) return TIQ_EINVAL;
     if (y && ldy < N) return TIQ_EINVAL;

@@ -23,6 +23,7 @@
 //     computed over the workgroup's activation rows, which needs K covered by
 //     one workgroup (at most 2048 with 8 wavefronts of 8 units).
 #include <algorithm>
+#include <utility>
 
 #include "tiq_internal.hpp"
 
@@ -788,6 +789,116 @@ __global__ __launch_bounds__(kWaves * 64, 1) void split_product_kernel(const uin
     }
 }
 
+template <int... J, typename F>
+__device__ __forceinline__ void for_each_slot(std::integer_sequence<int, J...>, F&& f) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+
+// The fp32 head of a batched decode (a 50257 x K tied embedding, far more
+// rows than one round of workgroups) from the previous call's operand planes:
+// one workgroup per CU loops over the 32-row weight tiles t = blockIdx.x +
+// i gridDim.x of its row tile (blockIdx.y); its wavefronts split each tile's
+// K into the same unit ranges as skinny_kernel and stream (weights, planes)
+// units through a ring of kStreamSlots register slots that runs on across
+// tile boundaries, so the next tile's weights are in flight while a tile's
+// partial sums are reduced and stored (skinny_kernel holds one workgroup a CU
+// and loads a whole tile before computing). Weights in the tiles of
+// tile_f32 (1 KB of consecutive memory per load instruction, nontemporal).
+// Per unit: the six plane products of the fp32 weights and activations as in
+// skinny_kernel, in the same order, and the same fixed-order reduction over
+// the wavefronts: the outputs equal skinny_kernel's bit for bit.
+// Each wavefront reaches the per-tile barriers once per tile of its
+// workgroup whatever its unit count (every wavefront holds >= 1 unit).
+constexpr int kStreamSlots = 4;
+__global__ __launch_bounds__(kWaves * 64, 1) void stream_f32_kernel(const uint16_t* __restrict__ x3, int M, int K,
+                                                                   const uint8_t* __restrict__ wt, int N,
+                                                                   float* __restrict__ y, int64_t ldy) {
+    constexpr int D = kStreamSlots;
+    __shared__ float red[kWaves][32][33];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+    const int U = K / 32, m0 = blockIdx.y * 32;
+    const int u0 = wave * U / kWaves, cnt = (wave + 1) * U / kWaves - u0;  // >= 1 (the host checks U >= 8)
+    const int T = (N + 31) / 32, G = gridDim.x;
+    const int n_my = (T - (int)blockIdx.x + G - 1) / G;  // tiles blockIdx.x + i G < T
+    const int L = n_my * cnt;
+    const bool xrow_ok = m0 + r < M;
+    const uint16_t* x3t = x3 + (int64_t)blockIdx.y * U * 6 * 64 * 8 + lane * 8;
+    const uint8_t* wl = wt + lane * 16;
+    u32x4 wring[D][4];
+    u32x4 xring[D][3][2];
+    auto issue = [&](int s, auto slot) __attribute__((always_inline)) {
+        constexpr int j = decltype(slot)::value;
+        const int i = s / cnt, u = u0 + (s - i * cnt);
+        const uint8_t* wb = wl + ((int64_t)((int)blockIdx.x + i * G) * U + u) * 4096;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            wring[j][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + 1024 * q));
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                xring[j][q][e] = *reinterpret_cast<const u32x4*>(x3t + (((int64_t)u * 3 + q) * 2 + e) * 64 * 8);
+    };
+    floatx16 acc;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+    auto step = [&](int s, auto slot) __attribute__((always_inline)) {
+        constexpr int j = decltype(slot)::value;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            bf16x8 xq[3];
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                u32x4 tq = xring[j][q][e];
+                if (!xrow_ok) tq = u32x4{0u, 0u, 0u, 0u};
+                xq[q] = __builtin_bit_cast(bf16x8, tq);
+            }
+            float wf[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wf[i] = __uint_as_float(wring[j][2 * e + i / 4][i % 4]);
+            bf16x8 w0, w1, w2;
+            split3(wf, w0, w1, w2);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, xq[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, xq[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, xq[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, xq[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, xq[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w2, xq[0], acc, 0, 0, 0);
+        }
+        if (s + D < L) issue(s + D, slot);  // the slot's next unit, possibly of the next tile
+        const int i = s / cnt;
+        if (s - i * cnt == cnt - 1) {  // this wavefront's share of tile i is summed
+#pragma unroll
+            for (int q = 0; q < 16; ++q) red[wave][r][8 * (q >> 2) + 4 * h + (q & 3)] = acc[q];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+            __syncthreads();
+            const int n0 = 32 * ((int)blockIdx.x + i * G);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {  // 1024 outputs, two per thread, wavefront order
+                const int o = threadIdx.x + kWaves * 64 * tt;
+                const int m = o >> 5, nn = o & 31;
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) v += red[w][m][nn];
+                if (m0 + m < M && n0 + nn < N) y[(int64_t)(m0 + m) * ldy + n0 + nn] = v;
+            }
+            __syncthreads();  // red is free for the next tile
+        }
+    };
+    for_each_slot(std::make_integer_sequence<int, D>{}, [&](auto slot) __attribute__((always_inline)) {
+        if (decltype(slot)::value < L) issue(decltype(slot)::value, slot);
+    });
+    int s0 = 0;
+    for (; s0 + D <= L; s0 += D)
+        for_each_slot(std::make_integer_sequence<int, D>{},
+                      [&](auto slot) __attribute__((always_inline)) { step(s0 + decltype(slot)::value, slot); });
+    for_each_slot(std::make_integer_sequence<int, D>{}, [&](auto slot) __attribute__((always_inline)) {
+        if (s0 + decltype(slot)::value < L) step(s0 + decltype(slot)::value, slot);
+    });
+}
+
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 // Workspace: the split activation planes, row tiles x 32 x 3K bf16 in operand order.
@@ -952,8 +1063,25 @@ size_t decode_linear_workspace(int64_t M, int64_t K, int64_t N) {
 
 size_t decode_planes_bytes(int64_t M, int64_t K) { return planes_bytes(M, K); }
 
+// fp32 tiles (the head): planes in, fp32 rows out, nothing fused
+static int run_decode_f32_tiles(const LinearArgs& a, const uint16_t* x_planes, const float* next_ln_w,
+                         uint16_t* planes_out) {
+    if (a.M < 1 || a.M > 64 || a.K <= 0 || a.K % 32 != 0 || a.K / 32 < kWaves || a.N <= 0 ||
+        a.N > 0x7fffffff - 31 || a.ldy > 0x7fffffff)
+        return TIQ_EUNSUPPORTED;
+    if (!x_planes || a.bias || a.fuse.act || a.fuse.res || next_ln_w || planes_out) return TIQ_EUNSUPPORTED;
+    if (!a.y || !a.w) return TIQ_EINVAL;
+    if (!aligned(a.w, 16) || !aligned(x_planes, 16)) return TIQ_EALIGN;
+    const int64_t T = (a.N + 31) / 32;
+    const dim3 grid((unsigned)std::min<int64_t>(T, 256), (unsigned)((a.M + 31) / 32));
+    hipLaunchKernelGGL(stream_f32_kernel, grid, dim3(kWaves * 64), 0, a.stream, x_planes, (int)a.M, (int)a.K, a.w,
+                       (int)a.N, static_cast<float*>(a.y), a.ldy);
+    return launch_status();
+}
+
 int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float* next_ln_w,
                       const float* next_ln_b, float next_eps, uint16_t* planes_out) {
+    if (a.fmt == kF32T) return run_decode_f32_tiles(a, x_planes, next_ln_w, planes_out);
     if (a.fmt != kW8 && a.fmt != kW8T && a.fmt != kF32) return TIQ_EUNSUPPORTED;
     if (a.M < kSkinnyMinRows || a.M > 64 || a.K <= 0 || a.K % 32 != 0 || a.N <= 0 || a.N > 0x7fffffff)
         return TIQ_EUNSUPPORTED;
@@ -1086,6 +1214,38 @@ int launch_tile_int8(const uint8_t* w, int64_t N, int64_t K, int64_t ldw, uint8_
     const int64_t nchunks = N * K / 16;
     hipLaunchKernelGGL(tile_int8_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, stream, w, ldw, K / 32,
                        nchunks, tiles);
+    return launch_status();
+}
+
+// One thread per 16 bytes of the fp32 tiles: block b = (t, u) of
+// (ceil(N / 32), K / 32), chunk c = 64 q + l of the block holds row 32 t + l % 32,
+// columns 32 u + 16 (l / 32) + 4 q .. + 3 (zeros for rows past N).
+__global__ __launch_bounds__(256) void tile_f32_kernel(const float* __restrict__ w, int64_t ldw, int64_t N,
+                                                       int64_t U, int64_t nchunks, float* __restrict__ tiles) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nchunks) return;
+    const int64_t b = i >> 8, t = b / U, u = b - t * U;
+    const int c = (int)(i & 255), q = c >> 6, l = c & 63, r = l & 31, h = l >> 5;
+    const int64_t row = 32 * t + r;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < N) v = *reinterpret_cast<const float4*>(w + row * ldw + 32 * u + 16 * h + 4 * q);
+    reinterpret_cast<float4*>(tiles)[i] = v;
+}
+
+size_t tile_f32_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || K % 32 != 0) return 0;
+    return (size_t)((N + 31) / 32) * 32 * (size_t)K * 4;
+}
+
+int launch_tile_f32(const float* w, int64_t N, int64_t K, int64_t ldw, float* tiles, hipStream_t stream) {
+    if (N < 0 || K < 0) return TIQ_EINVAL;
+    if (N == 0 || K == 0) return TIQ_OK;
+    if (!w || !tiles || ldw < K) return TIQ_EINVAL;
+    if (K % 32 != 0) return TIQ_EUNSUPPORTED;
+    if (!aligned(w, 16) || !aligned(tiles, 16) || ldw % 4 != 0) return TIQ_EALIGN;
+    const int64_t nchunks = (int64_t)(tile_f32_bytes(N, K) / 16);
+    hipLaunchKernelGGL(tile_f32_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, stream, w, ldw, N,
+                       K / 32, nchunks, tiles);
     return launch_status();
 }
 

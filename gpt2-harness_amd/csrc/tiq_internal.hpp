@@ -12,6 +12,7 @@ enum WFormat : int {
     kW4G = 2,  // group-wise nibbles, row n at byte n * ((K + 1) / 2), fp16 group scales
     kF32 = 3,  // fp32 weights (an unquantized Linear such as the tied lm_head), no scale
     kW8T = 4,  // int8 codes in 32 x 32 operand tiles (tiq_tile_int8; batched decode only)
+    kF32T = 5, // fp32 weights in 32 x 32 operand tiles (tiq_tile_f32; the batched decode head)
 };
 
 // Optional work fused around a decode GEMV: LayerNorm of the activation rows
@@ -88,6 +89,12 @@ int run_decode_linear(const LinearArgs& a, const uint16_t* x_planes, const float
 // count of 32-row tiles, else K <= 8192), the operand planes of a previous
 // decode linear in.
 constexpr int64_t kMaxSlices = 4;
+
+// fp32 weights in operand tiles (skinny.hip): ceil(N / 32) x (K / 32) blocks
+// of 4 KB, rows past N zero; byte 1024 q + 16 l + 4 j of block (t, u) holds
+// w[32 t + l % 32][32 u + 16 (l / 32) + 4 q + j].
+size_t tile_f32_bytes(int64_t N, int64_t K);
+int launch_tile_f32(const float* w, int64_t N, int64_t K, int64_t ldw, float* tiles, hipStream_t stream);
 int64_t decode_slices_count(int64_t M, int64_t K, int64_t N);
 size_t decode_slices_bytes(int64_t M, int64_t K, int64_t N);  // 0: shape not supported
 int launch_decode_slices(const LinearArgs& a, const uint16_t* x_planes, float* part);

@@ -53,6 +53,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_decode_linear_workspace": ([_i32, _i64, _i64, _i64], _sz),
     "tiq_decode_planes_bytes": ([_i64, _i64], _sz),
     "tiq_tile_int8": ([_vp, _i64, _i64, _i64, _vp, _vp], _i32),
+    "tiq_tile_f32_bytes": ([_i64, _i64], _sz),
+    "tiq_tile_f32": ([_vp, _i64, _i64, _i64, _vp, _vp], _i32),
     "tiq_decode_linear": ([_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _f32, _i32,
                            _vp, _i64, _vp, _vp, _f32, _vp, _vp, _sz, _vp], _i32),
     "tiq_decode_linear_noalloc": ([_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _f32,
@@ -71,7 +73,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _vp], _i32),
 }
 
-WF_INT8, WF_INT4, WF_INT4G, WF_F32, WF_INT8_TILED = 0, 1, 2, 3, 4
+WF_INT8, WF_INT4, WF_INT4G, WF_F32, WF_INT8_TILED, WF_F32_TILED = 0, 1, 2, 3, 4, 5
 ACT_NONE, ACT_GELU_TANH = 0, 1
 
 _LIB: ctypes.CDLL | None = None

@@ -262,6 +262,15 @@ class FusedDecoder(_DecoderBase):
                                            lin.codes.stride(0), t.data_ptr(),
                                            torch.cuda.current_stream(dev).cuda_stream), "tile int8 codes")
                 self.tiles[id(lin)] = t
+            # the fp32 head (the tied embedding) in 4 KB operand tiles, which
+            # the decode linear streams with one workgroup per CU (the
+            # row-major weights stay for the embedding and the prefill)
+            V = cfg.vocab_size
+            if self.head_q is None and C % 32 == 0 and C >= 256:
+                t = torch.empty(int(L.tiq_tile_f32_bytes(V, C)) // 4, dtype=torch.float32, device=dev)
+                _lib.check(L.tiq_tile_f32(self.head_w.data_ptr(), V, C, self.head_w.stride(0), t.data_ptr(),
+                                          torch.cuda.current_stream(dev).cuda_stream), "tile fp32 head")
+                self.tiles[id(model.lm_head)] = t
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
@@ -286,7 +295,7 @@ class FusedDecoder(_DecoderBase):
         w = lin.codes if isinstance(lin, QuantLinear) else self.head_w
         tiles = getattr(self, "tiles", {}).get(id(lin))
         if tiles is not None:
-            w, wf = tiles, _lib.WF_INT8_TILED
+            w, wf = tiles, (_lib.WF_F32_TILED if wf == _lib.WF_F32 else _lib.WF_INT8_TILED)
         scale = lin.scale.data_ptr() if isinstance(lin, QuantLinear) else None
         bias = _lib.ptr(lin.bias) if isinstance(lin, QuantLinear) else None
         rc = self.L.tiq_decode_linear(

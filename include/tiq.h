@@ -49,6 +49,8 @@ enum tiq_weight_format {
     TIQ_WF_F32 = 3,
     /* int8 codes rearranged by tiq_tile_int8 (tiq_decode_linear only) */
     TIQ_WF_INT8_TILED = 4,
+    /* fp32 weights rearranged by tiq_tile_f32 (tiq_decode_linear from planes only) */
+    TIQ_WF_F32_TILED = 5,
 };
 
 /* Activations fused after a linear. */
@@ -307,6 +309,23 @@ size_t tiq_decode_planes_bytes(int64_t M, int64_t K);
  * (TIQ_WF_INT8): the products are the same, in the same order. No
  * counterpart in the reference (a device layout of this library). */
 int tiq_tile_int8(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* tiles, void* stream);
+
+/* The fp32 weights of an (N, K) unquantized Linear (the tied lm_head,
+ * model.py:585; leading dimension ldw floats, 16-byte aligned rows)
+ * rearranged for tiq_decode_linear with w_format TIQ_WF_F32_TILED:
+ * tiq_tile_f32_bytes(N, K) bytes (ceil(N / 32) * 32 rows, rows past N zero)
+ * in 4 KB blocks, block t * (K / 32) + u holding rows 32 t .. 32 t + 31 and
+ * columns 32 u .. 32 u + 31, byte 1024 q + 16 l + 4 j of the block being
+ * w[32 t + l % 32][32 u + 16 (l / 32) + 4 q + j], so each 64-lane load of
+ * the product reads 1 KB of consecutive memory. Needs K % 32 == 0. With those
+ * tiles tiq_decode_linear takes only operand planes in (x_planes, 1..64 rows,
+ * K >= 256) and writes only the fp32 rows y (no bias, activation, residual or
+ * planes out); it streams the tiles with one workgroup per CU looping over
+ * them and gives the same results, bit for bit, as TIQ_WF_F32 on the
+ * row-major weights. No counterpart in the reference (a device layout of
+ * this library). */
+size_t tiq_tile_f32_bytes(int64_t N, int64_t K);
+int tiq_tile_f32(const float* w, int64_t N, int64_t K, int64_t ldw, float* tiles, void* stream);
 int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int64_t M, int64_t K, const void* w,
                       int w_format, const float* scale, const float* bias, int64_t N, float* y, int64_t ldy,
                       const float* ln_weight, const float* ln_bias, float ln_eps, int activation,

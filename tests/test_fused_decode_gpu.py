@@ -829,3 +829,64 @@ def test_qkv_attention_arguments(dev):
     assert L.tiq_decode_qkv_attention(*args(4, 128, 64, 16, _lib.WF_F32)) == -4
     assert L.tiq_decode_qkv_attention(*args(4, 128, 64, 16)) == -5  # TIQ_EWORKSPACE
     assert L.tiq_decode_qkv_attention(*args(0, 128, 64, 0)) == 0
+
+
+@pytest.mark.parametrize("N,K,ldw", [(100, 64, 64), (64, 256, 260), (50257, 768, 768)])
+def test_tile_f32_layout(dev, N, K, ldw):
+    """tiq_tile_f32: block (t, u) of 4 KB holds rows 32 t .. 32 t + 31 and columns
+    32 u .. 32 u + 31, chunk 64 q + l the 4 floats w[32 t + l % 32][32 u +
+    16 (l / 32) + 4 q ..]; rows past N are zero; a padded leading dimension."""
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(N + K)
+    w = torch.randn(N, ldw, generator=gen)
+    n_bytes = int(L.tiq_tile_f32_bytes(N, K))
+    T, U = (N + 31) // 32, K // 32
+    assert n_bytes == T * 32 * K * 4
+    t = torch.full((n_bytes // 4,), float("nan"), device=dev)
+    _lib.check(L.tiq_tile_f32(w.to(dev).data_ptr(), N, K, ldw, t.data_ptr(), _st()), "tile f32")
+    wp = torch.zeros(T * 32, K)
+    wp[:N] = w[:, :K]
+    want = wp.view(T, 32, U, 2, 4, 4).permute(0, 2, 4, 3, 1, 5).reshape(-1)
+    assert torch.equal(t.cpu(), want)
+
+
+def test_tile_f32_errors(dev):
+    L = _lib.lib()
+    w = torch.zeros(64, 64, device=dev)
+    t = torch.zeros(64 * 64, device=dev)
+    assert L.tiq_tile_f32(w.data_ptr(), 64, 48, 64, t.data_ptr(), _st()) == -4  # K % 32
+    assert L.tiq_tile_f32(w.data_ptr(), 64, 64, 40, t.data_ptr(), _st()) == -1  # ldw < K
+    assert L.tiq_tile_f32(w.data_ptr(), 64, 64, 66, t.data_ptr(), _st()) == -3  # rows not 16-byte aligned
+    assert L.tiq_tile_f32_bytes(64, 48) == 0
+
+
+@pytest.mark.parametrize("M", [5, 32, 40, 64])
+@pytest.mark.parametrize("K,N", [(768, 50257), (1600, 5003), (256, 1000), (1600, 64)])
+def test_decode_linear_f32_tiles(dev, M, K, N):
+    """The fp32 head from operand planes with tiled weights (one workgroup per
+    CU streaming the tiles): bit-identical to the row-major weights' one-split
+    product where that path takes one split, and to float64 within the fp32
+    bar everywhere; workspace 0; the refused fusions."""
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(M + K + N)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen)
+    wd = w.to(dev)
+    t = torch.empty(int(L.tiq_tile_f32_bytes(N, K)) // 4, device=dev)
+    _lib.check(L.tiq_tile_f32(wd.data_ptr(), N, K, K, t.data_ptr(), _st()), "tile f32")
+    pl = _split_planes(x.to(dev), dev)
+    assert L.tiq_decode_linear_workspace(_lib.WF_F32_TILED, M, K, N) == 0
+    yt = torch.full((M, N), float("nan"), device=dev)
+    _lib.check(_dl(None, pl, M, K, t, _lib.WF_F32_TILED, None, None, N, yt), "tiled head")
+    yr = torch.empty(M, N, device=dev)
+    _lib.check(_dl(None, pl, M, K, wd, _lib.WF_F32, None, None, N, yr), "row-major head")
+    if N % 8 != 0 or N > 8192:  # the row-major path takes one split there: same products, same order
+        assert torch.equal(yt, yr)
+    _f64_check(yt, x @ w.T, x.double() @ w.double().T)
+    # refused: fp32 rows in, a bias, planes out
+    assert _dl(x.to(dev), None, M, K, t, _lib.WF_F32_TILED, None, None, N, yt) == -4
+    b = torch.zeros(N, device=dev)
+    assert _dl(None, pl, M, K, t, _lib.WF_F32_TILED, None, b, N, yt) == -4
+    if N % 32 == 0:
+        po = torch.zeros(int(L.tiq_decode_planes_bytes(M, N)), dtype=torch.uint8, device=dev)
+        assert _dl(None, pl, M, K, t, _lib.WF_F32_TILED, None, None, N, yt, planes=po) == -4
