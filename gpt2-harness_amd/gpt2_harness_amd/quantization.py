@@ -494,34 +494,35 @@ def perplexity_with_error_bars(
     returning ``(x, y)`` id tensors, as the reference's ``TokenDataset`` or
     :class:`SyntheticTokenStream`. The forward passes (prefill-shaped Linears,
     ``M = batch_size * block_size``) and the summed cross entropy run on the
-    GPU; only one scalar per batch comes back to the host.
+    GPU; the chunk sums come back to the host once, after the last batch.
     """
     model = model.to(device).eval()
     batches = dataset.sequential_batches("val", batch_size=batch_size, limit=n_chunks * batches_per_chunk)
-    chunk_losses: list[float] = []
-    for c in range(0, len(batches), batches_per_chunk):
-        group = batches[c : c + batches_per_chunk]
-        if not group:
-            continue
-        total, n = 0.0, 0
-        for x, y in group:
-            logits = model(x.to(device))["logits"].float()
-            y = y.to(logits.device)
-            total += float(F.cross_entropy(logits.reshape(-1, logits.size(-1)), y.reshape(-1), reduction="sum"))
-            n += y.numel()
-        chunk_losses.append(total / n)
-    mean = statistics.fmean(chunk_losses)
-    std = statistics.stdev(chunk_losses) if len(chunk_losses) > 1 else 0.0
-    ppls = [math.exp(v) for v in chunk_losses]
-    return {
-        "loss_mean": mean,
-        "loss_std": std,
-        "ppl_mean": statistics.fmean(ppls),
-        "ppl_std": statistics.stdev(ppls) if len(ppls) > 1 else 0.0,
-        "ppl_of_mean_loss": math.exp(mean),
-        "n_chunks": len(chunk_losses),
-        "chunk_losses": chunk_losses,
-    }
+    # chunk c = batches [c * batches_per_chunk, (c + 1) * batches_per_chunk): its
+    # loss is the token mean of the summed cross entropy; the per-chunk sums
+    # stay on the device (fp64) and come back in one transfer at the end
+    n_chunk = -(-len(batches) // batches_per_chunk)
+    sums = torch.zeros(n_chunk, dtype=torch.float64, device=device)
+    tokens = [0] * n_chunk
+    for i, (x, y) in enumerate(batches):
+        logits = model(x.to(device))["logits"].float()
+        nll = F.cross_entropy(logits.flatten(0, -2), y.to(logits.device).flatten(), reduction="sum")
+        sums[i // batches_per_chunk] += nll.double()
+        tokens[i // batches_per_chunk] += y.numel()
+    losses = [s / n for s, n in zip(sums.tolist(), tokens)]
+    return _chunk_spread(losses)
+
+
+def _chunk_spread(losses: list[float]) -> dict[str, Any]:
+    """Mean and sample standard deviation of the chunk losses and of their
+    perplexities (the keys of ``quantization.py:305-313``)."""
+    def sd(v: list[float]) -> float:
+        return statistics.stdev(v) if len(v) > 1 else 0.0
+
+    ppls = [math.exp(v) for v in losses]
+    mean = statistics.fmean(losses)
+    return {"loss_mean": mean, "loss_std": sd(losses), "ppl_mean": statistics.fmean(ppls), "ppl_std": sd(ppls),
+            "ppl_of_mean_loss": math.exp(mean), "n_chunks": len(losses), "chunk_losses": losses}
 
 
 @dataclass

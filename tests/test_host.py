@@ -11,6 +11,7 @@
 from __future__ import annotations
 
 import hashlib
+import math
 import re
 from pathlib import Path
 
@@ -221,3 +222,22 @@ def test_paired_loss_delta():
     assert not paired_loss_delta([1.0, 1.2], [1.1, 1.1])["distinguishable"]   # mean 0
     with pytest.raises(ValueError):
         paired_loss_delta([1.0], [1.0, 2.0])
+
+
+def test_chunk_spread_statistics():
+    """The spread of perplexity_with_error_bars: mean and sample standard
+    deviation of the chunk losses and of exp(loss), and exp(mean loss)."""
+    from gpt2_harness_amd.quantization import _chunk_spread
+
+    d = _chunk_spread([1.0, 2.0, 4.0])
+    mean = 7.0 / 3.0
+    sd = math.sqrt(((1 - mean) ** 2 + (2 - mean) ** 2 + (4 - mean) ** 2) / 2)
+    p = [math.exp(1.0), math.exp(2.0), math.exp(4.0)]
+    pm = sum(p) / 3
+    psd = math.sqrt(sum((v - pm) ** 2 for v in p) / 2)
+    assert d["n_chunks"] == 3 and d["chunk_losses"] == [1.0, 2.0, 4.0]
+    assert abs(d["loss_mean"] - mean) < 1e-12 and abs(d["loss_std"] - sd) < 1e-12
+    assert abs(d["ppl_mean"] - pm) < 1e-9 and abs(d["ppl_std"] - psd) < 1e-9
+    assert abs(d["ppl_of_mean_loss"] - math.exp(mean)) < 1e-9
+    one = _chunk_spread([0.5])
+    assert one["loss_std"] == 0.0 and one["ppl_std"] == 0.0 and one["ppl_mean"] == math.exp(0.5)
