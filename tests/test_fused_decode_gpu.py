@@ -890,3 +890,30 @@ def test_decode_linear_f32_tiles(dev, M, K, N):
     if N % 32 == 0:
         po = torch.zeros(int(L.tiq_decode_planes_bytes(M, N)), dtype=torch.uint8, device=dev)
         assert _dl(None, pl, M, K, t, _lib.WF_F32_TILED, None, None, N, yt, planes=po) == -4
+
+
+@pytest.mark.parametrize("B,C,H,T", [(8, 768, 12, 64), (32, 1600, 25, 256)])
+def test_qkv_attention_out_of_range_position(dev, c_oracle, B, C, H, T):
+    """A position outside the cache through the fused q, k, v call: NaN output
+    rows and planes' rows, nothing written to either cache (both the whole-cache
+    kernel and the filled-slot one, whose first keys go out before pos is read)."""
+    hd = 64
+    N = 3 * H * hd
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(C + T)
+    qd, sd, _ = _w8(c_oracle, N, C, gen, dev)
+    pl = _split_planes(torch.randn(B, C, generator=gen).to(dev), dev)
+    kc = torch.randn(B, H, T, hd, generator=gen).to(dev)
+    vc = torch.randn(B, H, T, hd, generator=gen).to(dev)
+    k0, v0 = kc.clone(), vc.clone()
+    n_ws = int(L.tiq_decode_qkv_attention_workspace(B, C, N))
+    ws = torch.empty(n_ws, dtype=torch.uint8, device=dev)
+    y = torch.zeros(B, H * hd, device=dev)
+    for bad in (T, T + 3, -1):
+        p = torch.tensor([bad], device=dev)
+        _lib.check(L.tiq_decode_qkv_attention(pl.data_ptr(), B, C, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None,
+                                              H, H, hd, kc.data_ptr(), vc.data_ptr(), T, p.data_ptr(), y.data_ptr(),
+                                              H * hd, None, ws.data_ptr(), n_ws, _st()), "qkv attention")
+        torch.cuda.synchronize()
+        assert torch.isnan(y).all()
+        assert torch.equal(kc, k0) and torch.equal(vc, v0)
