@@ -692,14 +692,15 @@ __global__ __launch_bounds__(kWaves * 64, 1) void skinny_kernel(
 }
 
 // The product of a split batched decode linear whose output the reduction
-// kernel finishes: int8 weights (row-major or operand tiles), the activation
+// kernel (or the decode attention, for the q, k, v projection) finishes: int8
+// weights (row-major or operand tiles), the activation
 // planes of the previous call in, raw fp32 partial sums out (slice z of
 // `part` holds K units [z U / S, (z + 1) U / S) of every output; scale, bias
 // and the rest are applied by the reduction). A workgroup of 8 wavefronts owns
 // RT 32-row weight tiles (N rows 32 t0 .. 32 (t0 + RT) - 1) and 32 activation
 // rows; its wavefronts split its K units, at most MU each, and every
 // activation operand a wavefront loads feeds the MFMAs of all RT tiles. All
-// loads are issued at once; the wavefronts' partial tiles are summed through
+// loads are issued at once, activations first; the wavefronts' partial tiles are summed through
 // LDS in wavefront order (results do not depend on timing).
 template <int WF, int RT, int MU>
 __global__ __launch_bounds__(kWaves * 64, 1) void split_product_kernel(const uint16_t* __restrict__ x3, int M, int K,
@@ -715,6 +716,20 @@ __global__ __launch_bounds__(kWaves * 64, 1) void split_product_kernel(const uin
     const int u0 = ub + wave * Us / kWaves, cnt = ub + (wave + 1) * Us / kWaves - u0;  // <= MU (host checks)
     const bool xrow_ok = m0 + r < M;
     const uint16_t* x3t = x3 + (int64_t)blockIdx.y * U * 6 * 64 * 8 + lane * 8;
+    // the activation operands first (L2 hits), then the weights (HBM): a unit's
+    // MFMAs then wait for its own weights, not for every weight of the
+    // wavefront as they would behind activations requested last (in-order
+    // completion)
+    u32x4 xv[MU][3][2];
+#pragma unroll
+    for (int c = 0; c < MU; ++c)
+        if (c < cnt) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    xv[c][q][e] = *reinterpret_cast<const u32x4*>(x3t + (((int64_t)(u0 + c) * 3 + q) * 2 + e) * 64 * 8);
+        }
     u32x4 wreg[MU][RT];
 #pragma unroll
     for (int c = 0; c < MU; ++c)
@@ -729,16 +744,6 @@ __global__ __launch_bounds__(kWaves * 64, 1) void split_product_kernel(const uin
                                                                  32 * (u0 + c) + 16 * h);
                 }
             }
-        }
-    u32x4 xv[MU][3][2];
-#pragma unroll
-    for (int c = 0; c < MU; ++c)
-        if (c < cnt) {
-#pragma unroll
-            for (int q = 0; q < 3; ++q)
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    xv[c][q][e] = *reinterpret_cast<const u32x4*>(x3t + (((int64_t)(u0 + c) * 3 + q) * 2 + e) * 64 * 8);
         }
     floatx16 acc[RT];
 #pragma unroll
