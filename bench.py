@@ -629,8 +629,43 @@ def decode_xl_section(dev, new_tokens=128, check_steps=4):
         nbytes = N * K + 4 * N + 2 * B * K + 2 * B * N
         per[f"{K}x{N}"] = {"linear": name, "us": us, "GB/s": nbytes / (us * 1e-6) / 1e9}
         del gr
+    # the fp32 tied head at M = 32 from LayerNorm f's planes (4 N K bytes a
+    # call, 322 MB: past the Infinity Cache), its weights as the decoder holds
+    # them (4 KB operand tiles, streamed by one workgroup per CU) and row-major
+    # (one workgroup per 32 rows): a graph of 10 calls, HIP events, median of 3
+    head = {}
+    V, C = cfg.vocab_size, cfg.n_embd
+    tiles = dec.tiles.get(id(qm.lm_head))
+    for label, wt, wf in (("tiled", tiles, _lib.WF_F32_TILED), ("row_major", dec.head_w, _lib.WF_F32)):
+        if wt is None:
+            continue
+        st = s_cap.cuda_stream
+        call = lambda: _lib.check(dec.L.tiq_decode_linear(
+            None, 0, dec.p_ln1.data_ptr(), B, C, wt.data_ptr(), wf, None, None, V, dec.logits.data_ptr(), V, None,
+            None, 1e-5, 0, None, 0, None, None, 1e-5, None, dec.chain_ws.data_ptr(), dec.chain_ws_bytes, st), "head")
+        with torch.cuda.stream(s_cap):
+            call()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s_cap):
+                for _ in range(10):
+                    call()
+        gr.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            gr.replay()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / 10)
+        us = statistics.median(ts)
+        head[label] = {"us": us, "GB/s": 4 * V * C / (us * 1e-6) / 1e9}
+        del gr
     del flush
     res["decode_linear_M32_cold"] = per
+    res["lm_head_fp32_M32"] = head
     del dec, qm
     torch.cuda.empty_cache()
     # the oracle on the same seed-0 weights, first check_steps tokens
