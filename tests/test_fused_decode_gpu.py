@@ -917,3 +917,36 @@ def test_qkv_attention_out_of_range_position(dev, c_oracle, B, C, H, T):
         torch.cuda.synchronize()
         assert torch.isnan(y).all()
         assert torch.equal(kc, k0) and torch.equal(vc, v0)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 50257), (2, 50257), (1, 57344), (2, 1025), (1, 60000), (2, 3)])
+def test_argmax_few_rows(dev, rows, cols):
+    """One or two rows (a single-sequence decode step), vocabulary-sized and
+    short: first index of the maximum on ties, a NaN never chosen, index 0 for
+    a row of -inf and NaN, the token in its id slot and the position advanced
+    once."""
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(rows * 7 + cols)
+    logits = torch.randn(rows, cols, generator=gen)
+    hi = cols - 1
+    logits[0, hi] = 9.0
+    logits[0, min(hi, 1)] = 9.0  # tie with a lower index
+    logits[0, min(hi, 2)] = float("nan")
+    if rows > 1:
+        logits[1].fill_(float("-inf"))
+        logits[1, :: max(1, cols // 5)] = float("nan")
+    want = []
+    for r in range(rows):  # the rule: maximum over non-NaN values, first index; 0 if none above -inf
+        row = logits[r].clone()
+        row[torch.isnan(row)] = float("-inf")
+        want.append(int(row.argmax()) if bool((row > float("-inf")).any()) else 0)
+    out = torch.full((rows,), -1, dtype=torch.long, device=dev)
+    ids = torch.zeros(rows, 8, dtype=torch.long, device=dev)
+    p = torch.tensor([3], device=dev)
+    ws = torch.empty(int(L.tiq_argmax_rows_workspace(rows)), dtype=torch.uint8, device=dev)
+    _lib.check(L.tiq_argmax_rows(logits.to(dev).data_ptr(), rows, cols, cols, out.data_ptr(), ids.data_ptr(), 8,
+                                 p.data_ptr(), ws.data_ptr(), ws.numel(), _st()), "argmax")
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == want
+    assert ids.cpu()[:, 4].tolist() == want and int(p) == 4
+    assert not ids.cpu()[:, :4].any() and not ids.cpu()[:, 5:].any()
