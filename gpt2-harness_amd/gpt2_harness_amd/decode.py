@@ -67,11 +67,10 @@ class _DecoderBase:
             raise ValueError(f"prompt {tuple(idx.shape)} does not fit batch={self.B}, max_len={self.T}")
         from .model import KVCache
 
-        cache = KVCache.empty(self.cfg.n_layer)
+        # the prompt's keys and values go straight into slots 0..T0-1 of the
+        # preallocated cache (T0 <= its capacity: no growth, no copy after)
+        cache = KVCache.over(self.k, self.v)
         logits = self.model(idx, cache=cache, last_only=True)["logits"][:, -1, :]
-        for i in range(self.cfg.n_layer):
-            self.k[i][:, :, :T0].copy_(cache.keys[i])
-            self.v[i][:, :, :T0].copy_(cache.values[i])
         self.out[:, :T0].copy_(idx)
         return logits
 

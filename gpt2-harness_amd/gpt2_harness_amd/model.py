@@ -84,6 +84,16 @@ class KVCache:
     def empty(cls, n_layer: int) -> KVCache:
         return cls(n_layer)
 
+    @classmethod
+    def over(cls, keys: list[torch.Tensor], values: list[torch.Tensor]) -> KVCache:
+        """An empty cache whose layer buffers are the given ``(B, heads,
+        capacity, head_dim)`` tensors (a decoder's preallocated cache): a
+        prefill appends into them in place (past ``capacity`` they grow by a
+        copy, as an empty cache's do)."""
+        cache = cls(len(keys))
+        cache._k, cache._v = list(keys), list(values)
+        return cache
+
     @property
     def seq_len(self) -> int:
         """Positions already processed (layer 0's fill level): the absolute

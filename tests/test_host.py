@@ -131,6 +131,25 @@ def test_kv_cache_length_semantics():
     assert kk.shape[-2] == 4
 
 
+def test_kv_cache_over_preallocated_buffers():
+    """KVCache.over: appends land in the given buffers in place (no copy while
+    they have room), the views cover the filled slots, and a buffer outgrown
+    is replaced by a larger copy holding the same history."""
+    kb = [torch.full((2, 3, 8, 4), -1.0) for _ in range(2)]
+    vb = [torch.full((2, 3, 8, 4), -1.0) for _ in range(2)]
+    c = g.KVCache.over(kb, vb)
+    assert c.seq_len == 0 and c.length(1) == 0
+    k = torch.arange(2 * 3 * 5 * 4, dtype=torch.float32).view(2, 3, 5, 4)
+    kk, vv = c.update(1, k, -k)
+    assert kk.data_ptr() == kb[1].data_ptr() and vv.data_ptr() == vb[1].data_ptr()
+    assert torch.equal(kb[1][:, :, :5], k) and torch.equal(vb[1][:, :, :5], -k)
+    assert bool((kb[1][:, :, 5:] == -1).all()) and bool((kb[0] == -1).all())
+    assert c.length(1) == 5 and c.length(0) == 0
+    kk, _ = c.update(1, k, k)  # 10 > 8 slots: grown
+    assert kk.shape[-2] == 10 and kk.data_ptr() != kb[1].data_ptr()
+    assert torch.equal(kk[:, :, :5], k) and torch.equal(kk[:, :, 5:], k)
+
+
 def test_synthetic_token_stream_windows():
     """The perplexity windows: non-overlapping blocks of T predictions that
     share one id with the next (ids[wT : wT + T + 1]), y = x shifted by one,
