@@ -346,6 +346,108 @@ __global__ __launch_bounds__(64 * kArgFinalWaves) void argmax_final_kernel(
 }
 
 
+// Causal self-attention of a prompt block (CausalSelfAttention.forward at
+// T > 1, model.py:284-309): T queries at absolute positions first .. first +
+// T - 1 over the S = first + T cached keys. Grid (query tiles of 64, heads,
+// sequences); 256 threads, four per query row, each holding 16 of the 64
+// dims. Per block of 64 keys (keys and values staged in LDS): the row's 64
+// scores (16-dim partial dots summed over the row's four threads), the causal
+// mask (-inf past the query's position), then an online softmax in fp32 --
+// the running maximum, the rescale of the partial output and the running sum
+// -- and the weighted sum of the values. q, k, v and y are read and written
+// through (batch, head, position) strides in floats, the 64 dims contiguous,
+// so the q, k, v projection's rows, a cache's (B, H, capacity, 64) buffers
+// and the (B, T, C) output rows serve directly, with no copy.
+constexpr int kPaRows = 64, kPaKeys = 64;
+
+__global__ __launch_bounds__(256) void prefill_attention_kernel(
+    const float* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_st, const float* __restrict__ k,
+    int64_t k_sb, int64_t k_sh, int64_t k_st, const float* __restrict__ v, int64_t v_sb, int64_t v_sh,
+    int64_t v_st, int T, int first, float* __restrict__ y, int64_t y_sb, int64_t y_sh, int64_t y_st) {
+    __shared__ float4 ks[kPaKeys][kHeadDim / 4 + 1];  // rows padded: the four threads of a row read apart
+    __shared__ float4 vs[kPaKeys][kHeadDim / 4 + 1];
+    const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, i = tid >> 2, c4 = tid & 3;
+    const int t = tile * kPaRows + i;  // this thread's query row (rows past T compute on row T - 1, unstored)
+    const int tq = min(t, T - 1);
+    const int64_t qpos = (int64_t)first + tq;
+    const float* qr = q + b * q_sb + h * q_sh + tq * q_st + 16 * c4;
+    float qv[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 f = reinterpret_cast<const float4*>(qr)[j];
+        qv[4 * j] = f.x, qv[4 * j + 1] = f.y, qv[4 * j + 2] = f.z, qv[4 * j + 3] = f.w;
+    }
+    const float* kb = k + b * k_sb + h * k_sh;
+    const float* vb = v + b * v_sb + h * v_sh;
+    // keys this tile needs: 0 .. first + min(T, 64 (tile + 1)) - 1
+    const int64_t s_end = (int64_t)first + min(T, kPaRows * (tile + 1));
+    float mx = -INFINITY, sum = 0.f, acc[16];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+    for (int64_t j0 = 0; j0 < s_end; j0 += kPaKeys) {
+        __syncthreads();  // the previous block's keys and values are consumed
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {  // 1024 float4 of keys and of values, four each a thread
+            const int e = tid + 256 * u, kk = e >> 4, dq = e & 15;
+            const int64_t slot = j0 + kk < s_end ? j0 + kk : s_end - 1;
+            ks[kk][dq] = reinterpret_cast<const float4*>(kb + slot * k_st)[dq];
+            vs[kk][dq] = reinterpret_cast<const float4*>(vb + slot * v_st)[dq];
+        }
+        __syncthreads();
+        float sc[kPaKeys];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < kPaKeys; ++kk) {
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 f = ks[kk][4 * c4 + j];
+                d = fmaf(qv[4 * j], f.x, d);
+                d = fmaf(qv[4 * j + 1], f.y, d);
+                d = fmaf(qv[4 * j + 2], f.z, d);
+                d = fmaf(qv[4 * j + 3], f.w, d);
+            }
+            d += __shfl_xor(d, 1, 4);
+            d += __shfl_xor(d, 2, 4);
+            const float sv = j0 + kk <= qpos ? d * 0.125f : -INFINITY;  // 1 / sqrt(64), exact
+            sc[kk] = sv;
+            bm = fmaxf(bm, sv);
+        }
+        const float mnew = fmaxf(mx, bm);  // finite: key 0 is visible to every query
+        const float alpha = expf(mx - mnew);
+        float ps = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < kPaKeys; ++kk) {
+            sc[kk] = expf(sc[kk] - mnew);
+            ps += sc[kk];
+        }
+        sum = sum * alpha + ps;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) acc[d] *= alpha;
+#pragma unroll
+        for (int kk = 0; kk < kPaKeys; ++kk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 f = vs[kk][4 * c4 + j];
+                acc[4 * j] = fmaf(sc[kk], f.x, acc[4 * j]);
+                acc[4 * j + 1] = fmaf(sc[kk], f.y, acc[4 * j + 1]);
+                acc[4 * j + 2] = fmaf(sc[kk], f.z, acc[4 * j + 2]);
+                acc[4 * j + 3] = fmaf(sc[kk], f.w, acc[4 * j + 3]);
+            }
+        }
+        mx = mnew;
+    }
+    if (t < T) {
+        float* yr = y + b * y_sb + h * y_sh + t * y_st + 16 * c4;
+        const float r = 1.0f / sum;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            reinterpret_cast<float4*>(yr)[j] =
+                make_float4(acc[4 * j] * r, acc[4 * j + 1] * r, acc[4 * j + 2] * r, acc[4 * j + 3] * r);
+    }
+}
+
 // y = gelu_tanh(x) elementwise (the MLP activation of a prefill, one pass in
 // place of the reference's op chain at model.py:57-75): 4 values a thread per
 // step of a grid-stride loop; n % 4 tail by the first threads.
@@ -459,6 +561,26 @@ extern "C" int tiq_decode_qkv_attention(const uint16_t* x_planes, int64_t batch,
     if (rc != TIQ_OK) return rc;
     return decode_attention(part, N, batch, n_head, n_kv_head, head_dim, k_cache, v_cache, t_max, pos, y, ldy,
                             planes_out, stream, decode_slices_count(batch, n_embd, N), scale, bias);
+}
+
+extern "C" int tiq_prefill_attention(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const float* k,
+                                     int64_t k_sb, int64_t k_sh, int64_t k_st, const float* v, int64_t v_sb,
+                                     int64_t v_sh, int64_t v_st, int64_t batch, int64_t n_head, int64_t T,
+                                     int64_t first, int64_t head_dim, float* y, int64_t y_sb, int64_t y_sh,
+                                     int64_t y_st, void* stream) {
+    if (batch < 0 || n_head <= 0 || T < 0 || first < 0) return TIQ_EINVAL;
+    if (batch == 0 || T == 0) return TIQ_OK;
+    if (!q || !k || !v || !y) return TIQ_EINVAL;
+    if (head_dim != kHeadDim) return TIQ_EUNSUPPORTED;
+    if (batch > 65535 || n_head > 65535 || T > INT32_MAX - kPaRows || first > INT32_MAX - T) return TIQ_EUNSUPPORTED;
+    const int64_t strides[12] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, y_sb, y_sh, y_st};
+    for (int64_t st : strides)
+        if (st < 0 || st % 4 != 0) return TIQ_EALIGN;  // 16-byte rows of 4 floats
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(y, 16)) return TIQ_EALIGN;
+    const dim3 grid((unsigned)((T + kPaRows - 1) / kPaRows), (unsigned)n_head, (unsigned)batch);
+    hipLaunchKernelGGL(prefill_attention_kernel, grid, dim3(256), 0, as_stream(stream), q, q_sb, q_sh, q_st, k, k_sb,
+                       k_sh, k_st, v, v_sb, v_sh, v_st, (int)T, (int)first, y, y_sb, y_sh, y_st);
+    return launch_status();
 }
 
 extern "C" int tiq_gelu_tanh(const float* x, float* y, int64_t n, void* stream) {

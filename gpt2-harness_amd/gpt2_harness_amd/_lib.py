@@ -69,12 +69,16 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                   _i64, _vp, _vp, _sz, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
     "tiq_gelu_tanh": ([_vp, _vp, _i64, _vp], _i32),
+    "tiq_prefill_attention": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                               _i64, _i64, _vp, _i64, _i64, _i64, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),
     "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _vp], _i32),
 }
 
 WF_INT8, WF_INT4, WF_INT4G, WF_F32, WF_INT8_TILED, WF_F32_TILED = 0, 1, 2, 3, 4, 5
 ACT_NONE, ACT_GELU_TANH = 0, 1
+#: status codes of tiq.h
+OK, EINVAL, EBITS, EALIGN, EUNSUPPORTED, EWORKSPACE, ESCRATCH = 0, -1, -2, -3, -4, -5, -6
 
 _LIB: ctypes.CDLL | None = None
 

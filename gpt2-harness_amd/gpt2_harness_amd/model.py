@@ -151,6 +151,32 @@ def _causal_softmax_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return torch.matmul(probs, v)
 
 
+def _fused_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, first: int,
+                     p_drop: float) -> torch.Tensor | None:
+    """``_causal_softmax_attention`` as one HIP kernel (``tiq_prefill_attention``),
+    its output as ``(B, T, heads * head_dim)`` rows, for fp32 GPU tensors with
+    64-dim heads that need no gradient and no dropout; ``None`` otherwise. q, k
+    and v are read in place through their strides (the projection's rows, a
+    cache's buffers): no copies."""
+    B, H, T, hd = q.shape
+    ok = (q.is_cuda and hd == 64 and p_drop == 0.0 and k.shape[-2] == first + T
+          and all(t.dtype == torch.float32 and t.stride(-1) == 1 for t in (q, k, v))
+          and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)))
+    if not ok:
+        return None
+    from . import _lib
+
+    y = torch.empty(B, T, H * hd, device=q.device, dtype=torch.float32)
+    rc = _lib.lib().tiq_prefill_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), B, H, T, first, hd, y.data_ptr(), y.stride(0), hd,
+        y.stride(1), _lib.stream_of(q))
+    if rc in (_lib.EALIGN, _lib.EUNSUPPORTED):
+        return None  # strides or sizes the kernel does not take: the torch ops below
+    _lib.check(rc, "prefill attention")
+    return y
+
+
 class CausalSelfAttention(nn.Module):
     """Fused ``c_attn`` (q, k, v side by side), heads of 64 columns, causal
     attention over the cache, ``c_proj``."""
@@ -171,6 +197,9 @@ class CausalSelfAttention(nn.Module):
         if cache is not None:
             k, v = cache.update(self.layer_idx, k, v)
         p = self.config.dropout if self.training else 0.0
+        y = _fused_attention(q, k, v, first, p)
+        if y is not None:
+            return self.c_proj(y)
         y = _causal_softmax_attention(q, k, v, first, p)
         return self.c_proj(y.transpose(1, 2).reshape(B, T, C))
 

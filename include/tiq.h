@@ -398,6 +398,22 @@ int tiq_decode_qkv_attention(const uint16_t* x_planes, int64_t batch, int64_t n_
                              float* y, int64_t ldy, uint16_t* planes_out, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* Causal self-attention of T queries per (sequence, head) over S = first + T
+ * keys (CausalSelfAttention.forward, model.py:284-309, a prompt block or a
+ * cached step): query t, at absolute position first + t, attends to keys
+ * 0 .. first + t with softmax(q k^T / sqrt(head_dim)) in fp32 (an online
+ * softmax over blocks of 64 keys). q (batch, n_head, T, 64), k and v (batch,
+ * n_head, S, 64) and y (batch, n_head, T, 64) are addressed through their
+ * (batch, head, position) strides in floats with the 64 dims contiguous:
+ * the rows of the q, k, v projection, a KV cache's buffers and the (batch,
+ * T, n_head * 64) output rows are read and written in place. head_dim must be
+ * 64; pointers 16-byte aligned and strides multiples of 4 (TIQ_EALIGN
+ * otherwise). No counterpart in the reference (a chain of torch ops there). */
+int tiq_prefill_attention(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const float* k, int64_t k_sb,
+                          int64_t k_sh, int64_t k_st, const float* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                          int64_t batch, int64_t n_head, int64_t T, int64_t first, int64_t head_dim, float* y,
+                          int64_t y_sb, int64_t y_sh, int64_t y_st, void* stream);
+
 /* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) elementwise over n fp32
  * values (16-byte aligned; y may alias x): the MLP activation gelu_tanh
  * (model.py:57-75, applied at model.py:354) in one pass instead of the

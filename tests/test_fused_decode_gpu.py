@@ -950,3 +950,58 @@ def test_argmax_few_rows(dev, rows, cols):
     assert out.cpu().tolist() == want
     assert ids.cpu()[:, 4].tolist() == want and int(p) == 4
     assert not ids.cpu()[:, :4].any() and not ids.cpu()[:, 5:].any()
+
+
+def _attn64(q, k, v, first):
+    """float64 causal attention of queries at first .. first + T - 1 over keys 0 .. S - 1."""
+    T, S = q.shape[-2], k.shape[-2]
+    s = (q.double() @ k.double().transpose(-2, -1)) / 8.0
+    mask = torch.arange(S)[None, :] > (first + torch.arange(T))[:, None]
+    return F.softmax(s.masked_fill(mask, float("-inf")), dim=-1) @ v.double()
+
+
+@pytest.mark.parametrize("B,H,T,first,cap", [(2, 12, 64, 0, 0), (2, 12, 70, 0, 0), (1, 4, 1, 0, 0),
+                                             (3, 4, 70, 30, 256), (32, 25, 128, 0, 256), (1, 2, 1, 100, 128),
+                                             (2, 3, 200, 500, 1024)])
+def test_prefill_attention(dev, B, H, T, first, cap):
+    """tiq_prefill_attention against float64: q, k, v read in place as views of
+    the projection's (B, T, 3C) rows (cap = 0) or, with a history of `first`
+    positions, k and v from (B, H, cap, 64) cache buffers; the output written as
+    (B, T, C) rows; T not a multiple of the 64-row tile; a single query."""
+    hd, C = 64, H * 64
+    gen = torch.Generator().manual_seed(B * 100 + T + first)
+    qkv = torch.randn(B, T, 3 * C, generator=gen)
+    q, k, v = qkv.view(B, T, 3, H, hd).permute(2, 0, 3, 1, 4).unbind(0)
+    if cap:
+        kc = torch.randn(B, H, cap, hd, generator=gen)
+        vc = torch.randn(B, H, cap, hd, generator=gen)
+        kc[:, :, first : first + T] = k
+        vc[:, :, first : first + T] = v
+        kd, vd = kc.to(dev)[:, :, : first + T], vc.to(dev)[:, :, : first + T]
+        kr, vr = kc[:, :, : first + T], vc[:, :, : first + T]
+    else:
+        kd = vd = None
+        kr, vr = k, v
+    qkvd = qkv.to(dev)
+    qd, kd2, vd2 = qkvd.view(B, T, 3, H, hd).permute(2, 0, 3, 1, 4).unbind(0)
+    if kd is None:
+        kd, vd = kd2, vd2
+    y = torch.full((B, T, C), float("nan"), device=dev)
+    _lib.check(_lib.lib().tiq_prefill_attention(
+        qd.data_ptr(), qd.stride(0), qd.stride(1), qd.stride(2), kd.data_ptr(), kd.stride(0), kd.stride(1),
+        kd.stride(2), vd.data_ptr(), vd.stride(0), vd.stride(1), vd.stride(2), B, H, T, first, hd, y.data_ptr(),
+        y.stride(0), hd, y.stride(1), _st()), "prefill attention")
+    ref = _attn64(q, kr, vr, first).transpose(1, 2).reshape(B, T, C)
+    err = float((y.cpu().double() - ref).abs().max())
+    assert err < 2e-5, err
+
+
+def test_prefill_attention_arguments(dev):
+    L = _lib.lib()
+    buf = torch.zeros(4 * 3 * 64 * 64, device=dev)
+    f = buf.data_ptr()
+    args = lambda hd, st=64, p=f: (p, 0, 0, st, f, 0, 0, 64, f, 0, 0, 64, 1, 1, 4, 0, hd, f, 0, 0, 64, _st())
+    assert L.tiq_prefill_attention(*args(32)) == -4
+    assert L.tiq_prefill_attention(*args(64, 66)) == -3
+    assert L.tiq_prefill_attention(*args(64, 64, f + 4)) == -3
+    assert L.tiq_prefill_attention(*args(64)) == 0
