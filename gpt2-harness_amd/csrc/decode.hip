@@ -349,102 +349,151 @@ __global__ __launch_bounds__(64 * kArgFinalWaves) void argmax_final_kernel(
 // Causal self-attention of a prompt block (CausalSelfAttention.forward at
 // T > 1, model.py:284-309): T queries at absolute positions first .. first +
 // T - 1 over the S = first + T cached keys. Grid (query tiles of 64, heads,
-// sequences); 256 threads, four per query row, each holding 16 of the 64
-// dims. Per block of 64 keys (keys and values staged in LDS): the row's 64
-// scores (16-dim partial dots summed over the row's four threads), the causal
-// mask (-inf past the query's position), then an online softmax in fp32 --
-// the running maximum, the rescale of the partial output and the running sum
-// -- and the weighted sum of the values. q, k, v and y are read and written
-// through (batch, head, position) strides in floats, the 64 dims contiguous,
-// so the q, k, v projection's rows, a cache's (B, H, capacity, 64) buffers
-// and the (B, T, C) output rows serve directly, with no copy.
-constexpr int kPaRows = 64, kPaKeys = 64;
+// sequences); one wavefront per tile, lane (g, c) = (lane / 4, lane % 4)
+// holding query rows 4 g .. 4 g + 3 of the tile and dims 16 c .. 16 c + 15:
+// each 16-byte read of a key or value from LDS feeds four rows (16 FMAs).
+// Per block of 64 keys staged in LDS, 16 keys at a time: the rows' scores
+// (16-dim partial dots summed over the row's four lanes by quad DPP moves),
+// the causal mask (-inf past the query's position), an online softmax in
+// fp32 -- the running maximum, the rescale of the partial outputs, the
+// running sum -- and the weighted sum of the values. q, k, v and y are read
+// and written through (batch, head, position) strides in floats, the 64 dims
+// contiguous, so the q, k, v projection's rows, a cache's (B, H, capacity, 64)
+// buffers and the (B, T, C) output rows serve directly, with no copy.
+constexpr int kPaRows = 64, kPaKeys = 64, kPaSub = 16;
+constexpr int kPaR = 2;                         // query rows a lane holds
+constexpr int kPaThreads = kPaRows / kPaR * 4;  // four lanes a row group
 
-__global__ __launch_bounds__(256) void prefill_attention_kernel(
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_move<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);  // quad_perm [2, 3, 0, 1]
+    return v;
+}
+
+__global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(
     const float* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_st, const float* __restrict__ k,
     int64_t k_sb, int64_t k_sh, int64_t k_st, const float* __restrict__ v, int64_t v_sb, int64_t v_sh,
     int64_t v_st, int T, int first, float* __restrict__ y, int64_t y_sb, int64_t y_sh, int64_t y_st) {
-    __shared__ float4 ks[kPaKeys][kHeadDim / 4 + 1];  // rows padded: the four threads of a row read apart
+    __shared__ float4 ks[kPaKeys][kHeadDim / 4 + 1];  // rows padded
     __shared__ float4 vs[kPaKeys][kHeadDim / 4 + 1];
     const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, i = tid >> 2, c4 = tid & 3;
-    const int t = tile * kPaRows + i;  // this thread's query row (rows past T compute on row T - 1, unstored)
-    const int tq = min(t, T - 1);
-    const int64_t qpos = (int64_t)first + tq;
-    const float* qr = q + b * q_sb + h * q_sh + tq * q_st + 16 * c4;
-    float qv[16];
+    const int lane = threadIdx.x, g = lane >> 2, c4 = lane & 3;
+    const int t0 = tile * kPaRows + kPaR * g;  // rows t0 .. t0 + kPaR - 1 (past T: computed on row T - 1, unstored)
+    float qv[kPaR][16];
+    int64_t qpos[kPaR];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float4 f = reinterpret_cast<const float4*>(qr)[j];
-        qv[4 * j] = f.x, qv[4 * j + 1] = f.y, qv[4 * j + 2] = f.z, qv[4 * j + 3] = f.w;
+    for (int r = 0; r < kPaR; ++r) {
+        const int tq = min(t0 + r, T - 1);
+        qpos[r] = (int64_t)first + tq;
+        const float4* qr = reinterpret_cast<const float4*>(q + b * q_sb + h * q_sh + tq * q_st + 16 * c4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 f = qr[j];
+            qv[r][4 * j] = f.x, qv[r][4 * j + 1] = f.y, qv[r][4 * j + 2] = f.z, qv[r][4 * j + 3] = f.w;
+        }
     }
     const float* kb = k + b * k_sb + h * k_sh;
     const float* vb = v + b * v_sb + h * v_sh;
-    // keys this tile needs: 0 .. first + min(T, 64 (tile + 1)) - 1
-    const int64_t s_end = (int64_t)first + min(T, kPaRows * (tile + 1));
-    float mx = -INFINITY, sum = 0.f, acc[16];
+    const int64_t s_end = (int64_t)first + min(T, kPaRows * (tile + 1));  // keys this tile needs
+    float mx[kPaR], sum[kPaR], acc[kPaR][16];
 #pragma unroll
-    for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+    for (int r = 0; r < kPaR; ++r) {
+        mx[r] = -INFINITY, sum[r] = 0.f;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) acc[r][d] = 0.f;
+    }
     for (int64_t j0 = 0; j0 < s_end; j0 += kPaKeys) {
-        __syncthreads();  // the previous block's keys and values are consumed
+        __syncthreads();  // the previous block is consumed
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {  // 1024 float4 of keys and of values, four each a thread
-            const int e = tid + 256 * u, kk = e >> 4, dq = e & 15;
+        for (int u = 0; u < kPaKeys * 16 / kPaThreads; ++u) {  // the block's keys and values, 16 float4 a key
+            const int e = lane + kPaThreads * u, kk = e >> 4, dq = e & 15;
             const int64_t slot = j0 + kk < s_end ? j0 + kk : s_end - 1;
             ks[kk][dq] = reinterpret_cast<const float4*>(kb + slot * k_st)[dq];
             vs[kk][dq] = reinterpret_cast<const float4*>(vb + slot * v_st)[dq];
         }
         __syncthreads();
-        float sc[kPaKeys];
-        float bm = -INFINITY;
+        const int nsub = (int)min<int64_t>(kPaKeys / kPaSub, (s_end - j0 + kPaSub - 1) / kPaSub);
+        for (int sb = 0; sb < nsub; ++sb) {
+            const int kb0 = sb * kPaSub;
+            float sc[kPaR][kPaSub];
 #pragma unroll
-        for (int kk = 0; kk < kPaKeys; ++kk) {
-            float d = 0.f;
+            for (int kk = 0; kk < kPaSub; ++kk) {
+                float d[kPaR];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 f = ks[kk][4 * c4 + j];
-                d = fmaf(qv[4 * j], f.x, d);
-                d = fmaf(qv[4 * j + 1], f.y, d);
-                d = fmaf(qv[4 * j + 2], f.z, d);
-                d = fmaf(qv[4 * j + 3], f.w, d);
+                for (int r = 0; r < kPaR; ++r) d[r] = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 f = ks[kb0 + kk][4 * c4 + j];
+#pragma unroll
+                    for (int r = 0; r < kPaR; ++r) {
+                        d[r] = fmaf(qv[r][4 * j], f.x, d[r]);
+                        d[r] = fmaf(qv[r][4 * j + 1], f.y, d[r]);
+                        d[r] = fmaf(qv[r][4 * j + 2], f.z, d[r]);
+                        d[r] = fmaf(qv[r][4 * j + 3], f.w, d[r]);
+                    }
+                }
+                const int64_t key = j0 + kb0 + kk;
+#pragma unroll
+                for (int r = 0; r < kPaR; ++r) {
+                    const float full = quad_sum(d[r]);
+                    sc[r][kk] = key <= qpos[r] ? full * 0.125f : -INFINITY;  // 1 / sqrt(64), exact
+                }
             }
-            d += __shfl_xor(d, 1, 4);
-            d += __shfl_xor(d, 2, 4);
-            const float sv = j0 + kk <= qpos ? d * 0.125f : -INFINITY;  // 1 / sqrt(64), exact
-            sc[kk] = sv;
-            bm = fmaxf(bm, sv);
-        }
-        const float mnew = fmaxf(mx, bm);  // finite: key 0 is visible to every query
-        const float alpha = expf(mx - mnew);
-        float ps = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < kPaKeys; ++kk) {
-            sc[kk] = expf(sc[kk] - mnew);
-            ps += sc[kk];
-        }
-        sum = sum * alpha + ps;
+            for (int r = 0; r < kPaR; ++r) {
+                float bm = sc[r][0];
 #pragma unroll
-        for (int d = 0; d < 16; ++d) acc[d] *= alpha;
+                for (int kk = 1; kk < kPaSub; ++kk) bm = fmaxf(bm, sc[r][kk]);
+                const float mnew = fmaxf(mx[r], bm);  // finite: key 0 is visible to every query
+                const float alpha = expf(mx[r] - mnew);
+                // lane c of the row's quad exponentiates keys 4 jj + c, the quad
+                // broadcasts them: each exponential computed once
+                float pe[kPaSub / 4], ps = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < kPaKeys; ++kk) {
+                for (int jj = 0; jj < kPaSub / 4; ++jj) {
+                    const float mine = c4 == 0 ? sc[r][4 * jj] : c4 == 1 ? sc[r][4 * jj + 1]
+                                     : c4 == 2 ? sc[r][4 * jj + 2] : sc[r][4 * jj + 3];
+                    pe[jj] = expf(mine - mnew);
+                    ps += pe[jj];
+                }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 f = vs[kk][4 * c4 + j];
-                acc[4 * j] = fmaf(sc[kk], f.x, acc[4 * j]);
-                acc[4 * j + 1] = fmaf(sc[kk], f.y, acc[4 * j + 1]);
-                acc[4 * j + 2] = fmaf(sc[kk], f.z, acc[4 * j + 2]);
-                acc[4 * j + 3] = fmaf(sc[kk], f.w, acc[4 * j + 3]);
+                for (int jj = 0; jj < kPaSub / 4; ++jj) {
+                    sc[r][4 * jj] = dpp_move<0x00>(pe[jj]);  // quad_perm [0, 0, 0, 0]
+                    sc[r][4 * jj + 1] = dpp_move<0x55>(pe[jj]);
+                    sc[r][4 * jj + 2] = dpp_move<0xAA>(pe[jj]);
+                    sc[r][4 * jj + 3] = dpp_move<0xFF>(pe[jj]);
+                }
+                sum[r] = sum[r] * alpha + quad_sum(ps);
+                mx[r] = mnew;
+#pragma unroll
+                for (int d = 0; d < 16; ++d) acc[r][d] *= alpha;
+            }
+#pragma unroll
+            for (int kk = 0; kk < kPaSub; ++kk) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 f = vs[kb0 + kk][4 * c4 + j];
+#pragma unroll
+                    for (int r = 0; r < kPaR; ++r) {
+                        acc[r][4 * j] = fmaf(sc[r][kk], f.x, acc[r][4 * j]);
+                        acc[r][4 * j + 1] = fmaf(sc[r][kk], f.y, acc[r][4 * j + 1]);
+                        acc[r][4 * j + 2] = fmaf(sc[r][kk], f.z, acc[r][4 * j + 2]);
+                        acc[r][4 * j + 3] = fmaf(sc[r][kk], f.w, acc[r][4 * j + 3]);
+                    }
+                }
             }
         }
-        mx = mnew;
     }
-    if (t < T) {
-        float* yr = y + b * y_sb + h * y_sh + t * y_st + 16 * c4;
-        const float r = 1.0f / sum;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            reinterpret_cast<float4*>(yr)[j] =
-                make_float4(acc[4 * j] * r, acc[4 * j + 1] * r, acc[4 * j + 2] * r, acc[4 * j + 3] * r);
+    for (int r = 0; r < kPaR; ++r) {
+        if (t0 + r < T) {
+            float4* yr = reinterpret_cast<float4*>(y + b * y_sb + h * y_sh + (int64_t)(t0 + r) * y_st + 16 * c4);
+            const float inv = 1.0f / sum[r];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                yr[j] = make_float4(acc[r][4 * j] * inv, acc[r][4 * j + 1] * inv, acc[r][4 * j + 2] * inv,
+                                    acc[r][4 * j + 3] * inv);
+        }
     }
 }
 
@@ -578,7 +627,7 @@ extern "C" int tiq_prefill_attention(const float* q, int64_t q_sb, int64_t q_sh,
         if (st < 0 || st % 4 != 0) return TIQ_EALIGN;  // 16-byte rows of 4 floats
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(y, 16)) return TIQ_EALIGN;
     const dim3 grid((unsigned)((T + kPaRows - 1) / kPaRows), (unsigned)n_head, (unsigned)batch);
-    hipLaunchKernelGGL(prefill_attention_kernel, grid, dim3(256), 0, as_stream(stream), q, q_sb, q_sh, q_st, k, k_sb,
+    hipLaunchKernelGGL(prefill_attention_kernel, grid, dim3(kPaThreads), 0, as_stream(stream), q, q_sb, q_sh, q_st, k, k_sb,
                        k_sh, k_st, v, v_sb, v_sh, v_st, (int)T, (int)first, y, y_sb, y_sh, y_st);
     return launch_status();
 }
