@@ -124,7 +124,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 117; }
+extern "C" int tiq_version(void) { return 118; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
