@@ -1071,8 +1071,7 @@ size_t decode_planes_bytes(int64_t M, int64_t K) { return planes_bytes(M, K); }
 // fp32 tiles (the head): planes in, fp32 rows out, nothing fused
 static int run_decode_f32_tiles(const LinearArgs& a, const uint16_t* x_planes, const float* next_ln_w,
                          uint16_t* planes_out) {
-    if (a.M < 1 || a.M > 64 || a.K <= 0 || a.K % 32 != 0 || a.K / 32 < kWaves || a.N <= 0 ||
-        a.N > 0x7fffffff - 31 || a.ldy > 0x7fffffff)
+    if (a.M < 1 || a.M > 64 || a.K <= 0 || a.K % 32 != 0 || a.K / 32 < kWaves || a.N <= 0 || a.N > 0x7fffffff - 31)
         return TIQ_EUNSUPPORTED;
     if (!x_planes || a.bias || a.fuse.act || a.fuse.res || next_ln_w || planes_out) return TIQ_EUNSUPPORTED;
     if (!a.y || !a.w) return TIQ_EINVAL;
