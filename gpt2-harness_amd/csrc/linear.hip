@@ -56,14 +56,21 @@ LinearArgs make_args(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
 // lo = rne(x - hi), lo2 = rne(x - hi - lo). Both differences are exact in fp32
 // and lo2 holds the last 8 significant bits, so hi + lo + lo2 == x; an int8
 // weight is exact in bf16, so every product the MFMA forms is exact and the
-// GEMM over the three planes is as accurate as an fp32 GEMM.
+// GEMM over the three planes is as accurate as an fp32 GEMM. gelu: the planes
+// of gelu_tanh(x) (the same function as tiq_gelu_tanh's), x read once.
 __global__ void split_bf16x3_kernel(const float* __restrict__ x, int64_t ldx, int M, int K,
-                                    uint16_t* __restrict__ x3) {
+                                    uint16_t* __restrict__ x3, bool gelu) {
     const int k4 = K / 4;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)M * k4) return;
     const int m = (int)(i / k4), k = (int)(i % k4) * 4;
-    const float4 v = *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k);
+    float4 v = *reinterpret_cast<const float4*>(x + (int64_t)m * ldx + k);
+    if (gelu) {
+        v.x = gelu_tanh(v.x);
+        v.y = gelu_tanh(v.y);
+        v.z = gelu_tanh(v.z);
+        v.w = gelu_tanh(v.w);
+    }
     // pairs through v_cvt_pk_bf16_f32 (round to nearest even)
     uint32_t p[3][2];
 #pragma unroll
@@ -85,8 +92,8 @@ size_t split_workspace(int64_t M, int64_t K) { return (size_t)(M * 3 * K * 2 + 2
 
 // fp32 activations through the matrix cores when a GEMM takes the three-plane
 // problem (the staged kernel, else the LDS-dequant one); TIQ_EUNSUPPORTED
-// otherwise (the caller falls back).
-int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
+// otherwise (the caller falls back). gelu_in: the product takes gelu_tanh(x).
+int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes, bool gelu_in = false) {
     if (a.x_dtype != TIQ_F32 || a.fmt == kF32 || a.M < kGemmMinRows || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
     if (!aligned(a.x, 16) || a.ldx % 4 != 0 || a.M * 3 * a.K > 0x7fffffffLL) return TIQ_EUNSUPPORTED;
     LinearArgs g = a;
@@ -100,7 +107,8 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     if (!ws || ws_bytes < split_workspace(a.M, a.K) || !aligned(ws, 16)) return TIQ_EWORKSPACE;
     const int64_t n = a.M * (a.K / 4);
     hipLaunchKernelGGL(split_bf16x3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, a.stream,
-                       static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, static_cast<uint16_t*>(ws));
+                       static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, static_cast<uint16_t*>(ws),
+                       gelu_in);
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
     if (!staged) return launch_gemm(g);
@@ -124,7 +132,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 118; }
+extern "C" int tiq_version(void) { return 119; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
@@ -192,6 +200,22 @@ extern "C" int tiq_gemm_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, 
         if (rc != TIQ_EUNSUPPORTED) return rc;
     }
     return launch_gemm(a);
+}
+
+extern "C" int tiq_linear_gelu_in_ws(const float* x, int64_t M, int64_t K, int64_t ldx, const void* w, int w_format,
+                                     const float* scale, const uint16_t* scale_f16, int group, const float* bias,
+                                     int64_t N, float* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    if (w_format != TIQ_WF_INT8 && w_format != TIQ_WF_INT4 && w_format != TIQ_WF_INT4_GROUPWISE) return TIQ_EINVAL;
+    const WFormat fmt = (WFormat)w_format;
+    const int64_t ldw = fmt == kW8 ? K : fmt == kW4 ? K / 2 : (K + 1) / 2;
+    LinearArgs a = make_args(x, TIQ_F32, M, K, ldx, static_cast<const uint8_t*>(w), ldw, scale, scale_f16, group,
+                             bias, N, y, TIQ_F32, ldy, stream, fmt);
+    int rc = check_linear(a);
+    if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    if (M < kGemmMinRows || K % 64 != 0) return TIQ_EUNSUPPORTED;
+    if (workspace && !aligned(workspace, 16)) return TIQ_EALIGN;
+    return run_linear_split(a, workspace, workspace_bytes, true);
 }
 
 extern "C" int tiq_gemv_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,

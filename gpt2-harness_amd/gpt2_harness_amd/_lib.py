@@ -69,6 +69,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                   _i64, _vp, _vp, _sz, _vp], _i32),
     "tiq_embed_tokens": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], _i32),
     "tiq_gelu_tanh": ([_vp, _vp, _i64, _vp], _i32),
+    "tiq_linear_gelu_in_ws": ([_vp, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _sz, _vp],
+                              _i32),
     "tiq_prefill_attention": ([_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                _i64, _i64, _vp, _i64, _i64, _i64, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),

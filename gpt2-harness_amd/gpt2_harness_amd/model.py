@@ -213,7 +213,10 @@ class MLP(nn.Module):
         self.c_proj = nn.Linear(4 * config.n_embd, config.n_embd, bias=config.mlp_bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.c_proj(gelu_tanh(self.c_fc(x)))
+        h = self.c_fc(x)
+        fused = getattr(self.c_proj, "forward_gelu_in", None)  # a quantized c_proj over a prefill's rows
+        y = fused(h) if fused is not None else None
+        return y if y is not None else self.c_proj(gelu_tanh(h))
 
 
 class Block(nn.Module):

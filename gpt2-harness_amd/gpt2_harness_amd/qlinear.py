@@ -85,6 +85,39 @@ class QuantLinear(nn.Module):
             linear_into(self, x2, y)
         return y.reshape(*lead, N)
 
+    def forward_gelu_in(self, x: torch.Tensor) -> torch.Tensor | None:
+        """``self(gelu_tanh(x))`` for fp32 GPU rows of a prefill (at least 128
+        rows, ``K % 64 == 0``, no gradient wanted), the activation applied
+        while the library splits ``x`` into the matrix cores' bf16 planes
+        (``tiq_linear_gelu_in_ws``): bit for bit ``self(gelu_tanh(x))``
+        without the activation's own pass. None where that entry point does
+        not apply; the caller then takes the two steps."""
+        K, N = self.in_features, self.out_features
+        if (not x.is_cuda or x.dtype != torch.float32 or x.shape[-1] != K or K % 64
+                or (torch.is_grad_enabled() and x.requires_grad)):
+            return None
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, K)
+        M = x2.size(0)
+        if M < 128:
+            return None
+        if x2.stride(-1) != 1 or x2.stride(0) != K or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        L = _lib.lib()
+        y = torch.empty((M, N), dtype=torch.float32, device=x.device)
+        ws_bytes = int(L.tiq_gemm_w8_workspace(_lib.dtype_code(torch.float32), M, K, N))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+        wf = {FMT_W8: _lib.WF_INT8, FMT_W4: _lib.WF_INT4}.get(self.fmt, _lib.WF_INT4G)
+        s32 = None if self.fmt == FMT_W4G else self.scale.data_ptr()
+        s16 = self.scale.data_ptr() if self.fmt == FMT_W4G else None
+        rc = L.tiq_linear_gelu_in_ws(x2.data_ptr(), M, K, K, self.codes.data_ptr(), wf, s32, s16, self.group_size,
+                                     _lib.ptr(self.bias), N, y.data_ptr(), N, ws.data_ptr(), ws_bytes,
+                                     _lib.stream_of(x2))
+        if rc == _lib.EUNSUPPORTED:
+            return None
+        _lib.check(rc, f"quantized linear over gelu_tanh ({self.fmt}, M={M}, K={K}, N={N})")
+        return y.reshape(*lead, N)
+
     @property
     def weight(self) -> torch.Tensor:
         """The dequantized ``W_hat`` (fp32, ``(N, K)``), as the reference stores it."""

@@ -420,6 +420,24 @@ int tiq_prefill_attention(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_
  * reference's chain of torch ops. */
 int tiq_gelu_tanh(const float* x, float* y, int64_t n, void* stream);
 
+/* A quantized Linear over gelu_tanh of fp32 rows: the MLP's
+ * c_proj(gelu_tanh(c_fc(x))) of a prefill (model.py:57-75 and the c_proj
+ * slot, model.py:355, at M = B * T rows). The activation is applied while x
+ * is split into the three exact bf16 planes the matrix cores take, so y is
+ * bit for bit what tiq_linear_w8_ws / tiq_linear_w4_ws / tiq_linear_w4g_ws
+ * compute on tiq_gelu_tanh(x), without the activation's own read and write of
+ * x. w, w_format (TIQ_WF_INT8, TIQ_WF_INT4, TIQ_WF_INT4_GROUPWISE), scale,
+ * scale_f16 and group as tiq_linear_fused; x and y fp32; x is only read.
+ * Needs M >= 128, K % 64 == 0, x 16-byte aligned with ldx % 4 == 0 and a
+ * workspace of tiq_gemm_w8_workspace(TIQ_F32, M, K, N) bytes (at least the
+ * planes' M * 3K * 2, else TIQ_EWORKSPACE; with less than the full size a
+ * product with few output tiles runs unsplit); TIQ_EUNSUPPORTED for other
+ * shapes, for which the caller applies tiq_gelu_tanh and the plain entry
+ * point. */
+int tiq_linear_gelu_in_ws(const float* x, int64_t M, int64_t K, int64_t ldx, const void* w, int w_format,
+                          const float* scale, const uint16_t* scale_f16, int group, const float* bias, int64_t N,
+                          float* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
 /* x[b] = wte[tokens[b]] + wpe[*pos]  (model.py:561-564 for one position). */
 int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const float* wte, int64_t vocab,
                      const float* wpe, int64_t n_positions, int64_t batch, int64_t n_embd, float* x,
