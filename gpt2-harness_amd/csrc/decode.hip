@@ -349,10 +349,10 @@ __global__ __launch_bounds__(64 * kArgFinalWaves) void argmax_final_kernel(
 // Causal self-attention of a prompt block (CausalSelfAttention.forward at
 // T > 1, model.py:284-309): T queries at absolute positions first .. first +
 // T - 1 over the S = first + T cached keys. Grid (query tiles of 64, heads,
-// sequences); one wavefront per tile, lane (g, c) = (lane / 4, lane % 4)
-// holding query rows 4 g .. 4 g + 3 of the tile and dims 16 c .. 16 c + 15:
-// each 16-byte read of a key or value from LDS feeds four rows (16 FMAs).
-// Per block of 64 keys staged in LDS, 16 keys at a time: the rows' scores
+// sequences); 128 threads (two wavefronts) per tile, thread (g, c) =
+// (tid / 4, tid % 4) holding query rows 2 g and 2 g + 1 of the tile and dims
+// 16 c .. 16 c + 15: each 16-byte read of a key or value from LDS feeds both
+// rows (eight FMAs). Per block of 64 keys staged in LDS, 16 keys at a time: the rows' scores
 // (16-dim partial dots summed over the row's four lanes by quad DPP moves),
 // the causal mask (-inf past the query's position), an online softmax in
 // fp32 -- the running maximum, the rescale of the partial outputs, the

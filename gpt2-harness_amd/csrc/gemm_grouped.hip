@@ -27,7 +27,7 @@ int run_w4g(const LinearArgs& a, TY* y, int64_t ldy, const float* bias, int64_t 
     const int ngroups = (int)((a.K + kGroup - 1) / kGroup);
     hipLaunchKernelGGL((gemm_staged<kBM, kBN, 1, kW4G, TY>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
                        a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, nullptr, bias, y, ldy,
-                       (int)a.M, (int)a.N, (int)a.K, (int)a.K, a.scale16, ngroups);
+                       (int)a.M, (int)a.N, (int)a.K, (int)a.K, a.scale16, ngroups, nullptr);
     return launch_status();
 }
 

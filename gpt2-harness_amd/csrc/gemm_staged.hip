@@ -18,9 +18,19 @@ int run_staged(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const int64_t slots = 256 * (BM * BN <= 128 * 128 ? 2 : 1);
     const int64_t grid = staged_persist<BM, BN, WMW>() ? std::min(tiles, slots) : tiles;
+    // int8 weights with bf16 output have a stamped copy for measurement
+    if constexpr (FMT == kW8 && sizeof(TY) == 2) {
+        if (uint64_t* sp = stamp_slots(grid)) {
+            hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY, true>), dim3((unsigned)grid), dim3(256), 0,
+                               a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
+                               static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K,
+                               (int)(a.kw ? a.kw : a.K), nullptr, 0, sp);
+            return launch_status();
+        }
+    }
     hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY>), dim3((unsigned)grid), dim3(256), 0, a.stream,
                        static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, static_cast<TY*>(a.y),
-                       a.ldy, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0);
+                       a.ldy, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0, nullptr);
     return launch_status();
 }
 
@@ -173,11 +183,11 @@ int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     if (a.fmt == kW4)
         hipLaunchKernelGGL((gemm_staged<128, 128, 2, kW4, float>), grid, dim3(256), 0, a.stream,
                            static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, part, (int64_t)a.N,
-                           (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0);
+                           (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0, nullptr);
     else
         hipLaunchKernelGGL((gemm_staged<128, 128, 2, kW8, float>), grid, dim3(256), 0, a.stream,
                            static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, part, (int64_t)a.N,
-                           (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0);
+                           (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0, nullptr);
     int rc = launch_status();
     if (rc != TIQ_OK) return rc;
     return launch_splitk_reduce(a, part, S, a.scale);

@@ -113,11 +113,14 @@ __device__ __forceinline__ uint32_t bf16x2_of_x16(uint32_t e, uint32_t o, int k)
 // fp32 accumulation. Built with the MFMA accumulators in AGPRs, the partial
 // tiles live there and the sums, which only the fold and the epilogue touch,
 // in VGPRs.
-template <int BM, int BN, int WMW, int FMT, typename TY>
+// STAMP: the measurement copy (per-workgroup entry / exit times to `stamp`).
+template <int BM, int BN, int WMW, int FMT, typename TY, bool STAMP = false>
 __global__ __launch_bounds__(256, 1) void gemm_staged(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
-    int K, int kw, const uint16_t* __restrict__ scale16, int ngroups) {
+    int K, int kw, const uint16_t* __restrict__ scale16, int ngroups, uint64_t* stamp) {
+    Stamp<STAMP> clock;
+    clock.start();
     static_assert(FMT == kW8 || FMT == kW4 || (FMT == kW4G && WMW == 1),
                   "int8 or reference-layout int4 weights; group-wise int4 in the 1 x 4 layout");
     constexpr bool GROUPED = FMT == kW4G;
@@ -534,6 +537,8 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     if (!more) break;
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's stores
     }
+    if constexpr (STAMP) __syncthreads();  // every wavefront's stores issued
+    clock.finish(stamp, (int64_t)blockIdx.z * gridDim.x + blockIdx.x);
 }
 
 // The kernel's PERSIST condition, on the host: tiles whose accumulators leave

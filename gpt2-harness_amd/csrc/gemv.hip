@@ -407,7 +407,8 @@ __device__ __forceinline__ float4 x4_of<float>(const u32x4& u, int) {
 }
 
 // R weight rows per wavefront (1 or 2) share the activation registers.
-template <int MT, int UM, int R, int FMT, typename TX, typename TY, bool LNF>
+// STAMP: the measurement copy (per-workgroup entry / exit times to `stamp`).
+template <int MT, int UM, int R, int FMT, typename TX, typename TY, bool LNF, bool STAMP = false>
 // The arguments up to M fill the 14 dwords the hardware preloads into SGPRs
 // at wave launch (built with kernarg preloading), so the first loads wait on
 // no kernarg fetch; the grid size is passed rather than read from the
@@ -417,7 +418,10 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
                                                          const TX* __restrict__ x,
                                                          const float* __restrict__ scale, TY* y, int ldw, int ldx,
                                                          int N, int K, int G, int M, int ldy,
-                                                         const float* __restrict__ bias, Fusion fz) {
+                                                         const float* __restrict__ bias, Fusion fz,
+                                                         uint64_t* stamp) {
+    Stamp<STAMP> clock;
+    clock.start();
     constexpr int KC = Fmt<FMT>::KC;
     constexpr int P = KC / 4;                          // float4 of activations per chunk
     constexpr int XB = KC * (int)sizeof(TX);           // activation bytes per chunk and row
@@ -585,6 +589,7 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
                 store_y<TY>(y + (int64_t)(m0 + m) * ldy + n0 + r, v);
             }
         }
+    clock.finish(stamp, (int64_t)blockIdx.y * G + blockIdx.x);
 }
 
 // Fallback for any shape or alignment: one wavefront per output (m, n),
@@ -659,9 +664,20 @@ bool run_direct(const LinearArgs& a, int& rc) {
     if constexpr (direct_fits<MT, UM, FMT, TX, LNF>()) {
         const int G = (int)((a.N + R - 1) / R);
         const dim3 grid((unsigned)G, (unsigned)((a.M + MT - 1) / MT));
+        // int8 weights with bf16 in and out have a stamped copy for measurement
+        if constexpr (FMT == kW8 && sizeof(TX) == 2 && sizeof(TY) == 2 && !LNF) {
+            if (uint64_t* sp = stamp_slots((int64_t)grid.x * grid.y)) {
+                hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, R, FMT, TX, TY, LNF, true>), grid, dim3(64), 0,
+                                   a.stream, a.w, static_cast<const TX*>(a.x), a.scale, static_cast<TY*>(a.y),
+                                   (int)a.ldw, (int)a.ldx, (int)a.N, (int)a.K, G, (int)a.M, (int)a.ldy, a.bias,
+                                   a.fuse, sp);
+                rc = launch_status();
+                return true;
+            }
+        }
         hipLaunchKernelGGL((gemv_direct_kernel<MT, UM, R, FMT, TX, TY, LNF>), grid, dim3(64), 0, a.stream, a.w,
                            static_cast<const TX*>(a.x), a.scale, static_cast<TY*>(a.y), (int)a.ldw, (int)a.ldx,
-                           (int)a.N, (int)a.K, G, (int)a.M, (int)a.ldy, a.bias, a.fuse);
+                           (int)a.N, (int)a.K, G, (int)a.M, (int)a.ldy, a.bias, a.fuse, nullptr);
         rc = launch_status();
         return true;
     }
@@ -783,6 +799,9 @@ int launch_gemv(const LinearArgs& a) {
         case kW4: return dispatch_types<kW4>(a);
         case kW4G: return dispatch_types<kW4G>(a);
         case kF32: return dispatch_types<kF32>(a);
+        // operand-tile layouts are read by the batched decode kernels only
+        case kW8T:
+        case kF32T: return TIQ_EUNSUPPORTED;
     }
     return TIQ_EINVAL;
 }

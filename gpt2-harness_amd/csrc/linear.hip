@@ -2,6 +2,8 @@
 // the decode GEMV (vector ALUs) and the prefill GEMM (matrix cores).
 #include <atomic>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include "tiq_internal.hpp"
 
@@ -20,6 +22,32 @@ int check_linear(const LinearArgs& a) {
     if (a.fmt == kW4 && (a.K % 2)) return TIQ_EINVAL;
     if (a.fmt == kW4G && (a.group < 2 || (a.group & 1))) return TIQ_EINVAL;
     return TIQ_OK;
+}
+
+// Measurement state of tiq_stamp_begin / tiq_stamp_end: the caller's stamp
+// buffer, the slots handed out so far and, per stamped launch, its first
+// slot and workgroup count.
+namespace {
+struct StampState {
+    std::mutex mu;
+    uint64_t* base = nullptr;
+    int64_t slots = 0, used = 0;
+    std::vector<std::pair<int64_t, int64_t>> log;
+};
+StampState& stamp_state() {
+    static StampState st;
+    return st;
+}
+}  // namespace
+
+uint64_t* stamp_slots(int64_t workgroups) {
+    StampState& st = stamp_state();
+    std::lock_guard<std::mutex> lk(st.mu);
+    if (!st.base || workgroups <= 0 || st.used + 2 * workgroups > st.slots) return nullptr;
+    uint64_t* p = st.base + st.used;
+    st.log.emplace_back(st.used, workgroups);
+    st.used += 2 * workgroups;
+    return p;
 }
 
 namespace {
@@ -147,6 +175,31 @@ extern "C" const char* tiq_status_string(int status) {
     }
     if (status <= TIQ_EHIP_BASE) return hipGetErrorString((hipError_t)(TIQ_EHIP_BASE - status));
     return "unknown status";
+}
+
+extern "C" int tiq_stamp_begin(uint64_t* buf, int64_t slots) {
+    if (slots < 0 || (slots > 0 && !buf)) return TIQ_EINVAL;
+    StampState& st = stamp_state();
+    std::lock_guard<std::mutex> lk(st.mu);
+    st.base = slots ? buf : nullptr;
+    st.slots = slots;
+    st.used = 0;
+    st.log.clear();
+    return TIQ_OK;
+}
+
+extern "C" int64_t tiq_stamp_end(int64_t* first_slot, int64_t* workgroups, int64_t max_launches) {
+    StampState& st = stamp_state();
+    std::lock_guard<std::mutex> lk(st.mu);
+    const int64_t n = (int64_t)st.log.size();
+    for (int64_t i = 0; i < n && i < max_launches; ++i) {
+        if (first_slot) first_slot[i] = st.log[i].first;
+        if (workgroups) workgroups[i] = st.log[i].second;
+    }
+    st.base = nullptr;
+    st.slots = st.used = 0;
+    st.log.clear();
+    return n;
 }
 
 extern "C" int tiq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q,

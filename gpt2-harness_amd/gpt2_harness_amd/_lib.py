@@ -24,6 +24,8 @@ _i64, _i32, _vp, _sz, _f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctyp
 #: (name, argtypes, restype) of every exported symbol
 SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_version": ([], _i32),
+    "tiq_stamp_begin": ([_vp, _i64], _i32),
+    "tiq_stamp_end": ([_vp, _vp, _i64], _i64),
     "tiq_status_string": ([_i32], ctypes.c_char_p),
     "tiq_quantize_per_channel": ([_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp], _i32),
     "tiq_quantize_per_tensor_workspace": ([_i64], _sz),

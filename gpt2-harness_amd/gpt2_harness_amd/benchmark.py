@@ -123,8 +123,10 @@ def benchmark_generation(
         torch.manual_seed(0)
         prompt = torch.randint(0, cfg.vocab_size, (batch_size, T)).to(device)
         arms: list[tuple[bool, str, Callable[[], Any]]] = []
+        extra_bytes = 0
         if mode == "graph":
             dec = make_decoder(model, batch_size, T + new_tokens)
+            extra_bytes = int(getattr(dec, "extra_weight_bytes", 0))
             arms.append((True, type(dec).__name__, lambda d=dec, p=prompt: d.run(p, new_tokens)))
         else:
             arms.append((True, "eager", lambda p=prompt: generate(model, p, new_tokens)))
@@ -136,7 +138,8 @@ def benchmark_generation(
                                  median_s=t["median_s"], min_s=t["min_s"], std_s=t["std_s"],
                                  ms_per_token=1e3 * t["median_s"] / new_tokens,
                                  tokens_per_s=new_tokens * batch_size / t["median_s"], device=str(device),
-                                 extra={"decoder": how}))
+                                 extra={"decoder": how,
+                                        "decoder_extra_weight_bytes": extra_bytes if use_cache else 0}))
     return rows
 
 

@@ -271,6 +271,14 @@ class FusedDecoder(_DecoderBase):
                                           torch.cuda.current_stream(dev).cuda_stream), "tile fp32 head")
                 self.tiles[id(model.lm_head)] = t
 
+    @property
+    def extra_weight_bytes(self) -> int:
+        """Device bytes of the weight copies this decoder holds beyond the
+        model's own (the batched step's operand tiles of the int8 block codes
+        and of the fp32 tied head; 0 for one to four sequences, which read the
+        model's row-major codes)."""
+        return sum(t.numel() * t.element_size() for t in getattr(self, "tiles", {}).values())
+
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
         st = torch.cuda.current_stream(self.dev).cuda_stream

@@ -64,7 +64,10 @@ def _speed(model, device, enabled: bool) -> dict[str, Any]:
         return {}
     row = benchmark_generation(model, prompt_lens=[64], new_tokens=16, device=device, repeats=2, warmup=1,
                                both_arms=False)[0]
-    return {"ms_per_token": row.ms_per_token, "tokens_per_s": row.tokens_per_s, "decoder": row.extra["decoder"]}
+    # the speed's memory cost beside quantize_model's packed_bytes: weight
+    # copies the decoder keeps on the device in addition to the model's codes
+    return {"ms_per_token": row.ms_per_token, "tokens_per_s": row.tokens_per_s, "decoder": row.extra["decoder"],
+            "decoder_extra_weight_bytes": row.extra.get("decoder_extra_weight_bytes", 0)}
 
 
 @torch.no_grad()

@@ -75,10 +75,26 @@ class KVCache:
     (``model.py:139-151``).
     """
 
-    def __init__(self, n_layer: int) -> None:
-        self._k: list[torch.Tensor | None] = [None] * n_layer
-        self._v: list[torch.Tensor | None] = [None] * n_layer
-        self._len = [0] * n_layer
+    def __init__(self, keys: int | list[torch.Tensor | None], values: list[torch.Tensor | None] | None = None) -> None:
+        """``KVCache(n_layer)``: an empty cache. ``KVCache(keys=[...],
+        values=[...])`` (the reference's dataclass fields, ``model.py:106-126``):
+        per layer a filled ``(B, heads, T, head_dim)`` history or ``None``;
+        those tensors become the layers' buffers (full: the next append grows
+        them by a copy)."""
+        if isinstance(keys, int):
+            if values is not None:
+                raise ValueError("KVCache(n_layer) takes no values")
+            self._k: list[torch.Tensor | None] = [None] * keys
+            self._v: list[torch.Tensor | None] = [None] * keys
+            self._len = [0] * keys
+            return
+        if values is None or len(keys) != len(values):
+            raise ValueError("KVCache needs keys and values lists of the same length")
+        for k, v in zip(keys, values):
+            if (k is None) != (v is None) or (k is not None and k.shape != v.shape):
+                raise ValueError("each layer's keys and values must both be None or tensors of one shape")
+        self._k, self._v = list(keys), list(values)
+        self._len = [0 if k is None else int(k.shape[-2]) for k in keys]
 
     @classmethod
     def empty(cls, n_layer: int) -> KVCache:
@@ -91,7 +107,7 @@ class KVCache:
         prefill appends into them in place (past ``capacity`` they grow by a
         copy, as an empty cache's do)."""
         cache = cls(len(keys))
-        cache._k, cache._v = list(keys), list(values)
+        cache._k, cache._v = list(keys), list(values)  # buffers, 0 positions filled
         return cache
 
     @property
@@ -105,6 +121,7 @@ class KVCache:
 
     @property
     def keys(self) -> list[torch.Tensor | None]:
+        """Each layer's filled history (views; append with :meth:`update`)."""
         return [None if b is None else b[:, :, :n] for b, n in zip(self._k, self._len)]
 
     @property

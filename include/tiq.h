@@ -56,6 +56,22 @@ enum tiq_weight_format {
 /* Activations fused after a linear. */
 enum tiq_activation { TIQ_ACT_NONE = 0, TIQ_ACT_GELU_TANH = 1 };
 
+/* Measurement of kernel durations inside a timed run (no counterpart in the
+ * reference; for benchmark harnesses). Between tiq_stamp_begin(buf, slots)
+ * and tiq_stamp_end every launch of the decode GEMV's direct kernel (int8
+ * weights, bf16 activations and outputs) and of the staged prefill GEMM
+ * (int8 weights, bf16 output) runs a stamped copy of the kernel that writes,
+ * per workgroup g, its entry and exit time (the GPU's 100 MHz real-time
+ * counter) to buf[s + 2 g] and buf[s + 2 g + 1], s being the launch's first
+ * slot; launches beyond `slots` run unstamped. A launch captured in a HIP
+ * graph keeps its slots, so every replay rewrites them. buf is a device
+ * array of `slots` uint64 (NULL and 0: stamping off). Not thread safe with
+ * launches from other threads. tiq_stamp_end turns stamping off and copies
+ * up to max_launches (first slot, workgroup count) pairs, in launch order,
+ * into the host arrays; it returns the number of stamped launches. */
+int tiq_stamp_begin(uint64_t* buf, int64_t slots);
+int64_t tiq_stamp_end(int64_t* first_slot, int64_t* workgroups, int64_t max_launches);
+
 /* Library version (major*10000 + minor*100 + patch). */
 int tiq_version(void);
 /* Static string naming a status code (never NULL). */
@@ -211,9 +227,12 @@ int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx
  * 319,352,355 at M = B*T). With bf16 x, M >= 128 and a workspace of
  * tiq_gemm_w8_workspace(TIQ_BF16, M, K, N) bytes both split a product with few
  * output tiles over K (group-wise: whole groups a split), the fp32 slices
- * summed in a fixed order. Without a workspace, or where the GEMM does not take the
- * shape (K % 64, group % 64), they compute what tiq_linear_w4 /
- * tiq_linear_w4g compute. */
+ * summed in a fixed order. Where the GEMM does not take the shape (K % 64,
+ * group % 64), and for bf16 x or M < 128 without a workspace, they compute
+ * what tiq_linear_w4 / tiq_linear_w4g compute. With fp32 x, M >= 128 and a
+ * shape the GEMM takes, the planes need the workspace: TIQ_EWORKSPACE when it
+ * is NULL, smaller than tiq_linear_w8_workspace(x_dtype, M, K) or not 16-byte
+ * aligned (as tiq_linear_w8_ws). */
 int tiq_linear_w4_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                      const uint8_t* packed, const float* scale, const float* bias, int64_t N,
                      void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
@@ -344,7 +363,10 @@ int tiq_decode_linear(const float* x, int64_t ldx, const uint16_t* x_planes, int
  * fixed TIQ_NOALLOC_SCRATCH_BYTES array on the device of `stream`, so it
  * allocates nothing and returns TIQ_ESCRATCH (before any launch) when
  * tiq_decode_linear_workspace(w_format, M, K, N) exceeds that size (GPT-2-XL
- * shapes at M <= 64 need at most 4 MB). Every call on one GPU shares the
+ * block shapes at M <= 64 need at most 4.1 MB; the tied fp32 head in the
+ * row-major TIQ_WF_F32 layout, N = 50257 rows of K = 1600, needs 13.5 MB at
+ * M = 64: 0.6 MB of operand planes and one 12.9 MB partial slice; in the
+ * TIQ_WF_F32_TILED layout it needs none). Every call on one GPU shares the
  * array: calls that overlap on one GPU (concurrent streams, threads) race.
  * The first call on a device looks up the array's device address
  * (hipGetSymbolAddress); make that call outside stream capture. */

@@ -210,20 +210,26 @@ def forward(p, cfg: Shape, idx: torch.Tensor, cache: Cache | None = None, last_o
 
 
 @torch.no_grad()
-def generate_greedy(p, cfg: Shape, idx: torch.Tensor, max_new_tokens: int):
+def generate_greedy(p, cfg: Shape, idx: torch.Tensor, max_new_tokens: int, detail: bool = False):
     """Greedy cached decode. Returns ``(ids (B, T+n), margins (n,))`` where a
-    margin is the smallest top-1 minus top-2 logit gap over the batch."""
+    margin is the smallest top-1 minus top-2 logit gap over the batch; with
+    ``detail`` also the per-sequence gaps ``(n, B)`` and the last step's
+    logits ``(B, V)``."""
     cache = Cache(cfg.n_layer)
-    margins = []
+    margins, gaps, logits = [], [], None
     for step in range(max_new_tokens):
         if idx.size(1) >= cfg.n_positions:
             break
         step_input = idx if step == 0 else idx[:, -1:]
         logits = forward(p, cfg, step_input, cache, last_only=True)[:, -1, :]
         top2 = logits.topk(2, dim=-1).values
-        margins.append(float((top2[:, 0] - top2[:, 1]).min()))
+        gap = top2[:, 0] - top2[:, 1]
+        margins.append(float(gap.min()))
+        gaps.append(gap)
         nxt = logits.argmax(dim=-1, keepdim=True)
         idx = torch.cat([idx, nxt], dim=1)
+    if detail:
+        return idx, margins, torch.stack(gaps) if gaps else torch.empty(0, idx.size(0)), logits
     return idx, margins
 
 

@@ -150,6 +150,24 @@ def test_kv_cache_over_preallocated_buffers():
     assert torch.equal(kk[:, :, :5], k) and torch.equal(kk[:, :, 5:], k)
 
 
+def test_kv_cache_reference_constructor():
+    """KVCache(keys=..., values=...) as the reference's dataclass is built
+    (model.py:106-126): filled histories per layer (None: empty), lengths from
+    them, appends continue the history; mismatched lists are refused."""
+    k0 = torch.arange(2 * 3 * 4 * 4, dtype=torch.float32).view(2, 3, 4, 4)
+    c = g.KVCache(keys=[k0, None], values=[-k0, None])
+    assert c.seq_len == 4 and c.length(1) == 0
+    assert torch.equal(c.keys[0], k0) and torch.equal(c.values[0], -k0) and c.keys[1] is None
+    step = torch.ones(2, 3, 1, 4)
+    kk, vv = c.update(0, step, -step)
+    assert torch.equal(kk, torch.cat([k0, step], dim=2)) and torch.equal(vv, torch.cat([-k0, -step], dim=2))
+    assert g.KVCache.empty(3).length(2) == 0
+    with pytest.raises(ValueError):
+        g.KVCache(keys=[k0], values=[])
+    with pytest.raises(ValueError):
+        g.KVCache(keys=[k0], values=[None])
+
+
 def test_synthetic_token_stream_windows():
     """The perplexity windows: non-overlapping blocks of T predictions that
     share one id with the next (ids[wT : wT + T + 1]), y = x shifted by one,
@@ -260,3 +278,28 @@ def test_chunk_spread_statistics():
     assert abs(d["ppl_of_mean_loss"] - math.exp(mean)) < 1e-9
     one = _chunk_spread([0.5])
     assert one["loss_std"] == 0.0 and one["ppl_std"] == 0.0 and one["ppl_mean"] == math.exp(0.5)
+
+
+def test_greedy_agreement_reports_first_divergence():
+    """bench.greedy_agreement: equal generations report the last-step logit
+    difference; a token planted at step 5 of sequence 2 (and one later in
+    sequence 0) is reported as the first divergence, with the oracle's gap
+    there."""
+    import bench
+
+    gen = torch.Generator().manual_seed(0)
+    want = torch.randint(0, 100, (3, 4 + 8), generator=gen)
+    gaps = torch.rand(8, 3, generator=gen) + 0.5
+    gaps[5, 2] = 0.001
+    last = torch.randn(3, 100, generator=gen)
+    a = bench.greedy_agreement(want.clone(), want, gaps, last + 1e-6, last, 4)
+    assert a["tokens_match"] and a["steps"] == 8 and a["sequences"] == 3
+    assert abs(a["last_step_max_abs_logit_diff"] - 1e-6) < 1e-7 and "first_divergence" not in a
+    got = want.clone()
+    got[2, 4 + 5] += 1
+    got[0, 4 + 7] += 1
+    b = bench.greedy_agreement(got, want, gaps, None, last, 4)
+    assert not b["tokens_match"]
+    assert b["first_divergence"] == {"step": 5, "sequence": 2, "oracle_top2_margin": float(gaps[5, 2]),
+                                     "steps_all_equal": 5}
+    assert abs(b["min_top2_margin"] - 0.001) < 1e-6

@@ -91,6 +91,40 @@ def test_noalloc_equals_workspace_entry_on_two_calls(dev):
         assert torch.equal(planes, planes_ref), f"M={c['M']} K={c['K']} N={c['N']}: operand planes differ"
 
 
+def test_noalloc_fp32_head_shape(dev):
+    """The tied fp32 head of GPT-2-XL at 64 rows (row-major TIQ_WF_F32, no
+    scale or bias): 13.5 MB of its 16 MiB scratch -- operand planes and one
+    partial slice -- equal to the workspace entry bit for bit."""
+    L = _lib.lib()
+    M, K, N = 64, 1600, 50257
+    need = int(L.tiq_decode_linear_workspace(_lib.WF_F32, M, K, N))
+    assert 13_000_000 < need <= SCRATCH_BYTES
+    gen = torch.Generator(device=dev).manual_seed(5)
+    w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+    x = torch.randn(M, K, generator=gen, device=dev)
+    ln = (1 + 0.1 * torch.randn(K, generator=gen, device=dev), 0.1 * torch.randn(K, generator=gen, device=dev))
+
+    def call(y, ws):
+        args = [x.data_ptr(), x.stride(0), None, M, K, w.data_ptr(), _lib.WF_F32, None, None, N, y.data_ptr(),
+                y.stride(0), ln[0].data_ptr(), ln[1].data_ptr(), 1e-5, _lib.ACT_NONE, None, 0, None, None, 1e-5,
+                None]
+        if ws is None:
+            return L.tiq_decode_linear_noalloc(*args, _st())
+        return L.tiq_decode_linear(*args, ws.data_ptr(), ws.numel(), _st())
+
+    y = torch.full((M, N), 7.0, device=dev)
+    _lib.check(call(y, None), "tiq_decode_linear_noalloc (fp32 head)")
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    y_ref = torch.full((M, N), 7.0, device=dev)
+    _lib.check(call(y_ref, ws), "tiq_decode_linear (fp32 head)")
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(y, y_ref)
+    # and the head's result is the LayerNorm'd rows times the weights (fp32)
+    ref = torch.nn.functional.layer_norm(x.double(), (K,), ln[0].double(), ln[1].double(), 1e-5) @ w.double().T
+    assert (y.double() - ref).abs().max().item() <= 1e-3 * ref.abs().max().item()
+
+
 def test_noalloc_refuses_beyond_its_scratch(dev):
     """64 rows of K = 12800 into N = 8192 need 21.7 MB (planes plus eight
     partial slices): refused before any launch. The buffers are full size
