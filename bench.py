@@ -437,13 +437,13 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
         if stamped and fmt == "int8":
             # the same timed launches again, the stamped copy of the staged
             # kernel: each launch's first-workgroup entry to last-workgroup exit
-            st = Stamps(dev)
-            st.begin()
+            stamps = Stamps(dev)
+            stamps.begin()
             try:
                 us_st = timed([lambda a=a: run(*a) for a in sets])
             finally:
-                st.end()
-            d = st.durations_us()[3:]  # after timed()'s three warm-up launches
+                stamps.end()
+            d = stamps.durations_us()[3:]  # after timed()'s three warm-up launches
             if len(d) == reps:  # one stamped kernel a launch (no split-K at this size)
                 kus = statistics.fmean(d)
                 stamp = {"kernel_us": kus, "TFLOP/s": 2.0 * M * N * K / (kus * 1e-6) / 1e12, "launch_us": us_st}

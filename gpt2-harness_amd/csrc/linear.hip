@@ -160,7 +160,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 119; }
+extern "C" int tiq_version(void) { return 120; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
