@@ -73,12 +73,6 @@ __device__ __forceinline__ void staged_tile_of(int i, int& tm, int& tn, int tile
     tn = in / gm;
 }
 
-__device__ __forceinline__ uint32_t bf16x2_of_bytes_perm(uint32_t d, int sh) {
-    const float lo = (float)((int32_t)(d << (24 - sh)) >> 24);
-    const float hi = (float)((int32_t)(d << (16 - sh)) >> 24);
-    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
 // Nibbles as bf16 times 16: d holds 8 biased nibbles (column 2j in the low
 // nibble of byte j, code n - 8); e (even columns) and o (odd columns) get
 // each nibble in the high half of a byte with its top bit flipped, which as

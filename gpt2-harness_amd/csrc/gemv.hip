@@ -31,13 +31,17 @@
 //     moves; the per-channel scale and the bias are applied once per
 //     output; the group-wise format scales each 32-column chunk's partial sum
 //     by its group's fp16 scale.
+// gemv_rows16_kernel (4..16 bf16 rows, int8 weights): 16 (or 8, 4) weight
+// rows a workgroup on the matrix cores, so the activations are read once per
+// block of rows instead of once per row; see the kernel.
+//
 // Optional fusions for the decode step of a GPT-2 block (model.py:410-427):
 // LayerNorm of the staged activation rows (two-pass mean / variance over the
 // row held in LDS), GELU(tanh) of the output (model.py:57-75) and a residual
 // added to it (x + f(x)), so one launch replaces LayerNorm + Linear + GELU or
 // Linear + add. The fp32 weight format serves the unquantized tied lm_head.
-// No MFMA: at M <= 4 the int8->fp32 convert plus M FMAs per weight byte stay
-// within the VALU budget of the HBM stream.
+// The first two kernels use no MFMA: at M <= 4 the int8->fp32 convert plus M
+// FMAs per weight byte stay within the VALU budget of the HBM stream.
 #include "tiq_internal.hpp"
 
 namespace tiq {
@@ -592,6 +596,98 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
     clock.finish(stamp, (int64_t)blockIdx.y * G + blockIdx.x);
 }
 
+// Decode GEMV on the matrix cores for 2..16 bf16 activation rows and int8
+// weights: a workgroup takes 16 weight rows and every activation row, so the
+// activations are read once per 16 weight rows (the direct kernel reads them
+// once per row); its W wavefronts split K into runs of `pw` 64-column pairs.
+// For pair p a lane holds the 16 weight bytes of row n0 + l % 16 and the 16
+// bf16 of activation row l % 16 at columns 64 p + 16 (l / 16) .. + 15: two
+// v_mfma_f32_16x16x32_bf16, A = activations, B = weights (both operands
+// take a lane's 8 values from the same columns, so the pairing of columns
+// needs no particular order inside the instruction; an int8 code is exact in
+// bf16, every product is exact, fp32 sums). Loads go through buffer
+// descriptors sized to the 16 weight rows and the M activation rows: a row
+// past N or M, or a pair past the wavefront's run, reads zero with no memory
+// access and adds exact zeros, so no load is clamped or branched around.
+// Lane l ends with D[4 (l / 16) + q][l % 16], q = 0..3 (activation row,
+// weight row); the W partial tiles meet in LDS and one thread per output
+// sums them in wavefront order and applies scale, bias, activation and
+// residual.
+typedef __bf16 r16_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float r16_floatx4 __attribute__((ext_vector_type(4)));
+
+template <int W, int UP, typename TY>
+__global__ __launch_bounds__(64 * W) void gemv_rows16_kernel(const uint8_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ x,
+                                                            const float* __restrict__ scale, TY* y, int ldw, int ldx,
+                                                            int N, int K, int G, int M, int ldy, int pw, int rb,
+                                                            const float* __restrict__ bias, Fusion fz) {
+    static_assert(W >= 4, "one epilogue thread per output of the 16 x 16 tile");
+    __shared__ r16_floatx4 part[W][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = xcd_block(blockIdx.x, G) * rb;  // weight rows n0 .. n0 + rows - 1
+    const int rows = min(rb, N - n0);
+    // bytes each descriptor covers; an offset at or past them reads zero (the
+    // host keeps both below 2^31 - 256, so offset + 16 does not wrap)
+    const int wbytes = (rows - 1) * ldw + K, xbytes = ((M - 1) * ldx + K) * 2;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(w) + (int64_t)n0 * ldw, (short)0, wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, xbytes, 0x00020000);
+    const int first = wave * pw, cnt = min(pw, K / 64 - first);  // this wavefront's pairs
+    u32x4 wq[UP], xa[UP][2];
+#pragma unroll
+    for (int j = 0; j < UP; ++j) {
+        const int k0 = 64 * (first + j) + 16 * g;
+        wq[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, j < cnt ? r * ldw + k0 : wbytes, 0, 2);  // nontemporal
+    }
+#pragma unroll
+    for (int j = 0; j < UP; ++j) {
+        const int xo = j < cnt ? (r * ldx + 64 * (first + j) + 16 * g) * 2 : xbytes;
+        xa[j][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        xa[j][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+    }
+    // epilogue operands of this thread's output (row m = tid / 16, weight row
+    // n0 + tid % 16), requested beside the tiles
+    const int em = min(tid >> 4, M - 1), en = min(n0 + (tid & 15), N - 1);
+    const float ep_scale = scale[en];
+    const float ep_bias = bias ? bias[en] : 0.f;
+    float ep_res = 0.f;
+    if (fz.res) ep_res = fz.res[(int64_t)em * fz.ldr + en];
+    asm volatile("" ::"v"(ep_scale), "v"(ep_bias), "v"(ep_res));
+
+    r16_floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < UP; ++j) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const uint32_t d0 = s ? wq[j].z : wq[j].x, d1 = s ? wq[j].w : wq[j].y;
+            const u32x4 b = {bf16x2_of_bytes_perm(d0, 0), bf16x2_of_bytes_perm(d0, 16), bf16x2_of_bytes_perm(d1, 0),
+                             bf16x2_of_bytes_perm(d1, 16)};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(r16_bf16x8, xa[j][s]),
+                                                          __builtin_bit_cast(r16_bf16x8, b), acc, 0, 0, 0);
+        }
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (tid < 256) {
+        const int m = tid >> 4, n = tid & 15;
+        const float* pf = reinterpret_cast<const float*>(part);
+        const int at = (16 * (m >> 2) + n) * 4 + (m & 3);  // lane 16 (m / 4) + n, register m % 4
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < W; ++v) sum += pf[v * 256 + at];
+        if (m < M && n < rows) {
+            float o = sum * ep_scale + ep_bias;
+            o = apply_act(o, fz.act);
+            if (fz.res) o += ep_res;
+            store_y<TY>(y + (int64_t)m * ldy + n0 + n, o);
+        }
+    }
+}
+
 // Fallback for any shape or alignment: one wavefront per output (m, n),
 // scalar loads.
 template <int FMT, typename TX, typename TY>
@@ -743,6 +839,37 @@ bool try_direct(const LinearArgs& a, int& rc) {
     }
 }
 
+template <int W, int UP, typename TY>
+int run_rows16(const LinearArgs& a, int rb = 16) {
+    const int P = (int)(a.K / 64), pw = (P + W - 1) / W;
+    const int G = (int)((a.N + rb - 1) / rb);
+    hipLaunchKernelGGL((gemv_rows16_kernel<W, UP, TY>), dim3((unsigned)G), dim3(64 * W), 0, a.stream, a.w,
+                       static_cast<const uint16_t*>(a.x), a.scale, static_cast<TY*>(a.y), (int)a.ldw, (int)a.ldx,
+                       (int)a.N, (int)a.K, G, (int)a.M, (int)a.ldy, pw, rb, a.bias, a.fuse);
+    return launch_status();
+}
+
+
+// Many wavefronts with short runs: one pair a wavefront up to 16 pairs
+// (4, 8, 12 or 16 wavefronts), then 16 wavefronts with 2, 3, 4 or 7 pairs
+// each. Weight rows a workgroup: 16 on wide matrices, 8 or 4 on narrower
+// ones, so the grid stays near 150 workgroups or more (narrower blocks leave
+// MFMA columns zero, which costs no memory traffic). Both from a sweep over
+// GPT-2 small and XL shapes at M = 4 / 8 / 16 (graph-timed, cold weights).
+template <typename TY>
+int dispatch_rows16(const LinearArgs& a) {
+    const int64_t P = a.K / 64;
+    const int rb = a.N >= 2048 ? 16 : a.N >= 1200 ? 8 : 4;
+    if (P <= 4) return run_rows16<4, 1, TY>(a, rb);
+    if (P <= 8) return run_rows16<8, 1, TY>(a, rb);
+    if (P <= 12) return run_rows16<12, 1, TY>(a, rb);
+    if (P <= 16) return run_rows16<16, 1, TY>(a, rb);
+    if (P <= 32) return run_rows16<16, 2, TY>(a, rb);
+    if (P <= 48) return run_rows16<16, 3, TY>(a, rb);
+    if (P <= 64) return run_rows16<16, 4, TY>(a, rb);
+    return run_rows16<16, 7, TY>(a, rb);
+}
+
 template <int FMT, typename TX, typename TY>
 int run_generic(const LinearArgs& a) {
     const int64_t outs = a.M * a.N;
@@ -766,6 +893,8 @@ int dispatch_fmt(const LinearArgs& a) {
         return run_generic<FMT, TX, TY>(a);
     }
     int rc = TIQ_OK;
+    if constexpr (FMT == kW8 && sizeof(TX) == 2)
+        if (rows16_preferred(a)) return launch_rows16(a);
     // up to 4 rows; up to 16 bf16 rows without fusions on narrow matrices
     // (N < 2048), four rows a tile, where the batched kernel has too few tiles
     const bool direct_rows = a.M <= 4 || (a.M <= 16 && a.N < 2048 && a.x_dtype == TIQ_BF16 && !fused);
@@ -792,6 +921,30 @@ int dispatch_types(const LinearArgs& a) {
 }
 
 }  // namespace
+
+bool rows16_supported(const LinearArgs& a) {
+    if (a.fmt != kW8 || a.x_dtype != TIQ_BF16 || a.fuse.ln_w || a.M < 2 || a.M > 16) return false;
+    if (a.K % 64 != 0 || a.K / 64 > 112 || a.N > 0x7fffffff) return false;
+    if (!aligned(a.x, 16) || a.ldx % 8 != 0 || !aligned(a.w, 16) || a.ldw % 16 != 0) return false;
+    if (a.fuse.res && a.fuse.res != a.y && a.fuse.ldr < a.N) return false;
+    // the descriptors' 32-bit byte offsets: 16 weight rows, M activation rows
+    if (15 * a.ldw + a.K > 0x7fffff00LL || ((a.M - 1) * a.ldx + a.K) * 2 > 0x7fffff00LL) return false;
+    if (a.ldy > INT32_MAX || a.ldx > INT32_MAX || a.ldw > INT32_MAX) return false;
+    return true;
+}
+
+// Where it beats the direct kernel and the batched one (graph-timed, cold
+// weights, GPT-2 small and XL shapes): from 4 rows on matrices of 1200 rows
+// or more, from 9 rows on narrower ones (at 768 rows the direct kernel's
+// 768 one-wavefront workgroups win up to 8 rows).
+bool rows16_preferred(const LinearArgs& a) {
+    if (a.M < 4 || (a.N < 1200 && a.M <= 8)) return false;
+    return rows16_supported(a);
+}
+
+int launch_rows16(const LinearArgs& a) {
+    return a.y_dtype == TIQ_F32 ? dispatch_rows16<float>(a) : dispatch_rows16<uint16_t>(a);
+}
 
 int launch_gemv(const LinearArgs& a) {
     switch (a.fmt) {

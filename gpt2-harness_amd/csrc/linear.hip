@@ -150,6 +150,7 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes, bool gelu_i
 int run_linear(const LinearArgs& a) {
     int rc = check_linear(a);
     if (rc != TIQ_OK || a.M == 0 || a.N == 0) return rc;
+    if (rows16_preferred(a)) return launch_rows16(a);
     if (skinny_supported(a)) return launch_skinny(a);
     if (a.M >= kGemmMinRows && gemm_supported(a)) return launch_gemm(a);
     return launch_gemv(a);
@@ -332,6 +333,7 @@ static int linear_fused(const void* x, int x_dtype, int64_t M, int64_t K, int64_
     a.ws_bytes = workspace_bytes;
     int rc = check_linear(a);
     if (rc != TIQ_OK || M == 0 || N == 0) return rc;
+    if (rows16_preferred(a)) return launch_rows16(a);
     if (skinny_supported(a)) return launch_skinny(a);
     return launch_gemv(a);
 }

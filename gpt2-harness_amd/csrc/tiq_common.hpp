@@ -150,6 +150,14 @@ __device__ __forceinline__ void split3_words(const float (&x)[8], uint32_t (&pl)
 }
 
 // Sign-extended byte `i` of a dword, as float.
+// Signed bytes sh / 8 and sh / 8 + 1 of d as two bf16 (low half = the lower
+// byte): an int8 code is exact in bf16, so the top half of its float is it.
+__device__ __forceinline__ uint32_t bf16x2_of_bytes_perm(uint32_t d, int sh) {
+    const float lo = (float)((int32_t)(d << (24 - sh)) >> 24);
+    const float hi = (float)((int32_t)(d << (16 - sh)) >> 24);
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
 template <int I>
 __device__ __forceinline__ float sbyte_f32(uint32_t d) {
     return (float)((int32_t)(d << (24 - 8 * I)) >> 24);

@@ -62,6 +62,12 @@ uint64_t* stamp_slots(int64_t workgroups);
 int check_linear(const LinearArgs& a);
 
 int launch_gemv(const LinearArgs& a);
+// Decode GEMV on the matrix cores for 2..16 bf16 rows and int8 weights
+// (gemv.hip): whether it takes these arguments, whether the dispatch picks
+// it over the direct and batched kernels, and its launch.
+bool rows16_supported(const LinearArgs& a);
+bool rows16_preferred(const LinearArgs& a);
+int launch_rows16(const LinearArgs& a);
 int launch_gemm(const LinearArgs& a);
 // The GEMM with a given tile configuration: 0 automatic, 1-4 the LDS-dequant
 // kernel's tiles (gemm.hip), 10-15 the staged int8 kernel's (256x256, 256x128,

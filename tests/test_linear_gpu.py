@@ -153,11 +153,13 @@ def test_linear_w8_fp32_matrix_cores(dev, c_oracle, K, N, M):
     assert err_gpu <= 8 * max(err_cpu, floor), f"error {err_gpu:.3g} vs fp32 oracle {err_cpu:.3g}"
 
 
-# bf16 activations at 5..64 rows take the matrix-core decode kernel (one bf16
-# plane: every int8 x bf16 product is exact, fp32 accumulation); K beyond its
-# register budget (6400) takes the GEMV. Besides the 1e-3 contract, the fp32
-# result is held to a small multiple of torch fp32's own error against a
-# float64 computation of the same product.
+# bf16 activations at 4..16 rows take the 16-row matrix-core GEMV (9..16 rows
+# on matrices under 1200 rows; fewer rows there stay on the direct GEMV), at
+# 17..64 rows the batched matrix-core kernel (one bf16 plane: every int8 x bf16
+# product is exact, fp32 accumulation); K beyond its register budget (6400)
+# takes the GEMV. Besides the 1e-3 contract, the fp32 result is held to a
+# small multiple of torch fp32's own error against a float64 computation of
+# the same product.
 @pytest.mark.parametrize("KN", SMALL + [(1600, 4800), (6400, 1600)])
 @pytest.mark.parametrize("M", [5, 16, 33, 64])
 def test_linear_w8_bf16_batched(dev, c_oracle, KN, M):
@@ -176,10 +178,50 @@ def test_linear_w8_bf16_batched(dev, c_oracle, KN, M):
     assert err <= 8 * max(err32, 2.0 ** -24 * float(ref64.abs().max())), (err, err32)
 
 
+# The 16-row matrix-core GEMV at its edges: weight-row blocks of 16, 8 and 4
+# (N >= 2048, >= 1200, smaller) with a partial last block, K of one 64-column
+# pair (4 wavefronts, three of them idle) up to 100 pairs (16 wavefronts of 7),
+# runs that leave the last wavefronts without pairs (K = 1600: 25 pairs over
+# 16 wavefronts of 2), 4 / 9 / 16 rows, fp32 and bf16 output.
+@pytest.mark.parametrize("K,N", [(64, 40), (768, 1212), (1600, 2056), (3072, 1200), (6400, 768), (4160, 2048)])
+@pytest.mark.parametrize("M", [4, 9, 16])
+def test_rows16_edges(dev, c_oracle, K, N, M):
+    _run_w8("tiq_linear_w8", dev, c_oracle, K, N, M, torch.bfloat16, seed=K + N + M, bias=M != 9)
+
+
+@pytest.mark.parametrize("M,K,N", [(12, 768, 1212), (16, 1600, 4800), (4, 6400, 1600)])
+def test_rows16_gelu_and_residual_in_place(dev, c_oracle, M, K, N):
+    """GELU epilogue, then a residual added in place (y aliases it), bf16 rows."""
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, M * 7 + K, torch.bfloat16)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    qd, sd, bd, xd = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
+    st = torch.cuda.current_stream().cuda_stream
+    w_hat = OL.dequantize(q, s)
+    lin = OL.linear_ref(x, w_hat, b)
+    y = torch.empty(M, N, device=dev)
+    rc = L.tiq_linear_fused(xd.data_ptr(), 1, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
+                            bd.data_ptr(), N, y.data_ptr(), 0, N, None, None, 1e-5, 1, None, 0, st)
+    _lib.check(rc, "rows16 gelu")
+    torch.cuda.synchronize()
+    gelu = 0.5 * lin * (1 + torch.tanh(0.7978845608028654 * (lin + 0.044715 * lin ** 3)))
+    ok, err, bound = OL.within_tolerance(y, gelu, TOL)
+    assert ok, (err, bound)
+    r0 = torch.randn(M, N, generator=torch.Generator().manual_seed(M))
+    yr = r0.to(dev)
+    rc = L.tiq_linear_fused(xd.data_ptr(), 1, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
+                            bd.data_ptr(), N, yr.data_ptr(), 0, N, None, None, 1e-5, 0, yr.data_ptr(), N, st)
+    _lib.check(rc, "rows16 residual")
+    torch.cuda.synchronize()
+    ok, err, bound = OL.within_tolerance(yr, r0 + lin, TOL)
+    assert ok, (err, bound)
+
+
 @pytest.mark.parametrize("pad", [64, 4])
 def test_linear_w8_bf16_strided_rows(dev, c_oracle, pad):
-    """Row stride K + 64 (16-byte rows: matrix-core kernel) and K + 4 (8-byte
-    rows: the GEMV), strided output; nothing written outside the outputs."""
+    """Row stride K + 64 (16-byte rows: the 16-row matrix-core GEMV) and K + 4
+    (8-byte rows: the GEMV), strided output; nothing written outside the
+    outputs."""
     K, N, M = 768, 2304, 16
     w, x, b = _inputs(K, N, M, pad, torch.bfloat16)
     q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
