@@ -190,10 +190,12 @@ def per_shape_graph_times(ls: LinearSet, reps: int, entry: str = "tiq_linear_w8"
 class Stamps:
     """Kernel durations measured inside a timed run: between begin() and
     end() every stamped launch (tiq_stamp_begin) writes each workgroup's entry
-    and exit time (the GPU's 100 MHz real-time counter); a launch's duration
-    is its first workgroup's entry to its last workgroup's exit. Launches
-    captured in a graph keep their slots, so after the timed replays the
-    slots hold the last replay of each graph."""
+    and exit on the GPU's 100 MHz real-time counter and on its shader-clock
+    counter (four slots a workgroup); a launch's duration is its first
+    workgroup's entry to its last workgroup's exit, its clock the shader
+    cycles over the real time summed over its workgroups. Launches captured in
+    a graph keep their slots, so after the timed replays the slots hold the
+    last replay of each graph."""
 
     def __init__(self, dev, slots=1 << 23):
         import torch
@@ -218,15 +220,18 @@ class Stamps:
         self.launches = [(first[i], wgs[i]) for i in range(min(k, n))]
         return len(self.launches)
 
-    def durations_us(self):
-        """Per stamped launch: (last exit - first entry) in us."""
+    def _slots(self):
         self.torch.cuda.synchronize()
         h = self.buf.cpu()
-        out = []
-        for s0, g in self.launches:
-            t = h[s0: s0 + 2 * g].view(g, 2)
-            out.append(float(t[:, 1].max() - t[:, 0].min()) * 0.01)
-        return out
+        return [h[s0: s0 + 4 * g].view(g, 4) for s0, g in self.launches]
+
+    def durations_us(self):
+        """Per stamped launch: (last exit - first entry) in us."""
+        return [float(t[:, 1].max() - t[:, 0].min()) * 0.01 for t in self._slots()]
+
+    def clocks_ghz(self):
+        """Per stamped launch: shader cycles / real time over its workgroups, GHz."""
+        return [float((t[:, 3] - t[:, 2]).sum()) / float((t[:, 1] - t[:, 0]).sum() * 10) for t in self._slots()]
 
 
 def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed, per_shape=True, stamped=False):
@@ -251,9 +256,11 @@ def gemv_section(M, kn, layers, copies, steps, warmup, dev, seed, per_shape=True
             raise RuntimeError(f"stamped launches {n}, expected {want}")
         ms_st = replay_ms(graphs, steps, warmup)
         d = st.durations_us()[ls.launches_per_copy:]  # the captured launches (the first ones ran eagerly)
+        clk = statistics.fmean(st.clocks_ghz()[ls.launches_per_copy:])
         kus = statistics.fmean(d)
         res["stamped"] = {"kernel_us": kus, "kernel_us_min": min(d), "kernel_us_max": max(d), "launches": len(d),
-                          "ms_per_step": ms_st, "kernel_sum_over_step": kus * ls.launches_per_copy / (ms_st * 1e3)}
+                          "ms_per_step": ms_st, "kernel_sum_over_step": kus * ls.launches_per_copy / (ms_st * 1e3),
+                          "clock_GHz": clk}
         res["kernel_us"] = kus
         res["kernel_GB/s"] = ls.bytes_per_copy / ls.launches_per_copy / (kus * 1e-6) / 1e9
         del graphs
@@ -446,7 +453,11 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
             d = stamps.durations_us()[3:]  # after timed()'s three warm-up launches
             if len(d) == reps:  # one stamped kernel a launch (no split-K at this size)
                 kus = statistics.fmean(d)
-                stamp = {"kernel_us": kus, "TFLOP/s": 2.0 * M * N * K / (kus * 1e-6) / 1e12, "launch_us": us_st}
+                clk = statistics.fmean(stamps.clocks_ghz()[3:])
+                tf_k = 2.0 * M * N * K / (kus * 1e-6) / 1e12
+                # the matrix cores' peak scales with the shader clock (datasheet: 2.4 GHz)
+                stamp = {"kernel_us": kus, "TFLOP/s": tf_k, "launch_us": us_st, "clock_GHz": clk,
+                         "frac_of_peak_at_clock": tf_k / (BF16_PEAK_TFLOPS * clk / 2.4)}
         us_lib = timed([lambda x=x, wb=wb: torch.matmul(x, wb.T) for x, wb in lib_sets])
         tf_lib = 2.0 * M * N * K / (us_lib * 1e-6) / 1e12
         out[f"{K}x{N}"] = {"us": us, "TFLOP/s": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,

@@ -43,10 +43,10 @@ StampState& stamp_state() {
 uint64_t* stamp_slots(int64_t workgroups) {
     StampState& st = stamp_state();
     std::lock_guard<std::mutex> lk(st.mu);
-    if (!st.base || workgroups <= 0 || st.used + 2 * workgroups > st.slots) return nullptr;
+    if (!st.base || workgroups <= 0 || st.used + 4 * workgroups > st.slots) return nullptr;
     uint64_t* p = st.base + st.used;
     st.log.emplace_back(st.used, workgroups);
-    st.used += 2 * workgroups;
+    st.used += 4 * workgroups;
     return p;
 }
 
@@ -161,7 +161,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 120; }
+extern "C" int tiq_version(void) { return 121; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {

@@ -195,22 +195,30 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     return t[0];
 }
 
-// Per-workgroup entry and exit times (the GPU's 100 MHz real-time counter)
-// of a measurement launch: slot 2 g holds workgroup g's entry time, 2 g + 1
-// its exit time. Off (ON = false) the kernel is the product kernel, unchanged.
+// Per-workgroup entry and exit of a measurement launch: slots 4 g and 4 g + 1
+// hold workgroup g's entry and exit on the GPU's 100 MHz real-time counter,
+// 4 g + 2 and 4 g + 3 the same two moments on the shader-clock counter (its
+// ratio to the real time is the clock the workgroup ran at). Off (ON =
+// false) the kernel is the product kernel, unchanged.
 template <bool ON>
 struct Stamp {
-    uint64_t t0 = 0;
+    uint64_t t0 = 0, c0 = 0;
     __device__ __forceinline__ void start() {
-        if constexpr (ON) t0 = __builtin_amdgcn_s_memrealtime();
+        if constexpr (ON) {
+            t0 = __builtin_amdgcn_s_memrealtime();
+            c0 = __builtin_amdgcn_s_memtime();
+        }
     }
-    // after the workgroup's last store is issued; thread 0 writes both times
+    // after the workgroup's last store is issued; thread 0 writes the slots
     __device__ __forceinline__ void finish(uint64_t* slots, int64_t wg) {
         if constexpr (ON) {
+            const uint64_t c1 = __builtin_amdgcn_s_memtime();
             const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
             if (threadIdx.x == 0 && slots) {
-                slots[2 * wg] = t0;
-                slots[2 * wg + 1] = t1;
+                slots[4 * wg] = t0;
+                slots[4 * wg + 1] = t1;
+                slots[4 * wg + 2] = c0;
+                slots[4 * wg + 3] = c1;
             }
         }
     }

@@ -53,7 +53,7 @@ struct LinearArgs {
     size_t ws_bytes = 0;
 };
 
-// Measurement (tiq_stamp_begin): 2 * workgroups slots of the stamp buffer for
+// Measurement (tiq_stamp_begin): 4 * workgroups slots of the stamp buffer for
 // the next launch of a stamped kernel, or nullptr when stamping is off or
 // the buffer is full (the launch then runs the unstamped kernel).
 uint64_t* stamp_slots(int64_t workgroups);

@@ -61,9 +61,11 @@ enum tiq_activation { TIQ_ACT_NONE = 0, TIQ_ACT_GELU_TANH = 1 };
  * and tiq_stamp_end every launch of the decode GEMV's direct kernel (int8
  * weights, bf16 activations and outputs) and of the staged prefill GEMM
  * (int8 weights, bf16 output) runs a stamped copy of the kernel that writes,
- * per workgroup g, its entry and exit time (the GPU's 100 MHz real-time
- * counter) to buf[s + 2 g] and buf[s + 2 g + 1], s being the launch's first
- * slot; launches beyond `slots` run unstamped. A launch captured in a HIP
+ * per workgroup g, its entry and exit time on the GPU's 100 MHz real-time
+ * counter to buf[s + 4 g] and buf[s + 4 g + 1], and the same two moments on
+ * the shader-clock counter to buf[s + 4 g + 2] and buf[s + 4 g + 3] (cycles
+ * over real time: the clock the workgroup ran at), s being the launch's
+ * first slot; launches beyond `slots` run unstamped. A launch captured in a HIP
  * graph keeps its slots, so every replay rewrites them. buf is a device
  * array of `slots` uint64 (NULL and 0: stamping off). Not thread safe with
  * launches from other threads. tiq_stamp_end turns stamping off and copies

@@ -5,7 +5,9 @@ weights, bf16 in and out) and the staged prefill GEMM (int8, bf16 out) run a
 copy that also writes each workgroup's entry and exit time. The copy must
 compute exactly what the product kernel computes, hand out slots launch by
 launch (first slot, workgroup count) in launch order, and leave entry <= exit
-for every workgroup; with stamping off the product kernel runs again.
+on both counters for every workgroup (four slots a workgroup: real-time entry
+and exit, shader-clock entry and exit); with stamping off the product kernel
+runs again.
 """
 
 from __future__ import annotations
@@ -40,7 +42,7 @@ def _linear(L, x, q, s, N, y, ws=None):
     _lib.check(rc, "linear")
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 768, 2304), (1, 3072, 768), (4, 1600, 6400), (4096, 1600, 1600)])
+@pytest.mark.parametrize("M,K,N", [(1, 768, 2304), (1, 3072, 768), (3, 1600, 6400), (4096, 1600, 1600)])
 def test_stamped_copy_equals_product_kernel(dev, M, K, N):
     L = _lib.lib()
     gen = torch.Generator(device=dev).manual_seed(M + K + N)
@@ -66,12 +68,16 @@ def test_stamped_copy_equals_product_kernel(dev, M, K, N):
     assert torch.equal(y1, y_ref) and torch.equal(y2, y_ref)
     assert len(launches) == 2, launches
     (f0, g0), (f1, g1) = launches
-    assert f0 == 0 and g0 > 0 and f1 == 2 * g0 and g1 == g0
-    t = buf[: 2 * (g0 + g1)].view(-1, 2).cpu()
+    assert f0 == 0 and g0 > 0 and f1 == 4 * g0 and g1 == g0
+    t = buf[: 4 * (g0 + g1)].view(-1, 4).cpu()
     assert bool((t[:, 0] > 0).all()) and bool((t[:, 1] >= t[:, 0]).all())
+    assert bool((t[:, 3] >= t[:, 2]).all())
     span = int(t[:, 1].max() - t[:, 0].min())  # 10 ns ticks: both launches within 10 ms
     assert 0 < span < 1_000_000
-    assert int(buf[2 * (g0 + g1):].abs().sum()) == 0  # nothing past the handed-out slots
+    # shader cycles over real time: a clock between 0.3 and 3 GHz
+    ghz = float((t[:, 3] - t[:, 2]).sum()) / float((t[:, 1] - t[:, 0]).sum() * 10)
+    assert 0.3 < ghz < 3.0, ghz
+    assert int(buf[4 * (g0 + g1):].abs().sum()) == 0  # nothing past the handed-out slots
     # stamping off: no slots handed out, the product kernel again
     y3 = torch.empty_like(y_ref)
     _linear(L, x, q, s, N, y3, ws)
@@ -89,7 +95,7 @@ def test_stamp_buffer_full_runs_unstamped(dev):
     s = s.reshape(-1).contiguous()
     x = torch.randn(M, K, device=dev).to(torch.bfloat16)
     y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-    buf = torch.zeros(2 * N - 2, dtype=torch.int64, device=dev)  # one workgroup short
+    buf = torch.zeros(4 * N - 4, dtype=torch.int64, device=dev)  # one workgroup short
     assert L.tiq_stamp_begin(buf.data_ptr(), buf.numel()) == 0
     _linear(L, x, q, s, N, y)
     assert _end(L) == []
