@@ -296,6 +296,42 @@ def hbm_stream_section(dev, reps=10):
     return {"copy": {"GB/s": 8 * n / (statistics.median(ts) * 1e-3) / 1e9, "bytes": 8 * n}}
 
 
+def decode_linears_section(dev, layers=6, rounds=3):
+    """The batched decode step's four Linears at GPT-2-XL widths, M = 32,
+    called eagerly (no graph) exactly as the fused decoder's step calls them
+    (tiq_decode_linear from the previous op's operand planes), on a
+    ``layers``-layer XL-width model, ``rounds`` passes over its layers: a
+    short program for counter runs of those kernels (``--only decode_lin``);
+    the timed figures are decode_xl_section's."""
+    import torch
+
+    import gpt2_harness_amd as g
+    from gpt2_harness_amd import _lib
+
+    torch.manual_seed(0)
+    cfg = g.gpt2_config("gpt2-xl", n_layer=layers)
+    model = g.GPT(cfg).eval().to(dev)
+    qm, _ = g.quantize_model(model, 8)
+    del model
+    B, T0 = 32, 128
+    prompt = torch.randint(0, cfg.vocab_size, (B, T0)).to(dev)
+    dec = g.FusedDecoder(qm, B, T0 + 8)
+    dec.start(prompt)
+    W8, gelu = _lib.WF_INT8, _lib.ACT_GELU_TANH
+    blocks = list(qm.h)
+    for _ in range(rounds):
+        for i, b in enumerate(blocks):
+            nb = blocks[i + 1].ln_1 if i + 1 < len(blocks) else qm.ln_f
+            dec._dl(b.attn.c_attn, W8, y=dec.qkv, planes_in=dec.p_ln1)
+            dec._dl(b.attn.c_proj, W8, y=dec.x, planes_in=dec.p_att, res=dec.x, next_ln=b.ln_2,
+                    planes_out=dec.p_ln2)
+            dec._dl(b.mlp.c_fc, W8, planes_in=dec.p_ln2, act=gelu, planes_out=dec.p_hid)
+            dec._dl(b.mlp.c_proj, W8, y=dec.x, planes_in=dec.p_hid, res=dec.x, next_ln=nb,
+                    planes_out=dec.p_ln1)
+    torch.cuda.synchronize()
+    return {"layers": layers, "rounds": rounds, "calls": 4 * layers * rounds, "batch": B}
+
+
 def launch_floor_section(dev, launches=240, reps=5):
     """What one launch costs inside a HIP graph, the floor a decode GEMV sits
     on: back-to-back graph replays of `launches` launches of (a) a one-element
@@ -1036,7 +1072,7 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only (no detail sections, no CPU baseline)")
     ap.add_argument("--full-detail", default=None, metavar="PATH",
                     help="also write the uncompacted result line (every field of every section) to PATH")
-    ap.add_argument("--only", choices=["headline", "gemv", "gemv_xl", "gemm", "gemm4096", "gemm_g128", "quantize", "decode", "decode_xl", "eval", "schemes", "copy", "floor"],
+    ap.add_argument("--only", choices=["headline", "gemv", "gemv_xl", "gemm", "gemm4096", "gemm_g128", "quantize", "decode", "decode_xl", "decode_lin", "eval", "schemes", "copy", "floor"],
                     default=None,
                     help="run one section alone (for profiling); 'copy' runs a plain 256 MiB device copy "
                          "used to calibrate the HBM byte counters")
@@ -1092,6 +1128,9 @@ def main() -> int:
         return 0
     if args.only == "decode_xl":
         print(json.dumps(decode_xl_section(dev)))
+        return 0
+    if args.only == "decode_lin":  # the batched decode Linears alone, for counter runs
+        print(json.dumps(decode_linears_section(dev)))
         return 0
     if args.only == "eval":
         print(json.dumps(eval_section(dev)))
