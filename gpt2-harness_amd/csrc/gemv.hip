@@ -6,8 +6,10 @@
 // per call against 2-4*M*K bytes of activations; at decode sizes (0.6-10 MB)
 // one launch is about one trip to HBM plus the launch itself. Two kernels:
 //
-// gemv_direct_kernel (up to 4 rows, no LayerNorm; the default): one
-// wavefront per weight row, every load of the workgroup issued before any is
+// gemv_direct_kernel (up to 4 rows; the default, with the LayerNorm of fp32
+// rows fused for up to 8192 weight rows, and for a tied fp32 head at one
+// row): one wavefront per weight row (two or four at one row), every load of
+// the workgroup issued before any is
 // used -- the row's 16-byte chunks (nontemporal), the activations they
 // multiply (straight into registers) and the epilogue operands -- then one
 // FMA pass, a wavefront reduction and the store. Rows are dealt to the eight
@@ -746,10 +748,10 @@ int run_gemv(const LinearArgs& a) {
 template <int MT, int UM, int FMT, typename TX, bool LNF>
 constexpr bool direct_fits() {
     constexpr int XB = Fmt<FMT>::KC * (int)sizeof(TX);
-    // with LayerNorm: fp32 activations and int8 / int4 codes only, plus the
-    // LayerNorm weight and bias of the lane's columns (2 x KC VGPRs a chunk)
+    // with LayerNorm: fp32 activations, plus the LayerNorm weight and bias of
+    // the lane's columns (2 x KC VGPRs a chunk)
     if constexpr (LNF) {
-        if (sizeof(TX) != 4 || FMT == kF32) return false;
+        if (sizeof(TX) != 4) return false;
         return UM * (MT * (XB / 16) * 4 + 2 * Fmt<FMT>::KC) <= 160;
     }
     return UM * MT * (XB >= 16 ? XB / 16 : 1) * 4 <= 128;
@@ -780,9 +782,20 @@ bool run_direct(const LinearArgs& a, int& rc) {
     return false;
 }
 
+// Weight rows from which an fp32 matrix with a LayerNorm counts as a tied
+// head (four rows a wavefront).
+constexpr int64_t kDirectHeadRows = 16384;
+
 template <int UM, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct_mt(const LinearArgs& a, int& rc) {
     if (a.M == 1) {
+        // a tied fp32 head behind its LayerNorm (tens of thousands of rows):
+        // four rows a wavefront, so each wavefront's read of the activations
+        // and the LayerNorm weight and bias (12 bytes a column) serves 16
+        // bytes a column of weights (GPT-2's 50257 x 768 head: 24-25 us,
+        // 6.1-6.4 TB/s, against 36.4 us for the LDS-staged kernel)
+        if constexpr (FMT == kF32 && LNF)
+            if (a.N >= kDirectHeadRows) return run_direct<1, UM, 4, FMT, TX, TY, LNF>(a, rc);
         // two weight rows a wavefront share its activation loads: a gain on
         // wide matrices with short rows (N >= 2048, at most two chunks a
         // lane), a loss on narrow ones, where it halves the wavefronts
@@ -832,7 +845,11 @@ bool try_direct(const LinearArgs& a, int& rc) {
             // bias (12 bytes a column) from L2: worth it while a launch is
             // latency-bound, not for a head of 50257 rows, where that traffic
             // is twelve times the weights' and the LDS-staged kernel shares it
-            if (a.N > kDirectLnMaxRows || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16)) return false;
+            // (fp32 weights at M = 1, four rows a wavefront, are the exception:
+            // there the weights are 16 bytes a column of that read)
+            const bool head = FMT == kF32 && a.M == 1;
+            if ((a.N > kDirectLnMaxRows && !head) || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16))
+                return false;
             return run_direct_um<FMT, TX, TY, true>(a, rc);
         }
         return run_direct_um<FMT, TX, TY, false>(a, rc);

@@ -254,8 +254,12 @@ def test_direct_gemv_formats(dev, c_oracle, fmt, x_dtype, M, K, N):
     assert ok, (err, bound)
 
 
-def test_fused_f32_head_with_ln(dev):
-    K, N, M = 768, 50257, 2
+@pytest.mark.parametrize("M", [1, 2])
+def test_fused_f32_head_with_ln(dev, M):
+    """The tied fp32 head behind its LayerNorm: at one row the direct kernel
+    (four weight rows a wavefront, 50257 = 4 x 12564 + 1 leaves a partial last
+    wavefront), at two the LDS-staged one."""
+    K, N = 768, 50257
     gen = torch.Generator().manual_seed(4)
     w = torch.randn(N, K, generator=gen) * 0.02
     x = torch.randn(M, K, generator=gen)
