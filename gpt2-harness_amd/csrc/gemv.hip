@@ -782,20 +782,22 @@ bool run_direct(const LinearArgs& a, int& rc) {
     return false;
 }
 
-// Weight rows from which an fp32 matrix with a LayerNorm counts as a tied
-// head (four rows a wavefront).
-constexpr int64_t kDirectHeadRows = 16384;
+// Weight rows up to which a wavefront of the direct kernel reads the whole
+// activation row and its LayerNorm weight and bias for one or two weight
+// rows; above it only a head at one row (four or eight rows a wavefront).
+constexpr int64_t kDirectLnMaxRows = 8192;
 
 template <int UM, int FMT, typename TX, typename TY, bool LNF>
 bool run_direct_mt(const LinearArgs& a, int& rc) {
     if (a.M == 1) {
-        // a tied fp32 head behind its LayerNorm (tens of thousands of rows):
-        // four rows a wavefront, so each wavefront's read of the activations
-        // and the LayerNorm weight and bias (12 bytes a column) serves 16
-        // bytes a column of weights (GPT-2's 50257 x 768 head: 24-25 us,
-        // 6.1-6.4 TB/s, against 36.4 us for the LDS-staged kernel)
-        if constexpr (FMT == kF32 && LNF)
-            if (a.N >= kDirectHeadRows) return run_direct<1, UM, 4, FMT, TX, TY, LNF>(a, rc);
+        // a tied head behind its LayerNorm (tens of thousands of rows): four
+        // fp32 rows or eight rows of codes a wavefront, so each wavefront's
+        // read of the activations and the LayerNorm weight and bias (12 bytes
+        // a column) serves 16 or 8 bytes a column of weights (GPT-2's 50257 x
+        // 768 head: fp32 24-25 us, 6.1-6.4 TB/s, int8 12.1 us, against 36.4
+        // and 26.7 us for the LDS-staged kernel)
+        if constexpr (LNF)
+            if (a.N > kDirectLnMaxRows) return run_direct<1, UM, FMT == kF32 ? 4 : 8, FMT, TX, TY, LNF>(a, rc);
         // two weight rows a wavefront share its activation loads: a gain on
         // wide matrices with short rows (N >= 2048, at most two chunks a
         // lane), a loss on narrow ones, where it halves the wavefronts
@@ -825,7 +827,6 @@ bool run_direct_um(const LinearArgs& a, int& rc) {
     }
 }
 
-constexpr int64_t kDirectLnMaxRows = 8192;
 
 // The direct kernel, when it takes the arguments (no LayerNorm, int8 / int4 /
 // fp32 weights, a row of at most 8 chunks per lane, 16-byte activation rows).
@@ -845,10 +846,9 @@ bool try_direct(const LinearArgs& a, int& rc) {
             // bias (12 bytes a column) from L2: worth it while a launch is
             // latency-bound, not for a head of 50257 rows, where that traffic
             // is twelve times the weights' and the LDS-staged kernel shares it
-            // (fp32 weights at M = 1, four rows a wavefront, are the exception:
-            // there the weights are 16 bytes a column of that read)
-            const bool head = FMT == kF32 && a.M == 1;
-            if ((a.N > kDirectLnMaxRows && !head) || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16))
+            // (a head at M = 1 is the exception: four or eight weight rows a
+            // wavefront share that read)
+            if ((a.N > kDirectLnMaxRows && a.M != 1) || !aligned(a.fuse.ln_w, 16) || !aligned(a.fuse.ln_b, 16))
                 return false;
             return run_direct_um<FMT, TX, TY, true>(a, rc);
         }

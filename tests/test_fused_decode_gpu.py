@@ -254,6 +254,36 @@ def test_direct_gemv_formats(dev, c_oracle, fmt, x_dtype, M, K, N):
     assert ok, (err, bound)
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("M,N", [(1, 50257), (1, 8203), (2, 50257)])
+def test_fused_code_head_with_ln(dev, c_oracle, fmt, M, N):
+    """A head of int8 / int4 codes behind its LayerNorm (non-trivial weight
+    and bias): at one row over 8192 rows the direct kernel with eight weight
+    rows a wavefront (50257 and 8203 leave a partial last wavefront), at two
+    the LDS-staged one."""
+    K = 768
+    gen = torch.Generator().manual_seed(N + M)
+    w = torch.randn(N, K, generator=gen) * 0.02
+    x = torch.randn(M, K, generator=gen)
+    lw, lb = 1 + 0.1 * torch.randn(K, generator=gen), 0.1 * torch.randn(K, generator=gen)
+    bits = 8 if fmt == "int8" else 4
+    q, s = c_oracle.quantize_per_channel(w.numpy(), bits)
+    wd = torch.from_numpy(q if bits == 8 else c_oracle.pack_int4(q)).to(dev)
+    wf = _lib.WF_INT8 if bits == 8 else _lib.WF_INT4
+    sd = torch.from_numpy(s.reshape(-1)).to(dev)
+    y = torch.empty(M, N, device=dev)
+    # device copies stay referenced until the kernel has run
+    xd, lwd, lbd = x.to(dev), lw.to(dev), lb.to(dev)
+    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, wd.data_ptr(), wf, sd.data_ptr(), None, 0,
+                                     None, N, y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5, 0, None, 0,
+                                     _st())
+    _lib.check(rc, "code head")
+    torch.cuda.synchronize()
+    ref = OL.linear_ref(F.layer_norm(x, (K,), lw, lb, 1e-5), OL.dequantize(q, s))
+    ok, err, bound = OL.within_tolerance(y, ref)
+    assert ok, (err, bound)
+
+
 @pytest.mark.parametrize("M", [1, 2])
 def test_fused_f32_head_with_ln(dev, M):
     """The tied fp32 head behind its LayerNorm: at one row the direct kernel
