@@ -56,6 +56,14 @@ namespace {
 // vector-ALU GEMV (below it the GEMM wastes most of each tile).
 constexpr int64_t kGemmMinRows = 128;
 
+// fp32 rows against reference-layout int4 codes take the three-plane
+// matrix-core path (split over K where the tiles are few) from 32 rows, or
+// from 16 on matrices of 2048 rows or more: below 128 rows there is no
+// batched kernel for int4, and the LDS-staged GEMV, four activation rows a
+// tile, grows with M (GPT-2 small shapes at M = 64: 18-57 us against 12-19 us
+// through the planes; int8 has the batched kernel up to 64 rows).
+bool w4_planes_rows(int64_t M, int64_t N) { return M >= 32 || (M >= 16 && N >= 2048); }
+
 LinearArgs make_args(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w, int64_t ldw,
                      const float* scale, const uint16_t* scale16, int group, const float* bias, int64_t N, void* y,
                      int y_dtype, int64_t ldy, void* stream, WFormat fmt) {
@@ -122,7 +130,9 @@ size_t split_workspace(int64_t M, int64_t K) { return (size_t)(M * 3 * K * 2 + 2
 // problem (the staged kernel, else the LDS-dequant one); TIQ_EUNSUPPORTED
 // otherwise (the caller falls back). gelu_in: the product takes gelu_tanh(x).
 int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes, bool gelu_in = false) {
-    if (a.x_dtype != TIQ_F32 || a.fmt == kF32 || a.M < kGemmMinRows || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
+    if (a.x_dtype != TIQ_F32 || a.fmt == kF32 || a.K % 4 != 0) return TIQ_EUNSUPPORTED;
+    const bool few = a.M < kGemmMinRows;  // below the GEMM's own row count: int4 from fewer rows
+    if (few && !(a.fmt == kW4 && w4_planes_rows(a.M, a.N))) return TIQ_EUNSUPPORTED;
     if (!aligned(a.x, 16) || a.ldx % 4 != 0 || a.M * 3 * a.K > 0x7fffffffLL) return TIQ_EUNSUPPORTED;
     LinearArgs g = a;
     g.x = ws;
@@ -132,7 +142,8 @@ int run_linear_split(const LinearArgs& a, void* ws, size_t ws_bytes, bool gelu_i
     g.kw = a.K;
     const bool staged = staged_gemm_supported(g);
     if (!staged && !gemm_supported(g)) return TIQ_EUNSUPPORTED;
-    if (!ws || ws_bytes < split_workspace(a.M, a.K) || !aligned(ws, 16)) return TIQ_EWORKSPACE;
+    if (!ws || ws_bytes < split_workspace(a.M, a.K) || !aligned(ws, 16))
+        return few ? TIQ_EUNSUPPORTED : TIQ_EWORKSPACE;  // with fewer rows the GEMV path takes it
     const int64_t n = a.M * (a.K / 4);
     hipLaunchKernelGGL(split_bf16x3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, a.stream,
                        static_cast<const float*>(a.x), a.ldx, (int)a.M, (int)a.K, static_cast<uint16_t*>(ws),
@@ -232,8 +243,8 @@ extern "C" int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K
 }
 
 extern "C" size_t tiq_gemm_w8_workspace(int x_dtype, int64_t M, int64_t K, int64_t N) {
-    if ((x_dtype != TIQ_F32 && x_dtype != TIQ_BF16) || M < kGemmMinRows || K <= 0 || K % 64 != 0 || N <= 0)
-        return 0;
+    if ((x_dtype != TIQ_F32 && x_dtype != TIQ_BF16) || K <= 0 || K % 64 != 0 || N <= 0) return 0;
+    if (M < kGemmMinRows && !(x_dtype == TIQ_F32 && w4_planes_rows(M, N))) return 0;
     if (x_dtype == TIQ_F32) return split_workspace(M, K) + staged_split_workspace(M, N, 3 * K);
     return staged_split_workspace(M, N, K);
 }

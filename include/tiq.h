@@ -173,7 +173,9 @@ int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
  * bf16 activations tiq_linear_w4_ws / tiq_linear_w4g_ws) run a product with
  * few output tiles split over K (fp32 partial slices, summed in a fixed order
  * by a second kernel), plus, for fp32 activations, their bf16 planes. 0 when
- * none is needed. */
+ * none is needed. Nonzero from M >= 128, and for fp32 activations also from
+ * the fewer rows at which tiq_linear_w4_ws takes the planes (M >= 32, or
+ * M >= 16 with N >= 2048; the int8 entry points do not use it there). */
 size_t tiq_gemm_w8_workspace(int x_dtype, int64_t M, int64_t K, int64_t N);
 /* tiq_gemm_w8 with a caller workspace (see tiq_gemm_w8_workspace): the
  * prefill product of the reference's Linears (model.py:254,319,352,355 at
@@ -229,9 +231,14 @@ int tiq_linear_w4g(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx
  * 319,352,355 at M = B*T). With bf16 x, M >= 128 and a workspace of
  * tiq_gemm_w8_workspace(TIQ_BF16, M, K, N) bytes both split a product with few
  * output tiles over K (group-wise: whole groups a split), the fp32 slices
- * summed in a fixed order. Where the GEMM does not take the shape (K % 64,
- * group % 64), and for bf16 x or M < 128 without a workspace, they compute
- * what tiq_linear_w4 / tiq_linear_w4g compute. With fp32 x, M >= 128 and a
+ * summed in a fixed order. Reference-layout int4 (tiq_linear_w4_ws) with fp32
+ * x takes the planes from fewer rows too -- M >= 32, or M >= 16 with
+ * N >= 2048 -- given a workspace of tiq_gemm_w8_workspace(TIQ_F32, M, K, N)
+ * bytes (planes, then the fp32 slices of a product split over K); with a
+ * smaller one such a call computes what tiq_linear_w4 computes. Where the
+ * GEMM does not take the shape (K % 64, group % 64), and for bf16 x or
+ * M < 128 without a workspace, they compute what tiq_linear_w4 /
+ * tiq_linear_w4g compute. With fp32 x, M >= 128 and a
  * shape the GEMM takes, the planes need the workspace: TIQ_EWORKSPACE when it
  * is NULL, smaller than tiq_linear_w8_workspace(x_dtype, M, K) or not 16-byte
  * aligned (as tiq_linear_w8_ws). */

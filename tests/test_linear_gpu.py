@@ -360,6 +360,45 @@ def test_linear_w4_reference_layout(dev, c_oracle, KN, M):
         assert torch.equal(ybf.cpu(), y.cpu().to(torch.bfloat16)), "bf16 output is not RNE of the fp32 output"
 
 
+# fp32 rows against reference-layout int4 codes at 16..127 rows (a short
+# prompt's prefill) with the workspace of tiq_gemm_w8_workspace: the three
+# exact bf16 planes on the matrix cores, split over K (M >= 32, or >= 16 on
+# N >= 2048); without a workspace the same call takes the GEMV path. Both
+# within the oracle's bound, the planes also within 8x torch fp32's own error
+# against float64, and the two paths agree to that tolerance.
+@pytest.mark.parametrize("K,N,M", [(768, 2304, 16), (768, 768, 16), (768, 768, 33), (3072, 768, 64),
+                                   (768, 3072, 127), (1600, 6400, 40)])
+def test_linear_w4_fp32_few_rows_planes(dev, c_oracle, K, N, M):
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, M * 3 + K)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 4)
+    packed = torch.from_numpy(c_oracle.pack_int4(q)).to(dev)
+    sd, bd, xd = torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
+    n_ws = int(L.tiq_gemm_w8_workspace(_lib.F32, M, K, N))
+    planes = M >= 32 or N >= 2048
+    assert (n_ws > 0) == planes
+    ws = torch.empty(max(n_ws, 16), dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    ys = []
+    for wsp, nb in ((ws.data_ptr(), n_ws), (None, 0)):
+        y = torch.full((M, N), float("nan"), device=dev)
+        rc = L.tiq_linear_w4_ws(xd.data_ptr(), _lib.F32, M, K, K, packed.data_ptr(), sd.data_ptr(), bd.data_ptr(), N,
+                                y.data_ptr(), _lib.F32, N, wsp, nb, st)
+        _lib.check(rc, "tiq_linear_w4_ws")
+        ys.append(y)
+    torch.cuda.synchronize()
+    w_hat = OL.dequantize(q, s)
+    ref32 = OL.linear_ref(x, w_hat, b)
+    ref64 = x.double() @ w_hat.double().T + b.double()
+    err32 = float((ref32.double() - ref64).abs().max())
+    for y in ys:
+        ok, err, bound = OL.within_tolerance(y, ref32, TOL)
+        assert ok, (M, err, bound)
+    if planes:
+        err = float((ys[0].cpu().double() - ref64).abs().max())
+        assert err <= 8 * max(err32, 2.0 ** -24 * float(ref64.abs().max())), (err, err32)
+
+
 # int4 in the reference's nibble layout with bf16 rows and the GEMM workspace:
 # products with few 128 x 128 tiles split over K (6400x1600 at M = 256: 26
 # tiles, eight splits), the fp32 slices summed in order, scaled and biased
