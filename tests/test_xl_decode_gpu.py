@@ -111,6 +111,15 @@ def test_gpt2_xl_batch32_greedy_matches_oracle(dev):
     assert got.tolist() == want.tolist(), f"min margin {min(margins):.3g}"
 
 
+def test_gpt2_xl_batch32_decode_across_slot_256(dev):
+    """All 48 layers at batch 32, 128-token prompts and 136 captured decode
+    steps (positions 128..263): every generated token through the slot-256
+    boundary of the attention's first requests, against the oracle's."""
+    got, want, margins = _decode_vs_oracle(OM.GPT2_XL, dev, batch=32, prompt_len=128, new_tokens=136, seed=2)
+    assert got.shape == (32, 264)
+    assert got.tolist() == want.tolist(), f"min margin {min(margins):.3g}"
+
+
 def test_xl_width_batch32_decode_across_slot_256(dev):
     """Two XL-width layers, batch 32, a 250-token prompt and 12 new tokens: the
     cache of a layer (32 x 25 x 262 slots, 107 MB) takes the attention kernel
