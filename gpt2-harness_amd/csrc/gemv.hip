@@ -10,8 +10,9 @@
 // rows fused for up to 8192 weight rows, and for a tied fp32 head at one
 // row): one wavefront per weight row (two or four at one row), every load of
 // the workgroup issued before any is
-// used -- the row's 16-byte chunks (nontemporal), the activations they
-// multiply (straight into registers) and the epilogue operands -- then one
+// used -- the row's 16-byte chunks (8 bytes of nibbles for int4: 16 columns
+// a lane whatever the format; nontemporal), the activations they multiply
+// (straight into registers) and the epilogue operands -- then one
 // FMA pass, a wavefront reduction and the store. Rows are dealt to the eight
 // XCDs in contiguous blocks.
 //
@@ -57,6 +58,15 @@ struct Fmt {
     // columns per 16-byte weight chunk
     static constexpr int KC = (FMT == kW8) ? 16 : (FMT == kF32) ? 4 : 32;
 };
+
+// The direct kernel's chunk: 16 bytes (16 int8 / 4 fp32 columns), but 8 bytes
+// (16 columns) of nibbles, so that an int4 lane carries the activations (and
+// LayerNorm operands) of 16 columns, as an int8 lane does, rather than 32:
+// twice the lanes each with half the loads and arithmetic on a row.
+template <int FMT>
+constexpr int direct_kc() { return FMT == kW4 ? 16 : Fmt<FMT>::KC; }
+template <int FMT>
+constexpr int direct_chunk_bytes() { return FMT == kW4 ? 8 : 16; }
 
 template <typename TX>
 __device__ __forceinline__ float4 load_x4(const TX* p);
@@ -120,6 +130,32 @@ __device__ __forceinline__ float dot_w4(const uint4& w, const float4* xv) {
     return s;
 }
 
+// sum over the 16 columns of an 8-byte nibble chunk (w.x, w.y). A nibble n
+// moved into the high half of a byte with that byte's top bit flipped is the
+// signed byte 16 (n - 8), which becomes a float in one instruction; every
+// product and partial sum is then exactly 16 times the one of n - 8 (a power
+// of two), and the sum is scaled back once: the same result as converting
+// n - 8 directly, in the same column order.
+__device__ __forceinline__ float dot_w4h(const uint4& w, const float4* xv) {
+    float s = 0.f;
+    const uint32_t d[2] = {w.x, w.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float4 a = xv[2 * j], b = xv[2 * j + 1];
+        const uint32_t e = ((d[j] << 4) & 0xf0f0f0f0u) ^ 0x80808080u;  // even columns (low nibbles)
+        const uint32_t o = (d[j] & 0xf0f0f0f0u) ^ 0x80808080u;         // odd columns
+        s = fmaf(sbyte_f32<0>(e), a.x, s);
+        s = fmaf(sbyte_f32<0>(o), a.y, s);
+        s = fmaf(sbyte_f32<1>(e), a.z, s);
+        s = fmaf(sbyte_f32<1>(o), a.w, s);
+        s = fmaf(sbyte_f32<2>(e), b.x, s);
+        s = fmaf(sbyte_f32<2>(o), b.y, s);
+        s = fmaf(sbyte_f32<3>(e), b.z, s);
+        s = fmaf(sbyte_f32<3>(o), b.w, s);
+    }
+    return s * 0.0625f;
+}
+
 // sum over the 4 columns of an fp32 chunk
 __device__ __forceinline__ float dot_f32(const uint4& w, const float4* xv) {
     const float4 xx = xv[0];
@@ -137,6 +173,7 @@ __device__ __forceinline__ float dot_chunk(const uint4& w, const float4* xv) {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Bijective map of a workgroup index so that XCD b % 8 (where the hardware
 // places workgroup b) owns a contiguous range of the G workgroups.
@@ -428,7 +465,8 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
                                                          uint64_t* stamp) {
     Stamp<STAMP> clock;
     clock.start();
-    constexpr int KC = Fmt<FMT>::KC;
+    constexpr int KC = direct_kc<FMT>();
+    constexpr int CB = direct_chunk_bytes<FMT>();
     constexpr int P = KC / 4;                          // float4 of activations per chunk
     constexpr int XB = KC * (int)sizeof(TX);           // activation bytes per chunk and row
     constexpr int XQ = XB >= 16 ? XB / 16 : 1;         // 16-byte registers holding them
@@ -448,9 +486,15 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
         for (int u = 0; u < UM; ++u) {
             const int c = min(lane + 64 * u, NC - 1);
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                wv[u][r] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(w + (int64_t)min(n0 + r, N - 1) * ldw + 16 * (int64_t)c));
+            for (int r = 0; r < R; ++r) {
+                const uint8_t* src = w + (int64_t)min(n0 + r, N - 1) * ldw + CB * (int64_t)c;
+                if constexpr (CB == 8) {
+                    const u32x2 h = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src));
+                    wv[u][r] = u32x4{h.x, h.y, 0u, 0u};
+                } else {
+                    wv[u][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+                }
+            }
         }
     };
     // With a LayerNorm the activations are requested first: a wavefront's
@@ -575,7 +619,10 @@ __global__ __launch_bounds__(64) void gemv_direct_kernel(const uint8_t* __restri
             }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float part = dot_chunk<FMT>(make_uint4(wv[u][r].x, wv[u][r].y, wv[u][r].z, wv[u][r].w), xf);
+                const uint4 wc = make_uint4(wv[u][r].x, wv[u][r].y, wv[u][r].z, wv[u][r].w);
+                float part;
+                if constexpr (FMT == kW4) part = dot_w4h(wc, xf);
+                else part = dot_chunk<FMT>(wc, xf);
                 acc[r][m] += own ? part : 0.f;
             }
         }
@@ -747,12 +794,12 @@ int run_gemv(const LinearArgs& a) {
 // VGPRs, kept within 128 so that weights, activations and sums all fit.
 template <int MT, int UM, int FMT, typename TX, bool LNF>
 constexpr bool direct_fits() {
-    constexpr int XB = Fmt<FMT>::KC * (int)sizeof(TX);
+    constexpr int XB = direct_kc<FMT>() * (int)sizeof(TX);
     // with LayerNorm: fp32 activations, plus the LayerNorm weight and bias of
     // the lane's columns (2 x KC VGPRs a chunk)
     if constexpr (LNF) {
         if (sizeof(TX) != 4) return false;
-        return UM * (MT * (XB / 16) * 4 + 2 * Fmt<FMT>::KC) <= 160;
+        return UM * (MT * (XB / 16) * 4 + 2 * direct_kc<FMT>()) <= 160;
     }
     return UM * MT * (XB >= 16 ? XB / 16 : 1) * 4 <= 128;
 }
@@ -813,7 +860,7 @@ template <int FMT, typename TX, typename TY, bool LNF>
 bool run_direct_um(const LinearArgs& a, int& rc) {
     // exactly the chunks a lane needs: a spare round of (clamped, repeated)
     // loads costs address work and registers, 0.1-0.2 us a launch
-    switch ((a.K / Fmt<FMT>::KC + 63) / 64) {
+    switch ((a.K / direct_kc<FMT>() + 63) / 64) {
         case 0:
         case 1: return run_direct_mt<1, FMT, TX, TY, LNF>(a, rc);
         case 2: return run_direct_mt<2, FMT, TX, TY, LNF>(a, rc);
@@ -835,7 +882,7 @@ bool try_direct(const LinearArgs& a, int& rc) {
     if constexpr (FMT == kW4G) {
         return false;
     } else {
-        constexpr int KC = Fmt<FMT>::KC;
+        constexpr int KC = direct_kc<FMT>();
         constexpr size_t XB = KC * sizeof(TX);
         const size_t xa = XB >= 16 ? 16 : XB;
         if (!aligned(a.x, xa) || ((size_t)a.ldx * sizeof(TX)) % xa != 0) return false;

@@ -38,21 +38,27 @@ def _gelu(x):
     return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x.pow(3))))
 
 
+# LayerNorm + Linear + GELU at up to 8 rows, int8 and reference-layout int4
+# (the direct GEMV's one- and two-row wavefronts with the LayerNorm in
+# registers at 1-4 rows; 16 columns a lane in both formats).
+@pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("M", [1, 3, 4, 8])
 @pytest.mark.parametrize("K,N", [(768, 2304), (1600, 6400), (3072, 768)])
-def test_fused_ln_gelu_linear(dev, c_oracle, M, K, N):
+def test_fused_ln_gelu_linear(dev, c_oracle, M, K, N, bits):
     gen = torch.Generator().manual_seed(M * 7 + K)
     w = torch.randn(N, K, generator=gen) * 0.02
     x = torch.randn(M, K, generator=gen) * 2 + 0.5
     lw = 1 + 0.1 * torch.randn(K, generator=gen)
     lb = 0.1 * torch.randn(K, generator=gen)
     b = 0.1 * torch.randn(N, generator=gen)
-    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), bits)
+    codes = q if bits == 8 else c_oracle.pack_int4(q)
     y = torch.empty(M, N, device=dev)
     # device copies stay referenced until the kernel has run
-    xd, qd, sd, bd = x.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
+    xd, qd, sd, bd = x.to(dev), torch.from_numpy(codes).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev)
     lwd, lbd = lw.to(dev), lb.to(dev)
-    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, qd.data_ptr(), _lib.WF_INT8, sd.data_ptr(), None, 0,
+    wf = _lib.WF_INT8 if bits == 8 else _lib.WF_INT4
+    rc = _lib.lib().tiq_linear_fused(xd.data_ptr(), 0, M, K, K, qd.data_ptr(), wf, sd.data_ptr(), None, 0,
                                      bd.data_ptr(), N, y.data_ptr(), 0, N, lwd.data_ptr(), lbd.data_ptr(), 1e-5,
                                      _lib.ACT_GELU_TANH, None, 0, _st())
     _lib.check(rc, "fused")
