@@ -3,7 +3,9 @@
 The reference's ``generate`` (``sampling.py:100-181``) runs one Python-level
 forward pass per token over a ``torch.cat``-grown cache (``model.py:153-172``):
 every op is a separate launch issued from the host. Here the prompt is
-processed by the model's ordinary forward (prefill), and every later token by
+processed by the model's ordinary forward (prefill; short prompts in the fused
+decoder by the same ops over their rows with the epilogues fused into the
+Linears), and every later token by
 one replay of a captured HIP graph holding the whole decode step. The KV cache
 is preallocated, ``(B, kv_heads, T_max, head_dim)`` per layer, and the fill
 level is a device scalar, so the captured step is the same for every token.
@@ -192,6 +194,13 @@ def fused_supported(model) -> str | None:
     return None
 
 
+def _layer_norm(ln, x: torch.Tensor) -> torch.Tensor:
+    """The model's own LayerNorm module applied to rows (torch's kernel: at
+    tens of rows it costs less as a launch of its own than inside every
+    workgroup of the product that follows)."""
+    return ln(x)
+
+
 class FusedDecoder(_DecoderBase):
     """Decode step built from the library's fused decode kernels."""
 
@@ -230,6 +239,7 @@ class FusedDecoder(_DecoderBase):
         lins = [l for b in model.h for l in (b.attn.c_attn, b.attn.c_proj, b.mlp.c_fc, b.mlp.c_proj)]
         head_ok = self.head_q is None or self.head_q.fmt == FMT_W8
         self.chain = 5 <= B <= 64 and head_ok and all(l.fmt == FMT_W8 for l in lins)
+        self.rows_prefill = all(l.fmt == FMT_W8 for l in lins)
         if self.chain:
             L = self.L
             head_wf = _lib.WF_F32 if self.head_q is None else _lib.WF_INT8
@@ -291,6 +301,91 @@ class FusedDecoder(_DecoderBase):
             float(ln.eps) if ln is not None else 1e-5, act, None if res is None else res.data_ptr(),
             0 if res is None else res.stride(0), self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
         _lib.check(rc, "fused decode linear")
+
+    # Prompts of at most this many rows (batch x length) are prefilled by the
+    # block chain of fused Linears below rather than the model's forward.
+    ROW_PREFILL_MAX = 64
+
+    def _start(self, idx: torch.Tensor) -> None:
+        """Prefill and the first generated token. A prompt of at most
+        ``ROW_PREFILL_MAX`` rows (int8 blocks) runs the block's ops over all
+        of its rows with the epilogues fused into the Linears: LayerNorm,
+        ``c_attn``, the keys and values into the cache, causal attention over
+        the prompt (``tiq_prefill_attention``, reading q, k, v in place from
+        the projection's rows), ``c_proj`` + residual, LayerNorm, ``c_fc`` +
+        GELU, ``c_proj`` + residual (9 launches a block against the forward's
+        12: no separate residual adds or GELU pass); then LayerNorm + head on
+        each sequence's last row and the argmax kernels. GPT-2 small, one
+        64-token prompt: 0.94 against 1.04 ms, the same tokens. Longer
+        prompts take the model's forward (``model.py:528-599``), and so do
+        blocks with int4 codes, whose rows take the matrix cores through the
+        forward's workspace."""
+        B, T0 = idx.shape
+        if B * T0 > self.ROW_PREFILL_MAX or not self.rows_prefill:
+            super()._start(idx)
+            return
+        if B != self.B or T0 > self.T:
+            raise ValueError(f"prompt {tuple(idx.shape)} does not fit batch={self.B}, max_len={self.T}")
+        m, cfg, L = self.model, self.cfg, self.L
+        C, R, H, hd = cfg.n_embd, B * T0, self.H, self.hd
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        bufs = getattr(self, "_row_bufs", {}).get(T0)
+        if bufs is None:  # allocated by the uncaptured warm-up call of start()
+            qkv_w = m.h[0].attn.c_attn.out_features
+            bufs = (torch.empty(R, C, device=self.dev), torch.empty(R, qkv_w, device=self.dev),
+                    torch.empty(R, C, device=self.dev), torch.empty(R, m.h[0].mlp.c_fc.out_features, device=self.dev))
+            self._row_bufs = {**getattr(self, "_row_bufs", {}), T0: bufs}
+        x, qkv, att, hid = bufs
+        # the model's embedding: wte(idx) + wpe(0..T0-1) (model.py:564-568)
+        torch.add(m.wte(idx), m.wpe.weight[:T0], out=x.view(B, T0, C))
+        for i, block in enumerate(m.h):
+            attn, mlp = block.attn, block.mlp
+            self._linear_rows(attn.c_attn, _layer_norm(block.ln_1, x), qkv)
+            kv = qkv.view(B, T0, 3, H, hd)
+            self.k[i][:, :, :T0].copy_(kv[:, :, 1].transpose(1, 2))
+            self.v[i][:, :, :T0].copy_(kv[:, :, 2].transpose(1, 2))
+            rc = L.tiq_prefill_attention(
+                qkv.data_ptr(), T0 * qkv.stride(0), hd, qkv.stride(0), qkv.data_ptr() + 4 * C, T0 * qkv.stride(0),
+                hd, qkv.stride(0), qkv.data_ptr() + 8 * C, T0 * qkv.stride(0), hd, qkv.stride(0), B, H, T0, 0, hd,
+                att.data_ptr(), T0 * C, hd, C, st)
+            _lib.check(rc, "prefill attention")
+            self._linear_rows(attn.c_proj, att, x, res=x)
+            self._linear_rows(mlp.c_fc, _layer_norm(block.ln_2, x), hid, act=_lib.ACT_GELU_TANH)
+            self._linear_rows(mlp.c_proj, hid, x, res=x)
+        # LayerNorm + head on each sequence's last row (rows T0 - 1, 2 T0 - 1, ...)
+        last = x.view(B, T0, C)[:, T0 - 1]
+        ln = m.ln_f
+        if self.head_q is not None:
+            self._linear_rows(self.head_q, last, self.logits, ln=ln)
+        else:
+            rc = L.tiq_linear_fused_ws(last.data_ptr(), _lib.F32, B, C, last.stride(0), self.head_w.data_ptr(),
+                                       _lib.WF_F32, None, None, 0, None, cfg.vocab_size, self.logits.data_ptr(),
+                                       _lib.F32, cfg.vocab_size, ln.weight.data_ptr(), ln.bias.data_ptr(),
+                                       float(ln.eps), 0, None, 0, self.lin_ws.data_ptr(), self.lin_ws_bytes, st)
+            _lib.check(rc, "lm_head")
+        self.out[:, :T0].copy_(idx)
+        # the argmax records the first generated token at slot pos + 1 = T0
+        # and in tok, and advances pos to T0
+        self.pos.fill_(T0 - 1)
+        _lib.check(L.tiq_argmax_rows(self.logits.data_ptr(), B, cfg.vocab_size, cfg.vocab_size,
+                                     self.tok_flat.data_ptr(), self.out.data_ptr(), self.T, self.pos.data_ptr(),
+                                     self.argmax_ws.data_ptr(), self.argmax_ws.numel(), st), "argmax")
+
+    def _linear_rows(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0,
+                     res=None) -> None:
+        """One tiq_linear_fused call over any number of fp32 rows (no
+        workspace: the product splits its activations itself)."""
+        M, K = x.shape
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        scale16 = lin.scale.data_ptr() if lin.fmt == FMT_W4G else None
+        scale = None if lin.fmt == FMT_W4G else lin.scale.data_ptr()
+        rc = self.L.tiq_linear_fused(
+            x.data_ptr(), _lib.F32, M, K, x.stride(0), lin.codes.data_ptr(), _WF[lin.fmt], scale, scale16,
+            lin.group_size, _lib.ptr(lin.bias), lin.out_features, y.data_ptr(), _lib.F32, y.stride(0),
+            None if ln is None else ln.weight.data_ptr(), None if ln is None else ln.bias.data_ptr(),
+            float(ln.eps) if ln is not None else 1e-5, act, None if res is None else res.data_ptr(),
+            0 if res is None else res.stride(0), st)
+        _lib.check(rc, "fused prefill linear")
 
     def _dl(self, lin, wf, y=None, x=None, planes_in=None, ln=None, act: int = 0, res=None, next_ln=None,
             planes_out=None) -> None:

@@ -480,6 +480,33 @@ def test_fused_decoder_matches_eager_mini(dev, scheme):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("B,T0", [(1, 1), (1, 64), (4, 16), (2, 31)])
+@pytest.mark.parametrize("emb", [False, True])
+def test_row_prefill_matches_forward_prefill(dev, B, T0, emb):
+    """Prompts of up to 64 rows with int8 blocks: the fused decoder's own
+    prefill (fused-epilogue Linears over the rows, the prefill attention,
+    head and argmax kernels) against the model's forward prefill: the same
+    first token, slot and position, the caches and the last rows' logits to
+    fp32 rounding; with the fp32 tied head and with int8 head codes."""
+    cfg = g.GPTConfig(vocab_size=97, n_positions=96, n_layer=2, n_head=2, n_embd=128)
+    qm, _ = g.quantize_model(_model(cfg, dev), 8, include_embedding=emb)
+    prompt = OM.benchmark_prompt(97, B, T0).to(dev)
+    rows, fwd = g.FusedDecoder(qm, B, T0 + 4), g.FusedDecoder(qm, B, T0 + 4)
+    assert rows.rows_prefill
+    fwd.rows_prefill = False
+    rows.start(prompt)
+    fwd.start(prompt)
+    with torch.no_grad():
+        want = qm(prompt, last_only=True)["logits"][:, -1, :]
+    torch.cuda.synchronize()
+    assert torch.equal(rows.out, fwd.out) and torch.equal(rows.tok, fwd.tok) and torch.equal(rows.pos, fwd.pos)
+    assert int(rows.pos) == T0 and torch.equal(rows.out[:, T0], want.argmax(-1))
+    for i in range(cfg.n_layer):
+        for a, b in ((rows.k[i], fwd.k[i]), (rows.v[i], fwd.v[i])):
+            assert float((a - b).abs().max()) <= 1e-5 * float(b.abs().max()), i
+    assert float((rows.logits - want).abs().max()) <= 1e-4 * float(want.abs().max())
+
+
 def test_graph_replays_with_different_prompts(reference_decode, dev):
     """Captured prefill and decode graphs replayed for several prompts of the
     same length, with eager work in between, match eager generation each time."""
