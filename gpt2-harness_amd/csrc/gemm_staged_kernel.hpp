@@ -236,25 +236,27 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
                 *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(w) + (k0 % kw) + wdrow[i] + 32 * j);
         }
     };
-    auto wfrag = [&](int p, int i, int b) {
-        if constexpr (GROUPED) {
-            const u32x4 v = wr[p][i][0];
-            const uint32_t d = b == 0 ? v.x : b == 1 ? v.y : b == 2 ? v.z : v.w;
-            uint32_t e, o;
-            nibbles_x16(d, e, o);
-            const u32x4 t = {bf16x2_of_x16(e, o, 0), bf16x2_of_x16(e, o, 1), bf16x2_of_x16(e, o, 2),
-                             bf16x2_of_x16(e, o, 3)};
-            return __builtin_bit_cast(bf16x8, t);
-        } else if constexpr (WD) {
-            const u32x4 v = wr[p][i][b >> 1];
-            const uint32_t s0 = (b & 1) ? v.z : v.x, s1 = (b & 1) ? v.w : v.y;
-            const u32x4 t = {bf16x2_of_bytes_perm(s0, 0), bf16x2_of_bytes_perm(s0, 16),
-                             bf16x2_of_bytes_perm(s1, 0), bf16x2_of_bytes_perm(s1, 16)};
-            return __builtin_bit_cast(bf16x8, t);
-        } else {
-            return FW[0][0];
-        }
+    auto wfrag = [&](int p, int i, int b) {  // group-wise: block b of tile i from raw set p
+        const u32x4 v = wr[p][i][0];
+        const uint32_t d = b == 0 ? v.x : b == 1 ? v.y : b == 2 ? v.z : v.w;
+        uint32_t e, o;
+        nibbles_x16(d, e, o);
+        const u32x4 t = {bf16x2_of_x16(e, o, 0), bf16x2_of_x16(e, o, 1), bf16x2_of_x16(e, o, 2),
+                         bf16x2_of_x16(e, o, 3)};
+        return __builtin_bit_cast(bf16x8, t);
     };
+    // int8 rows in registers: dword d (bf16 pair d) of block b of tile i,
+    // widened from raw set p -- a fragment a dword a bundle, so that no bundle
+    // carries more vector-ALU work than its MFMA keeps the matrix core busy
+    // (160x256: 6% faster than a whole fragment in one bundle)
+    constexpr bool SPREAD = WD && !GROUPED;
+    auto wpart = [&](int p, int i, int b, int d) -> uint32_t {
+        const u32x4 v = wr[p][i][b >> 1];
+        const uint32_t s0 = (b & 1) ? v.z : v.x, s1 = (b & 1) ? v.w : v.y;
+        return bf16x2_of_bytes_perm(d < 2 ? s0 : s1, (d & 1) * 16);
+    };
+    u32x4 FWu[2][SPREAD ? TNn : 1];  // the widened fragments [set][tile] as dwords
+    static_assert(!SPREAD || 4 * TNn <= NMF, "a widened dword per bundle");
     // D[n][m] = sum_k w[n][k] x[m][k]: result register q of lane (r, h) holds
     // n = 8 (q / 4) + 4 h + q % 4, m = r of its 32 x 32 tile
     floatx16 acc[TNn][TMm];
@@ -274,6 +276,9 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
             } else {
                 part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FW[set][i], FX[set][j], part[i][j], 0, 0, 0);
             }
+        } else if constexpr (SPREAD) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, FWu[set][i]), FX[set][j],
+                                                                acc[i][j], 0, 0, 0);
         } else {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(FW[set][i], FX[set][j], acc[i][j], 0, 0, 0);
         }
@@ -356,7 +361,12 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < NRD; ++q) fread(smem, 0, 0, q);
-    if constexpr (WD) {
+    if constexpr (SPREAD) {
+#pragma unroll
+        for (int i = 0; i < TNn; ++i)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) FWu[0][i][d] = wpart(0, i, 0, d);
+    } else if constexpr (GROUPED) {
 #pragma unroll
         for (int i = 0; i < TNn; ++i) FW[0][i] = wfrag(0, i, 0);
     }
@@ -415,7 +425,9 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
 #pragma unroll
                     for (int q = t * NRD / NMF; q < (t + 1) * NRD / NMF; ++q) fread(cur, kk + 1, set ^ 1, q);
                 }
-                if constexpr (WD) {
+                if constexpr (SPREAD) {
+                    if (t < 4 * TNn) FWu[set ^ 1][t >> 2][t & 3] = wpart(p, t >> 2, kk + 1, t & 3);
+                } else if constexpr (GROUPED) {
                     if (t < TNn) FW[set ^ 1][t] = wfrag(p, t, kk + 1);
                 }
                 const int b = kk * NMF + t;
@@ -439,6 +451,12 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
             if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
             if constexpr (WD) {
                 if ((t + 1) * WLD / NMF > t * WLD / NMF) wload(k2, p, t * WLD / NMF);
+            }
+            // block 0 of the next step (raw set p ^ 1) into set 0, which this
+            // group's MFMAs do not read
+            if constexpr (SPREAD) {
+                if (t < 4 * TNn) FWu[0][t >> 2][t & 3] = wpart(p ^ 1, t >> 2, 0, t & 3);
+            } else if constexpr (GROUPED) {
                 if (t == NMF - 1) {
 #pragma unroll
                     for (int i = 0; i < TNn; ++i) FW[0][i] = wfrag(p ^ 1, i, 0);
