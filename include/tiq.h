@@ -74,7 +74,8 @@ enum tiq_activation { TIQ_ACT_NONE = 0, TIQ_ACT_GELU_TANH = 1 };
 int tiq_stamp_begin(uint64_t* buf, int64_t slots);
 int64_t tiq_stamp_end(int64_t* first_slot, int64_t* workgroups, int64_t max_launches);
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* Library version: one integer, raised with every change of the kernels
+ * (measurement records taken with one version name it). */
 int tiq_version(void);
 /* Static string naming a status code (never NULL). */
 const char* tiq_status_string(int status);
