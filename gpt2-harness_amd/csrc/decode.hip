@@ -12,6 +12,8 @@
 //   argmax_rows       -- logits.argmax(-1) (sampling.py:164), first index of
 //                        the maximum, the token also written into the id
 //                        buffer at column pos + 1.
+#include <cmath>
+
 #include "tiq_internal.hpp"
 
 namespace tiq {
@@ -497,6 +499,251 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(
     }
 }
 
+// ------------------------------------------------------------ screened head
+// The tied fp32 head and its argmax at one row (GPT.forward's lm_head,
+// model.py:585, then logits.argmax(-1), sampling.py:164), reading a bf16 copy
+// of the head instead of all of its fp32 rows. Per row v, with x the
+// LayerNorm'd row, a_v = x . bf16(w_v) in fp32 and the exact logit e_v =
+// x . w_v in fp32 differ by at most
+//   |x . (w_v - bf16(w_v))| + gamma (|x| . |w_v| + |x| . |bf16(w_v)|)
+//   <= ||x|| (err_v + gamma (2 norm_v + err_v)) = b_v
+// (Cauchy-Schwarz; gamma = C u / (1 - C u), u = 2^-24, bounds the rounding of
+// a length-C dot product in any order; err_v = ||w_v - bf16(w_v)||_2, norm_v =
+// ||w_v||_2; tiq_head_screen_prepare stores the row's coefficient
+// err_v + gamma (2 norm_v + err_v), rounded up, so b_v = ||x|| coef_v). Among a
+// workgroup's rows, every row with a_v + b_v below L = max (a_u - b_u) has an
+// exact logit below the exact logit of the row that attains L, so the
+// workgroup's exact maximum is among its rows with a_v + b_v >= L (usually
+// one): only those are recomputed from the fp32 weights. The workgroup writes
+// (its exact maximum, the first row attaining it) -- the semantics of
+// argmax_partial_kernel: NaN never wins, -inf everywhere gives the first row --
+// and argmax_parts_kernel reduces the workgroups' pairs. The logits buffer
+// holds a_v, and e_v for the recomputed rows.
+// Layout: kHsGroups workgroups of kHsWaves wavefronts (two a CU, all resident
+// at once); a wavefront takes the 4-row chunks gw, gw + W, gw + 2 W, ... of the
+// head (gw its index among the W wavefronts), the next chunk's bf16 rows in
+// flight while the current one is summed, so the head streams in one pass.
+constexpr int kHsWaves = 8, kHsGroups = 512, kHsChunk = 4, kHsMaxChunks = 8;
+constexpr int kHsMaxCols = 64 * 16;  // a lane holds 16 columns of the row
+
+__device__ __forceinline__ void better_i32(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+__global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4))) void head_screen_kernel(
+    const float* __restrict__ x, int C, const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
+    const uint16_t* __restrict__ wb, const float* __restrict__ wf, int64_t ldw, const float* __restrict__ row_coef,
+    int V, float* __restrict__ logits, float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float4 xs[64][4];  // the LayerNorm'd row, lane l's 16 columns at xs[l]
+    __shared__ float sxn;         // its 2-norm
+    __shared__ float lo[kHsWaves];
+    __shared__ float bv[kHsWaves];
+    __shared__ int bi[kHsWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int CK = C / 16;
+    const bool act = lane < CK;
+    const int cl = 16 * min(lane, CK - 1);  // a lane past the row repeats the last chunk, unused
+    const int W = gridDim.x * kHsWaves, gw = blockIdx.x * kHsWaves + wave;
+    const int NC = (V + kHsChunk - 1) / kHsChunk;
+    const int nch = gw < NC ? (NC - 1 - gw) / W + 1 : 0;  // this wavefront's chunks (<= kHsMaxChunks)
+    auto load = [&](int c, uint4 (&r)[kHsChunk][2]) {  // chunk gw + c W (rows clamped)
+        const int row0 = (gw + c * W) * kHsChunk;
+#pragma unroll
+        for (int q = 0; q < kHsChunk; ++q) {
+            const uint16_t* p = wb + (int64_t)min(row0 + q, V - 1) * C + cl;
+            r[q][0] = *reinterpret_cast<const uint4*>(p);
+            r[q][1] = *reinterpret_cast<const uint4*>(p + 8);
+        }
+    };
+    uint4 buf[2][kHsChunk][2];
+    if (nch > 0) load(0, buf[0]);
+    if (nch > 1) load(1, buf[1]);
+    // lane q + 4 c holds row q of chunk c: its bound's inputs requested now
+    const int lc = lane / kHsChunk, lq = lane % kHsChunk;
+    const int my_row = (gw + lc * W) * kHsChunk + lq;
+    const bool mine = lc < nch && my_row < V;
+    const int nl = mine ? my_row : 0;
+    const float k_l = row_coef[nl];
+    if (wave == 0) {  // LayerNorm (two-pass mean and biased variance, as torch) into LDS
+        float v[16], g[16], bb[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            *reinterpret_cast<float4*>(v + 4 * q) = reinterpret_cast<const float4*>(x + cl)[q];
+            *reinterpret_cast<float4*>(g + 4 * q) = reinterpret_cast<const float4*>(ln_w + cl)[q];
+            *reinterpret_cast<float4*>(bb + 4 * q) = reinterpret_cast<const float4*>(ln_b + cl)[q];
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sum += v[j];
+        const float mean = wave_sum_dpp(act ? sum : 0.f) / (float)C;
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) d += (v[j] - mean) * (v[j] - mean);
+        const float rstd = 1.0f / sqrtf(wave_sum_dpp(act ? d : 0.f) / (float)C + eps);
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            v[j] = (v[j] - mean) * rstd * g[j] + bb[j];
+            ss = fmaf(v[j], v[j], ss);
+        }
+        ss = wave_sum_dpp(act ? ss : 0.f);
+        if (act) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xs[lane][q] = *reinterpret_cast<const float4*>(v + 4 * q);
+        }
+        if (lane == 0) sxn = sqrtf(ss);
+    }
+    __syncthreads();
+    float xl[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(xl + 4 * q) = xs[act ? lane : 0][q];
+    // ||x|| with its own rounding covered (a relative 2^-10 is far above it)
+    const float xn = sxn * (1.0f + 0x1p-10f);
+    // a_v of this wavefront's rows, lane q + 4 c taking row q of chunk c
+    float a_l = 0.f;
+#pragma unroll
+    for (int c = 0; c < kHsMaxChunks; ++c) {
+        if (c < nch) {  // uniform across the wavefront
+            const uint4 (&r)[kHsChunk][2] = buf[c & 1];
+#pragma unroll
+            for (int q = 0; q < kHsChunk; ++q) {
+                const uint32_t w32[8] = {r[q][0].x, r[q][0].y, r[q][0].z, r[q][0].w,
+                                         r[q][1].x, r[q][1].y, r[q][1].z, r[q][1].w};
+                float s = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    s = fmaf(bf_lo(w32[j]), xl[2 * j], s);
+                    s = fmaf(bf_hi(w32[j]), xl[2 * j + 1], s);
+                }
+                const float a = wave_sum_dpp(act ? s : 0.f);
+                a_l = lane == q + kHsChunk * c ? a : a_l;
+            }
+            if (c + 2 < nch) load(c + 2, buf[c & 1]);  // its registers are free now
+        }
+    }
+    const float b_l = xn * k_l * (1.0f + 0x1p-10f);
+    const float hi_l = a_l + b_l;
+    if (mine) logits[my_row] = a_l;
+    const float low = wave_max_dpp(mine ? a_l - b_l : -INFINITY);
+    if (lane == 0) lo[wave] = low;
+    __syncthreads();
+    float L = lo[0];
+#pragma unroll
+    for (int w = 1; w < kHsWaves; ++w) L = fmaxf(L, lo[w]);
+    // the candidates of this wavefront, recomputed from the fp32 rows
+    float best = -INFINITY;
+    int bidx = INT32_MAX;
+    uint64_t cand = __ballot(mine && hi_l >= L);  // lane q + 4 c: row q of chunk c
+    while (cand) {
+        const int l = __builtin_ctzll(cand);
+        cand &= cand - 1;
+        const int n = (gw + (l / kHsChunk) * W) * kHsChunk + l % kHsChunk;
+        const float* p = wf + (int64_t)n * ldw + cl;
+        float s = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 f = reinterpret_cast<const float4*>(p)[q];
+            s = fmaf(f.x, xl[4 * q], s);
+            s = fmaf(f.y, xl[4 * q + 1], s);
+            s = fmaf(f.z, xl[4 * q + 2], s);
+            s = fmaf(f.w, xl[4 * q + 3], s);
+        }
+        const float e = wave_sum_dpp(act ? s : 0.f);
+        if (lane == 0) logits[n] = e;
+        better_i32(best, bidx, e, n);
+    }
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = bidx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // no row above -inf: the group's first row, as argmax_partial_kernel
+        float v = -INFINITY;
+        int i = gw < NC ? gw * kHsChunk : INT32_MAX;
+#pragma unroll
+        for (int w = 0; w < kHsWaves; ++w) better_i32(v, i, bv[w], bi[w]);
+        pv[blockIdx.x] = v;
+        pi[blockIdx.x] = i;
+    }
+}
+
+// The workgroups' (maximum, index) pairs of one row reduced to its argmax;
+// the token is written to out and to ids at column pos + 1, and pos advanced.
+__global__ __launch_bounds__(1024) void argmax_parts_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                            int P, int64_t* __restrict__ out,
+                                                            int64_t* __restrict__ ids, int64_t ld_ids,
+                                                            int64_t* __restrict__ pos_p) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t col = pos_p ? *pos_p + 1 : 0;
+    float v = -INFINITY;
+    int idx = INT32_MAX;
+    for (int k = tid; k < P; k += 1024) better_i32(v, idx, pv[k], pi[k]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) better_i32(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
+    if (lane == 0) {
+        sv[wave] = v;
+        si[wave] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w) better_i32(v, idx, sv[w], si[w]);
+        out[0] = idx;
+        if (ids && col >= 0 && col < ld_ids) ids[col] = idx;
+        if (pos_p && ids) *pos_p = col;
+    }
+}
+
+// bf16 copy of the head (round to nearest even), and per row the bound
+// coefficient err + gamma (2 norm + err) from the 2-norms of w - bf16(w) and of
+// w, summed in fp64 and rounded up to fp32.
+__device__ __forceinline__ float f32_round_up(double d) {  // d >= 0
+    float f = (float)d;
+    if ((double)f < d) f = __uint_as_float(__float_as_uint(f) + 1u);  // the next float up
+    return f;
+}
+
+__global__ __launch_bounds__(256) void head_screen_prepare_kernel(const float* __restrict__ w, int C, int64_t ldw,
+                                                                  uint16_t* __restrict__ wb,
+                                                                  float* __restrict__ row_coef) {
+    __shared__ double red[2][4];
+    const int64_t n = blockIdx.x;
+    const int tid = threadIdx.x;
+    double e2 = 0.0, n2 = 0.0;
+    for (int c = tid; c < C; c += 256) {
+        const float v = w[n * ldw + c];
+        const uint16_t h = f32_to_bf16_bits(v);
+        wb[n * C + c] = h;
+        const double d = (double)v - (double)bf16_bits_to_f32(h);
+        e2 += d * d;
+        n2 += (double)v * (double)v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        e2 += __shfl_xor(e2, off, 64);
+        n2 += __shfl_xor(n2, off, 64);
+    }
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = e2;
+        red[1][tid >> 6] = n2;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // the fp64 sums of C squares are within a relative C 2^-53 of the
+        // exact ones; one fp64 ulp per term more, rounded up
+        const double se = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) * (1.0 + (C + 4) * 0x1p-52);
+        const double sn = (red[1][0] + red[1][1] + red[1][2] + red[1][3]) * (1.0 + (C + 4) * 0x1p-52);
+        const double err = sqrt(se) * (1.0 + 0x1p-50), nrm = sqrt(sn) * (1.0 + 0x1p-50);
+        const double cu = (double)C * 0x1p-24, gamma = cu / (1.0 - cu);
+        row_coef[n] = f32_round_up((err + gamma * (2.0 * nrm + err)) * (1.0 + 0x1p-50));
+    }
+}
+
 // y = gelu_tanh(x) elementwise (the MLP activation of a prefill, one pass in
 // place of the reference's op chain at model.py:57-75): 4 values a thread per
 // step of a grid-stride loop; n % 4 tail by the first threads.
@@ -517,6 +764,7 @@ __global__ __launch_bounds__(256) void gelu_tanh_kernel(const float* x, float* y
 }  // namespace tiq
 
 using namespace tiq;
+
 
 // qkv rows, or (n_sl > 0) the raw partial slices of the q, k, v projection
 // with its scale and bias
@@ -651,6 +899,50 @@ extern "C" int tiq_embed_tokens(const int64_t* tokens, const int64_t* pos, const
     if (!tokens || !pos || !wte || !wpe || !x) return TIQ_EINVAL;
     hipLaunchKernelGGL(embed_kernel, dim3((unsigned)batch), dim3(256), 0, as_stream(stream), tokens, pos, wte, wpe,
                        vocab, n_positions, n_embd, x);
+    return launch_status();
+}
+
+extern "C" size_t tiq_head_screen_workspace(int64_t vocab) {
+    if (vocab <= 0) return 0;
+    return (size_t)kHsGroups * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int tiq_head_screen_prepare(const float* w, int64_t vocab, int64_t n_embd, int64_t ldw, uint16_t* w_bf16,
+                                       float* row_coef, void* stream) {
+    if (vocab <= 0 || n_embd <= 0 || ldw < n_embd) return TIQ_EINVAL;
+    if (!w || !w_bf16 || !row_coef) return TIQ_EINVAL;
+    if (vocab > INT32_MAX || n_embd > INT32_MAX) return TIQ_EUNSUPPORTED;
+    hipLaunchKernelGGL(head_screen_prepare_kernel, dim3((unsigned)vocab), dim3(256), 0, as_stream(stream), w,
+                       (int)n_embd, ldw, w_bf16, row_coef);
+    return launch_status();
+}
+
+extern "C" int tiq_head_argmax_screened(const float* x, int64_t n_embd, const float* ln_w, const float* ln_b,
+                                        float ln_eps, const uint16_t* w_bf16, const float* w, int64_t ldw,
+                                        const float* row_coef, int64_t vocab, float* logits, int64_t* out,
+                                        int64_t* ids, int64_t ld_ids, int64_t* pos, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    if (vocab <= 0 || n_embd <= 0 || ldw < n_embd) return TIQ_EINVAL;
+    if (!x || !ln_w || !ln_b || !w_bf16 || !w || !row_coef || !logits || !out || (ids && !pos))
+        return TIQ_EINVAL;
+    if (!workspace) return TIQ_EINVAL;
+    // every wavefront's chunks in its registers' reach (GPT-2's 50257 rows: 4 chunks a wavefront)
+    if (n_embd % 16 != 0 || n_embd > kHsMaxCols || vocab > (int64_t)kHsMaxChunks * kHsChunk * kHsGroups * kHsWaves)
+        return TIQ_EUNSUPPORTED;
+    if (!aligned(x, 16) || !aligned(ln_w, 16) || !aligned(ln_b, 16) || !aligned(w_bf16, 16) || !aligned(w, 16) ||
+        ldw % 4 != 0)
+        return TIQ_EALIGN;
+    if (workspace_bytes < tiq_head_screen_workspace(vocab)) return TIQ_EWORKSPACE;
+    if (!aligned(workspace, 4)) return TIQ_EALIGN;
+    const int64_t P = kHsGroups;
+    float* pv = static_cast<float*>(workspace);
+    int* pi = reinterpret_cast<int*>(pv + P);
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(head_screen_kernel, dim3((unsigned)P), dim3(64 * kHsWaves), 0, st, x, (int)n_embd, ln_w, ln_b,
+                       ln_eps, w_bf16, w, ldw, row_coef, (int)vocab, logits, pv, pi);
+    int rc = launch_status();
+    if (rc) return rc;
+    hipLaunchKernelGGL(argmax_parts_kernel, dim3(1), dim3(1024), 0, st, pv, pi, (int)P, out, ids, ld_ids, pos);
     return launch_status();
 }
 

@@ -77,6 +77,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                _i64, _i64, _vp, _i64, _i64, _i64, _vp], _i32),
     "tiq_argmax_rows_workspace": ([_i64], _sz),
     "tiq_argmax_rows": ([_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _vp], _i32),
+    "tiq_head_screen_workspace": ([_i64], _sz),
+    "tiq_head_screen_prepare": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp], _i32),
+    "tiq_head_argmax_screened": ([_vp, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
+                                  _vp, _sz, _vp], _i32),
 }
 
 WF_INT8, WF_INT4, WF_INT4G, WF_F32, WF_INT8_TILED, WF_F32_TILED = 0, 1, 2, 3, 4, 5

@@ -240,6 +240,21 @@ class FusedDecoder(_DecoderBase):
         head_ok = self.head_q is None or self.head_q.fmt == FMT_W8
         self.chain = 5 <= B <= 64 and head_ok and all(l.fmt == FMT_W8 for l in lins)
         self.rows_prefill = all(l.fmt == FMT_W8 for l in lins)
+        # One sequence with the tied fp32 head: the decode step's head and
+        # argmax read a bf16 copy of the head and recompute from the fp32
+        # rows only those whose certified bound reaches the best of their
+        # group (tiq_head_argmax_screened): the argmax of the fp32 logits
+        self.screen = (B == 1 and self.head_q is None and C % 16 == 0 and C <= 1024)
+        if self.screen:
+            V, L = cfg.vocab_size, self.L
+            st = torch.cuda.current_stream(dev).cuda_stream
+            self.head_bf16 = torch.empty(V, C, dtype=torch.int16, device=dev)  # bf16 bits
+            self.head_coef = torch.empty(V, device=dev)                          # bound coefficient a row
+            n = int(L.tiq_head_screen_workspace(V))
+            self.screen_ws = torch.empty(n, dtype=torch.uint8, device=dev)
+            _lib.check(L.tiq_head_screen_prepare(self.head_w.data_ptr(), V, C, self.head_w.stride(0),
+                                                 self.head_bf16.data_ptr(), self.head_coef.data_ptr(), st),
+                       "head screen prepare")
         if self.chain:
             L = self.L
             head_wf = _lib.WF_F32 if self.head_q is None else _lib.WF_INT8
@@ -285,9 +300,11 @@ class FusedDecoder(_DecoderBase):
     def extra_weight_bytes(self) -> int:
         """Device bytes of the weight copies this decoder holds beyond the
         model's own (the batched step's operand tiles of the int8 block codes
-        and of the fp32 tied head; 0 for one to four sequences, which read the
-        model's row-major codes)."""
-        return sum(t.numel() * t.element_size() for t in getattr(self, "tiles", {}).values())
+        and of the fp32 tied head; for one sequence with the fp32 tied head
+        its bf16 copy and one float a row for the screened argmax; 0 for two
+        to four sequences, which read the model's row-major codes)."""
+        extra = [self.head_bf16, self.head_coef] if getattr(self, "screen", False) else []
+        return sum(t.numel() * t.element_size() for t in [*getattr(self, "tiles", {}).values(), *extra])
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
         M, K = x.shape
@@ -480,6 +497,14 @@ class FusedDecoder(_DecoderBase):
             self._linear(mlp.c_fc, self.x, self.hid, ln=block.ln_2, act=_lib.ACT_GELU_TANH)
             self._linear(mlp.c_proj, self.hid, self.x, res=self.x)
         ln = m.ln_f
+        if self.screen:  # head + argmax, which also records the token and advances pos
+            _lib.check(L.tiq_head_argmax_screened(
+                self.x.data_ptr(), C, ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps),
+                self.head_bf16.data_ptr(), self.head_w.data_ptr(), self.head_w.stride(0), self.head_coef.data_ptr(),
+                cfg.vocab_size, self.logits.data_ptr(), self.tok_flat.data_ptr(),
+                self.out.data_ptr(), self.T, self.pos.data_ptr(), self.screen_ws.data_ptr(), self.screen_ws.numel(),
+                st), "screened head")
+            return
         if self.head_q is not None:
             self._linear(self.head_q, self.x, self.logits, ln=ln)
         else:

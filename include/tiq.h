@@ -485,6 +485,34 @@ size_t tiq_argmax_rows_workspace(int64_t rows);
 int tiq_argmax_rows(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t* out, int64_t* ids,
                     int64_t ld_ids, int64_t* pos, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The tied fp32 head and its argmax for one row (GPT.forward's lm_head,
+ * model.py:585, then logits.argmax(-1) and the id append, sampling.py:164-170),
+ * reading a bf16 copy of the head: every row's logit is first computed from the
+ * bf16 copy in fp32, together with a bound ||x|| row_coef[v] on its distance from
+ * the logit of the fp32 weights (row_coef = err + gamma (2 norm + err), err =
+ * ||w_v - bf16(w_v)||_2, norm = ||w_v||_2, gamma = C 2^-24 / (1 - C 2^-24): the
+ * bf16 rounding by Cauchy-Schwarz plus the rounding of both fp32 dot products
+ * in any order), and only the rows whose upper bound reaches the best lower
+ * bound of their workgroup are computed again from the fp32 weights; the token
+ * is the first index of the maximum of those exact logits (NaN never selected,
+ * as tiq_argmax_rows), so it is the argmax of the fp32 logits. x is the row
+ * before the final LayerNorm (ln_w, ln_b, ln_eps); n_embd % 16 == 0, n_embd <=
+ * 1024, vocab <= 131072; logits receives the bf16 estimates and the exact values
+ * of the recomputed rows. out, ids, ld_ids and pos as tiq_argmax_rows. The extra
+ * device bytes are the bf16 copy (2 bytes a weight) and one float a row, from
+ * tiq_head_screen_prepare. No counterpart in the reference beyond the head and
+ * argmax it replaces. */
+size_t tiq_head_screen_workspace(int64_t vocab);
+/* w_bf16 = round-to-nearest-even bf16 of the (vocab, n_embd) head w (rows of
+ * ldw floats) and row_coef[v] = err + gamma (2 norm + err) as above, the norms
+ * summed in fp64 and the coefficient rounded up to fp32. */
+int tiq_head_screen_prepare(const float* w, int64_t vocab, int64_t n_embd, int64_t ldw, uint16_t* w_bf16,
+                            float* row_coef, void* stream);
+int tiq_head_argmax_screened(const float* x, int64_t n_embd, const float* ln_w, const float* ln_b, float ln_eps,
+                             const uint16_t* w_bf16, const float* w, int64_t ldw, const float* row_coef,
+                             int64_t vocab, float* logits, int64_t* out, int64_t* ids, int64_t ld_ids, int64_t* pos,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
