@@ -412,14 +412,17 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
     """int8 -> bf16 prefill GEMM (tiq_gemm_w8_ws; fmt="int4": the reference
     nibble layout, tiq_linear_w4; fmt="int4_g128": the group-wise int4 GEMM,
     tiq_linear_w4g_ws, group 128, split over K where the tiles are few) per
-    shape: `reps` launches back
-    to back between one HIP event pair, rotating over `copies` independent
+    shape: a captured HIP graph of one launch per `copies` independent
     (activation, weight, output) sets (at M = 4096 on 1600 x 6400 the eight
     sets hold 600 MB, past the 256 MB Infinity Cache), so no launch finds its
-    operands left in the caches by the one before. Beside it, as the
-    measured-achievable reference (not this library's path), the platform's
-    bf16 GEMM (torch.matmul -> hipBLASLt) on bf16 weights of the same shape,
-    rotated the same way."""
+    operands left in the caches by the one before; the graph replayed between
+    one HIP event pair, the median over `reps // copies` timings, per launch.
+    In a graph neither side pays the host's launch cost (the platform GEMM's
+    eager call costs 20 us a launch on the host, more than its kernel at
+    M = 256). Beside it, as the measured-achievable reference (not this
+    library's path), the platform's bf16 GEMM (torch.matmul -> hipBLASLt) on
+    bf16 weights of the same shape, rotated the same way. The stamped pass
+    (M = 4096) times `reps` eager launches instead, one stamp slot each."""
     import torch
 
     import gpt2_harness_amd as g
@@ -441,10 +444,34 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1e3 / reps
 
+    def timed_graph(fns):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            for f in fns:
+                f()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                for f in fns:
+                    f()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(max(reps // len(fns), 3)):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / len(fns))
+        del graph
+        return statistics.median(ts)
+
     for K, N in kn:
         n_ws = int(L.tiq_gemm_w8_workspace(1, M, K, N))  # split-K partials when the tiles are few
         ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=dev)
-        st = torch.cuda.current_stream().cuda_stream
         sets, lib_sets = [], []
         for _ in range(copies):
             w = torch.randn(N, K, generator=gen, device=dev) * 0.02
@@ -458,10 +485,11 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
                 q, s = g.quantize_groupwise_int4(w, 128)
             x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
             sets.append((x, q, s, torch.empty(M, N, device=dev, dtype=torch.bfloat16)))
-            lib_sets.append((x, w.to(torch.bfloat16)))
+            lib_sets.append((x, w.to(torch.bfloat16), torch.empty(M, N, device=dev, dtype=torch.bfloat16)))
             del w
 
         def run(x, q, s, y):
+            st = torch.cuda.current_stream().cuda_stream  # the capturing stream inside a graph
             if fmt == "int8":
                 rc = L.tiq_gemm_w8_ws(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), None, N, y.data_ptr(), 1,
                                       N, ws.data_ptr(), n_ws, st)
@@ -474,7 +502,7 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
             if rc:
                 raise RuntimeError(f"{fmt} GEMM status {rc}")
 
-        us = timed([lambda a=a: run(*a) for a in sets])
+        us = timed_graph([lambda a=a: run(*a) for a in sets])
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
         stamp = None
         if stamped and fmt == "int8":
@@ -494,7 +522,7 @@ def gemm_section(M, kn, dev, reps=24, copies=8, fmt="int8", stamped=False):
                 # the matrix cores' peak scales with the shader clock (datasheet: 2.4 GHz)
                 stamp = {"kernel_us": kus, "TFLOP/s": tf_k, "launch_us": us_st, "clock_GHz": clk,
                          "frac_of_peak_at_clock": tf_k / (BF16_PEAK_TFLOPS * clk / 2.4)}
-        us_lib = timed([lambda x=x, wb=wb: torch.matmul(x, wb.T) for x, wb in lib_sets])
+        us_lib = timed_graph([lambda x=x, wb=wb, yb=yb: torch.matmul(x, wb.T, out=yb) for x, wb, yb in lib_sets])
         tf_lib = 2.0 * M * N * K / (us_lib * 1e-6) / 1e12
         out[f"{K}x{N}"] = {"us": us, "TFLOP/s": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
                            "library_bf16_us": us_lib, "library_bf16_TFLOP/s": tf_lib,

@@ -17,15 +17,19 @@ namespace {
 #include "gemm_staged_kernel.hpp"
 
 constexpr int kGroup = 128;  // two k64 steps
-constexpr int kBM = 224, kBN = 128;
+constexpr int kBN = 128;
+
+// Tile height: 224 rows, or 128 where M <= 512 fills 128-row tiles with
+// fewer rows than 224-row ones (M = 256: 256 rows of work instead of 448).
+int w4g_rows(int64_t M) { return M <= 512 && (M + 127) / 128 * 128 < (M + 223) / 224 * 224 ? 128 : 224; }
 
 // One workgroup per tile (the group-wise kernel does not run persistent);
 // gridDim.z = S splits of whole groups, fp32 slices without bias when S > 1.
-template <typename TY>
+template <int BM, typename TY>
 int run_w4g(const LinearArgs& a, TY* y, int64_t ldy, const float* bias, int64_t S) {
-    const int64_t tiles = ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
+    const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + kBN - 1) / kBN);
     const int ngroups = (int)((a.K + kGroup - 1) / kGroup);
-    hipLaunchKernelGGL((gemm_staged<kBM, kBN, 1, kW4G, TY>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
+    hipLaunchKernelGGL((gemm_staged<BM, kBN, 1, kW4G, TY>), dim3((unsigned)tiles, 1, (unsigned)S), dim3(256), 0,
                        a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, nullptr, bias, y, ldy,
                        (int)a.M, (int)a.N, (int)a.K, (int)a.K, a.scale16, ngroups, nullptr);
     return launch_status();
@@ -47,10 +51,11 @@ bool staged_w4g_supported(const LinearArgs& a) {
     return true;
 }
 
-// Splits of whole groups when the 224 x 128 tiles fill less than a round of
-// 256 CUs (at most 8, at most one a group, within the workspace); 1: none.
+// Splits of whole groups when the tiles fill less than a round of 256 CUs (at
+// most 8, at most one a group, within the workspace); 1: none.
 int64_t staged_w4g_splits(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
-    const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    const int bm = w4g_rows(M);
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + kBN - 1) / kBN);
     const int64_t groups = (K + kGroup - 1) / kGroup;
     int64_t S = std::min<int64_t>(std::min<int64_t>(256 / std::max<int64_t>(tiles, 1), groups), 8);
     S = std::min<int64_t>(S, (int64_t)(ws_bytes / (size_t)(M * N * 4)));
@@ -60,14 +65,18 @@ int64_t staged_w4g_splits(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
 int launch_staged_w4g(const LinearArgs& a, void* ws, size_t ws_bytes) {
     if (!staged_w4g_supported(a)) return TIQ_EUNSUPPORTED;
     const int64_t S = (ws && aligned(ws, 16)) ? staged_w4g_splits(a.M, a.N, a.K, ws_bytes) : 1;
+    const bool short_m = w4g_rows(a.M) == 128;
     if (S > 1 && a.M * a.N * S <= 0x7fffffffLL) {
         float* part = static_cast<float*>(ws);
-        int rc = run_w4g<float>(a, part, a.N, nullptr, S);
+        int rc = short_m ? run_w4g<128, float>(a, part, a.N, nullptr, S) : run_w4g<224, float>(a, part, a.N, nullptr, S);
         if (rc != TIQ_OK) return rc;
         return launch_splitk_reduce(a, part, S, nullptr);
     }
-    if (a.y_dtype == TIQ_F32) return run_w4g<float>(a, static_cast<float*>(a.y), a.ldy, a.bias, 1);
-    return run_w4g<uint16_t>(a, static_cast<uint16_t*>(a.y), a.ldy, a.bias, 1);
+    if (a.y_dtype == TIQ_F32)
+        return short_m ? run_w4g<128, float>(a, static_cast<float*>(a.y), a.ldy, a.bias, 1)
+                       : run_w4g<224, float>(a, static_cast<float*>(a.y), a.ldy, a.bias, 1);
+    return short_m ? run_w4g<128, uint16_t>(a, static_cast<uint16_t*>(a.y), a.ldy, a.bias, 1)
+                   : run_w4g<224, uint16_t>(a, static_cast<uint16_t*>(a.y), a.ldy, a.bias, 1);
 }
 
 }  // namespace tiq

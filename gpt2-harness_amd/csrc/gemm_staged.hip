@@ -13,7 +13,7 @@ namespace {
 
 #include "gemm_staged_kernel.hpp"
 
-template <int BM, int BN, int WMW, int FMT, typename TY>
+template <int BM, int BN, int WMW, int FMT, typename TY, int DEPTH = 2>
 int run_staged(const LinearArgs& a) {
     const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const int64_t slots = 256 * (BM * BN <= 128 * 128 ? 2 : 1);
@@ -21,14 +21,14 @@ int run_staged(const LinearArgs& a) {
     // int8 weights with bf16 output have a stamped copy for measurement
     if constexpr (FMT == kW8 && sizeof(TY) == 2) {
         if (uint64_t* sp = stamp_slots(grid)) {
-            hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY, true>), dim3((unsigned)grid), dim3(256), 0,
+            hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY, true, DEPTH>), dim3((unsigned)grid), dim3(256), 0,
                                a.stream, static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
                                static_cast<TY*>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K,
                                (int)(a.kw ? a.kw : a.K), nullptr, 0, sp);
             return launch_status();
         }
     }
-    hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+    hipLaunchKernelGGL((gemm_staged<BM, BN, WMW, FMT, TY, false, DEPTH>), dim3((unsigned)grid), dim3(256), 0, a.stream,
                        static_cast<const uint16_t*>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias, static_cast<TY*>(a.y),
                        a.ldy, (int)a.M, (int)a.N, (int)a.K, (int)(a.kw ? a.kw : a.K), nullptr, 0, nullptr);
     return launch_status();
@@ -144,6 +144,7 @@ int dispatch_staged_f32(const LinearArgs& a, int choice) {
     switch (choice) {
         case 0: return run_staged<256, 256, 2, FMT, float>(a);
         case 1: return run_staged<256, 128, 2, FMT, float>(a);
+        case 6: return run_staged<128, 128, 2, FMT, float, 4>(a);
         default: return run_staged<128, 128, 2, FMT, float>(a);
     }
 }
@@ -156,6 +157,7 @@ int dispatch_staged_bf16(const LinearArgs& a, int choice) {
         case 3: return run_staged<224, 256, 1, FMT, uint16_t>(a);
         case 4: return run_staged<160, 256, 1, FMT, uint16_t>(a);
         case 5: return run_staged<224, 128, 1, FMT, uint16_t>(a);
+        case 6: return run_staged<128, 128, 2, FMT, uint16_t, 4>(a);
         default: return run_staged<128, 128, 2, FMT, uint16_t>(a);
     }
 }
@@ -163,7 +165,15 @@ int dispatch_staged_bf16(const LinearArgs& a, int choice) {
 
 bool staged_gemm_supported(const LinearArgs& a) { return staged_supported_impl(a); }
 
-int staged_gemm_choice(const LinearArgs& a) { return staged_choice(a.M, a.N, a.K, a.y_dtype == TIQ_BF16); }
+// 128 x 128 tiles that all fit on the CUs at once (one a CU) take the copy with
+// four staging sets: the loads of a stage go out three k64 steps before they
+// are needed (GPT-2-XL shapes at M = 256 / 1024: 7-9% faster, bit-identical);
+// with more tiles two workgroups share a CU, which the deeper copy's registers
+// do not allow.
+int staged_gemm_choice(const LinearArgs& a) {
+    const int c = staged_choice(a.M, a.N, a.K, a.y_dtype == TIQ_BF16);
+    return c == 2 && ((a.M + 127) / 128) * ((a.N + 127) / 128) <= 256 ? 6 : c;
+}
 
 int launch_staged_gemm(const LinearArgs& a, int choice) {
     if (!staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
@@ -173,6 +183,10 @@ int launch_staged_gemm(const LinearArgs& a, int choice) {
 
 int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     if ((a.fmt != kW8 && a.fmt != kW4) || !staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
+    // a quarter of the CUs or more with tiles and a short K: the slices' trip
+    // through memory costs more than the idle CUs (GPT-2-XL at M = 256 with
+    // N >= 4800 and at M = 1024 with N = K = 1600: 7-11% slower split)
+    if (((a.M + 127) / 128) * ((a.N + 127) / 128) >= 64 && a.K / BK <= 32) return TIQ_EUNSUPPORTED;
     const int64_t S = staged_splits(a.M, a.N, a.K);
     const size_t need = staged_split_workspace(a.M, a.N, a.K);
     if (S <= 1 || !ws || ws_bytes < need || !aligned(ws, 16)) return TIQ_EUNSUPPORTED;

@@ -108,7 +108,11 @@ __device__ __forceinline__ uint32_t bf16x2_of_x16(uint32_t e, uint32_t o, int k)
 // tiles live there and the sums, which only the fold and the epilogue touch,
 // in VGPRs.
 // STAMP: the measurement copy (per-workgroup entry / exit times to `stamp`).
-template <int BM, int BN, int WMW, int FMT, typename TY, bool STAMP = false>
+// DEPTH: register staging sets (2, or up to 4 for the 2 x 2 layouts with the
+// weights staged through LDS): a stage's loads are issued DEPTH - 1 steps
+// before its LDS store, for tiles whose k64 step is too short to cover a trip
+// to memory (few tiles a CU at M = 256 .. 1024).
+template <int BM, int BN, int WMW, int FMT, typename TY, bool STAMP = false, int DEPTH = 2>
 __global__ __launch_bounds__(256, 1) void gemm_staged(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, const float* __restrict__ bias, TY* __restrict__ y, int64_t ldy, int M, int N,
@@ -119,6 +123,7 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
                   "int8 or reference-layout int4 weights; group-wise int4 in the 1 x 4 layout");
     constexpr bool GROUPED = FMT == kW4G;
     constexpr bool WD = WMW == 1 && (FMT == kW8 || GROUPED);  // weights straight into registers
+    static_assert(DEPTH == 2 || (!WD && DEPTH >= 2 && DEPTH <= 4), "deeper staging: LDS-staged weights only");
     constexpr int NT = 256;
     constexpr int WNW = 4 / WMW;
     constexpr int WM = BM / WMW, WN = BN / WNW;
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     const int xs0 = xrow * 128 + ((xch ^ swz8(xrow)) * 16);
     const int ws00 = XS + wrow * 128 + (((2 * wch) ^ swz8(wrow)) * 16);
     const int ws01 = XS + wrow * 128 + (((2 * wch + 1) ^ swz8(wrow)) * 16);
-    u32x4 sx[2][XL], sw[2][WL];
+    u32x4 sx[DEPTH][XL], sw[DEPTH][WL];
     auto gload = [&](int k0, int p, int q) {
         if (q < XL) {
             const uint32_t off = (uint32_t)min(m_blk + xrow + 32 * q, M - 1) * ldx2 + xch * 16;
@@ -350,7 +355,9 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     begin_tile();
     for (;;) {  // the workgroup's tiles
 #pragma unroll
-    for (int q = 0; q < NL; ++q) gload(kbase + min(1, nk - 1) * BK, 1, q);
+    for (int d = 1; d < DEPTH; ++d)
+#pragma unroll
+        for (int q = 0; q < NL; ++q) gload(kbase + min(d, nk - 1) * BK, d, q);
 #pragma unroll
     for (int q = 0; q < WLD; ++q) wload(kbase + min(1, nk - 1) * BK, 1, q);
 #pragma unroll
@@ -393,9 +400,9 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
         }
     }
 
-    // Step s: MFMAs on buffer s % 2; stage s + 1 (register set (s + 1) % 2)
+    // Step s: MFMAs on buffer s % 2; stage s + 1 (register set (s + 1) % DEPTH)
     // is stored to the other buffer over the first three k16 groups; stage
-    // s + 2 is loaded into set s % 2 over all four. Past the last stage the
+    // s + DEPTH is loaded into set s % DEPTH over all four. Past the last stage the
     // loads repeat it (clamped k), which keeps the loop body one path. WD:
     // raw weight set p (this step's) is widened one k16 group ahead; by the
     // end of the third group it is free and takes step s + 2's weights in the
@@ -406,7 +413,7 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
     auto step = [&](int s, int p) {
         uint8_t* cur = smem + (s & 1) * STAGE;
         uint8_t* nxt = smem + ((s + 1) & 1) * STAGE;
-        const int k2 = kbase + min(s + 2, nk - 1) * BK;
+        const int k2 = kbase + min(s + DEPTH, nk - 1) * BK;
         if (GROUPED && p == 0) {
             sconvert();
             sload((s0 + s) >> 1);
@@ -431,7 +438,7 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
                     if (t < TNn) FW[set ^ 1][t] = wfrag(p, t, kk + 1);
                 }
                 const int b = kk * NMF + t;
-                if ((b + 1) * NL / (3 * NMF) > b * NL / (3 * NMF)) lstore(nxt, p ^ 1, b * NL / (3 * NMF));
+                if ((b + 1) * NL / (3 * NMF) > b * NL / (3 * NMF)) lstore(nxt, (p + 1) % DEPTH, b * NL / (3 * NMF));
                 if ((b + 1) * NL / (4 * NMF) > b * NL / (4 * NMF)) gload(k2, p, b * NL / (4 * NMF));
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_sched_barrier(0);
@@ -467,11 +474,19 @@ __global__ __launch_bounds__(256, 1) void gemm_staged(
         }
     };
     int s = 0;
-    for (; s + 1 < nk; s += 2) {
+    for (; s + DEPTH - 1 < nk; s += DEPTH) {
         step(s, 0);
         step(s + 1, 1);
+        if constexpr (DEPTH > 2) step(s + 2, 2);
+        if constexpr (DEPTH > 3) step(s + 3, 3);
     }
     if (s < nk) step(s, 0);
+    if constexpr (DEPTH > 2) {
+        if (s + 1 < nk) step(s + 1, 1);
+    }
+    if constexpr (DEPTH > 3) {
+        if (s + 2 < nk) step(s + 2, 2);
+    }
     if constexpr (GROUPED) {  // the last group's partial tiles
         sconvert();
 #pragma unroll

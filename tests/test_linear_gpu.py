@@ -97,10 +97,10 @@ def test_gemm_w8_small_shapes(dev, c_oracle, KN, M):
 # Every GEMM tile configuration through tiq_gemm_w8_tile (10/11/12 the
 # register-staged int8 kernel at 256x256 / 256x128 / 128x128 tiles, 13/14/15
 # the same kernel with its wavefronts side by side along N at 224x256 /
-# 160x256 / 224x128 (bf16 output; 128x128 for fp32 output), 1-4 the
-# LDS-dequant kernel that also serves int4), on full, partial-row and
-# partial-column tiles.
-@pytest.mark.parametrize("tile", [10, 11, 12, 13, 14, 15, 1, 2, 3, 4])
+# 160x256 / 224x128 (bf16 output; 128x128 for fp32 output), 16 its 128x128
+# tile with four register staging sets, 1-4 the LDS-dequant kernel that also
+# serves int4), on full, partial-row and partial-column tiles.
+@pytest.mark.parametrize("tile", [10, 11, 12, 13, 14, 15, 16, 1, 2, 3, 4])
 @pytest.mark.parametrize("K,N,M", [(1600, 1600, 512), (1600, 4800, 300), (6400, 1600, 257), (768, 2304, 1024),
                                    (1600, 6400, 4096)])
 def test_gemm_w8_tiles(dev, c_oracle, tile, K, N, M):
@@ -114,9 +114,37 @@ def test_gemm_w8_tile_rejects_unknown_configuration(dev):
     s = torch.ones(64, device=dev)
     y = torch.empty(256, 64, device=dev)
     st = torch.cuda.current_stream().cuda_stream
-    for bad in (-1, 5, 9, 16):
+    for bad in (-1, 5, 9, 17):
         assert L.tiq_gemm_w8_tile(x.data_ptr(), 1, 256, 64, 64, q.data_ptr(), s.data_ptr(), None, 64, y.data_ptr(),
                                   0, 64, bad, st) == -1
+
+
+# The 128x128 tile with four staging sets sums the same products in the same
+# order as the two-set one: bit-identical outputs, fp32 and bf16, with a bias,
+# for k-step counts that leave every remainder of the four-step loop (25, 12,
+# 3, 1, 5 steps), partial tiles, and both fp32-output and bf16-output copies.
+@pytest.mark.parametrize("K,N,M", [(1600, 1600, 256), (768, 2304, 1024), (192, 640, 200), (64, 256, 130),
+                                   (320, 4800, 300)])
+def test_gemm_w8_deep_staging_bit_identical(dev, K, N, M):
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(K + N + M)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    s = torch.rand(N, generator=g, device=dev) * 1e-3 + 1e-4
+    b = torch.randn(N, generator=g, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    for ydt in (torch.float32, torch.bfloat16):
+        ys = []
+        for tile in (12, 16):
+            y = torch.full((M, N), float("nan"), device=dev).to(ydt)
+            rc = L.tiq_gemm_w8_tile(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), b.data_ptr(), N,
+                                    y.data_ptr(), _lib.dtype_code(ydt), N, tile, st)
+            _lib.check(rc, f"tile {tile}")
+            ys.append(y)
+        torch.cuda.synchronize()
+        assert not torch.isnan(ys[0].float()).any()
+        assert torch.equal(ys[0].cpu().view(torch.int16 if ydt == torch.bfloat16 else torch.int32),
+                           ys[1].cpu().view(torch.int16 if ydt == torch.bfloat16 else torch.int32))
 
 
 # fp32 activations through the matrix cores (three exact bf16 planes): the
@@ -468,12 +496,13 @@ def test_gemm_w4_groupwise_prefill(dev, c_oracle, KN, M):
 # Group-wise int4 with bf16 rows and the GEMM workspace: products with few
 # 128 x 128 tiles split over K, whole groups a split, the fp32 slices summed in
 # order (6400x1600 at M = 256: 26 tiles, eight splits of 6-7 groups; group
-# widths of one, three and sixteen k steps; partial tiles). The result is held
+# widths of one, three and sixteen k steps; partial tiles; 128-row tiles for
+# groups of 128 at M = 256 .. 512, 224-row ones at M = 129). The result is held
 # to the oracle's bound, and the bf16 output to the rounding of the fp32 one.
 @pytest.mark.parametrize("K,N,M,group", [(6400, 1600, 256, 128), (1600, 4800, 256, 128), (1600, 1600, 1024, 128),
                                          (6400, 1600, 1024, 128), (1600, 4800, 300, 128), (768, 2304, 129, 128),
                                          (1600, 4800, 300, 64), (1600, 1600, 257, 192),
-                                         (3072, 768, 129, 1024)])
+                                         (3072, 768, 129, 1024), (768, 2304, 512, 128), (1600, 6400, 384, 128)])
 def test_gemm_w4_groupwise_split_k(dev, c_oracle, K, N, M, group):
     L = _lib.lib()
     w, x, b = _inputs(K, N, M, M + group + K, torch.bfloat16)
