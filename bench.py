@@ -611,10 +611,12 @@ def decode_section(dev, repeats=3):
     want = golden["greedy_int8"]["ids"]
     res = {"model": "gpt2 (124M) seed 0, int8 per-channel", "prompt": 64, "new_tokens": 64}
     dec_t = g.GraphDecoder(qm, 1, 128)
-    dec_f = g.FusedDecoder(qm, 1, 128)
+    dec_f = g.FusedDecoder(qm, 1, 128)  # the screened head from the int8 copy
+    dec_b = g.FusedDecoder(qm, 1, 128, head_screen="bf16")
     for label, fn in (("eager", lambda: g.generate(qm, prompt, 64)),
                       ("graph_torch_ops", lambda: g.generate_graph(qm, prompt, 64, decoder=dec_t)),
-                      ("graph_fused", lambda: g.generate_graph(qm, prompt, 64, decoder=dec_f))):
+                      ("graph_fused", lambda: g.generate_graph(qm, prompt, 64, decoder=dec_f)),
+                      ("graph_fused_bf16_screen", lambda: g.generate_graph(qm, prompt, 64, decoder=dec_b))):
         out = fn()
         match = out.cpu().tolist() == want
         ts = []
@@ -626,7 +628,7 @@ def decode_section(dev, repeats=3):
             ts.append(time.perf_counter() - t0)
         med = statistics.median(ts)
         res[label] = {"tokens_per_s": 64 / med, "ms_per_token": 1e3 * med / 64, "tokens_match_reference": match}
-    del dec_t, dec_f, qm
+    del dec_t, dec_f, dec_b, qm
     # the reference's fifth scheme: int8 per-channel + embedding; the tied
     # head (50257 x 768) runs on int8 codes (token parity: the GPU tests
     # against the oracle, no reference fixture holds these tokens)

@@ -519,10 +519,16 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(
 // argmax_partial_kernel: NaN never wins, -inf everywhere gives the first row --
 // and argmax_parts_kernel reduces the workgroups' pairs. The logits buffer
 // holds a_v, and e_v for the recomputed rows.
+// I8: the copy is int8 codes q_v with a per-row scale s_v (half the bytes of
+// the bf16 copy), a_v = s_v (x . q_v) in fp32 and err_v = ||w_v - s_v q_v||_2;
+// the product by s_v is one more rounding, so gamma takes C + 1 for C (the
+// same bound otherwise: x . (s_v q_v) is a dot product of C terms plus one
+// multiplication).
 // Layout: kHsGroups workgroups of kHsWaves wavefronts (two a CU, all resident
-// at once); a wavefront takes the 4-row chunks gw, gw + W, gw + 2 W, ... of the
-// head (gw its index among the W wavefronts), the next chunk's bf16 rows in
-// flight while the current one is summed, so the head streams in one pass.
+// at once); a wavefront takes the chunks gw, gw + W, gw + 2 W, ... of the head
+// (4 rows a chunk, 8 for int8 codes: 64 bytes of a lane's columns either way;
+// gw its index among the W wavefronts), the next chunk's rows in flight while
+// the current one is summed, so the head streams in one pass.
 constexpr int kHsWaves = 8, kHsGroups = 512, kHsChunk = 4, kHsMaxChunks = 8;
 constexpr int kHsMaxCols = 64 * 16;  // a lane holds 16 columns of the row
 
@@ -533,40 +539,53 @@ __device__ __forceinline__ void better_i32(float& v, int& i, float ov, int oi) {
     }
 }
 
+template <bool I8>
 __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4))) void head_screen_kernel(
     const float* __restrict__ x, int C, const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
-    const uint16_t* __restrict__ wb, const float* __restrict__ wf, int64_t ldw, const float* __restrict__ row_coef,
-    int V, float* __restrict__ logits, float* __restrict__ pv, int* __restrict__ pi) {
+    const void* __restrict__ wq, const float* __restrict__ row_scale, const float* __restrict__ wf, int64_t ldw,
+    const float* __restrict__ row_coef, int V, float* __restrict__ logits, float* __restrict__ pv,
+    int* __restrict__ pi) {
+    constexpr int CH = I8 ? 2 * kHsChunk : kHsChunk;  // rows a chunk
+    constexpr int RU = I8 ? 1 : 2;                    // 16-byte loads of a row a lane
     __shared__ float4 xs[64][4];  // the LayerNorm'd row, lane l's 16 columns at xs[l]
     __shared__ float sxn;         // its 2-norm
     __shared__ float lo[kHsWaves];
     __shared__ float bv[kHsWaves];
     __shared__ int bi[kHsWaves];
+    __shared__ int nc[kHsWaves];             // candidates of each wavefront
+    __shared__ int crow[kHsWaves * 64];      // the workgroup's candidate rows, wavefront by wavefront
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int CK = C / 16;
     const bool act = lane < CK;
     const int cl = 16 * min(lane, CK - 1);  // a lane past the row repeats the last chunk, unused
     const int W = gridDim.x * kHsWaves, gw = blockIdx.x * kHsWaves + wave;
-    const int NC = (V + kHsChunk - 1) / kHsChunk;
+    const int NC = (V + CH - 1) / CH;
     const int nch = gw < NC ? (NC - 1 - gw) / W + 1 : 0;  // this wavefront's chunks (<= kHsMaxChunks)
-    auto load = [&](int c, uint4 (&r)[kHsChunk][2]) {  // chunk gw + c W (rows clamped)
-        const int row0 = (gw + c * W) * kHsChunk;
+    auto load = [&](int c, uint4 (&r)[CH][RU]) {  // chunk gw + c W (rows clamped)
+        const int row0 = (gw + c * W) * CH;
 #pragma unroll
-        for (int q = 0; q < kHsChunk; ++q) {
-            const uint16_t* p = wb + (int64_t)min(row0 + q, V - 1) * C + cl;
-            r[q][0] = *reinterpret_cast<const uint4*>(p);
-            r[q][1] = *reinterpret_cast<const uint4*>(p + 8);
+        for (int q = 0; q < CH; ++q) {
+            if constexpr (I8) {
+                const int8_t* p = static_cast<const int8_t*>(wq) + (int64_t)min(row0 + q, V - 1) * C + cl;
+                r[q][0] = *reinterpret_cast<const uint4*>(p);
+            } else {
+                const uint16_t* p = static_cast<const uint16_t*>(wq) + (int64_t)min(row0 + q, V - 1) * C + cl;
+                r[q][0] = *reinterpret_cast<const uint4*>(p);
+                r[q][1] = *reinterpret_cast<const uint4*>(p + 8);
+            }
         }
     };
-    uint4 buf[2][kHsChunk][2];
+    uint4 buf[2][CH][RU];
     if (nch > 0) load(0, buf[0]);
     if (nch > 1) load(1, buf[1]);
-    // lane q + 4 c holds row q of chunk c: its bound's inputs requested now
-    const int lc = lane / kHsChunk, lq = lane % kHsChunk;
-    const int my_row = (gw + lc * W) * kHsChunk + lq;
+    // lane q + 4 c (int8 copy: 8 q + c) holds row q of chunk c: its bound's
+    // inputs requested now
+    const int lc = I8 ? (lane & 7) : lane / CH, lq = I8 ? (lane >> 3) : lane % CH;
+    const int my_row = (gw + lc * W) * CH + lq;
     const bool mine = lc < nch && my_row < V;
     const int nl = mine ? my_row : 0;
     const float k_l = row_coef[nl];
+    const float s_l = I8 ? row_scale[nl] : 1.f;
     if (wave == 0) {  // LayerNorm (two-pass mean and biased variance, as torch) into LDS
         float v[16], g[16], bb[16];
 #pragma unroll
@@ -602,28 +621,62 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
     for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(xl + 4 * q) = xs[act ? lane : 0][q];
     // ||x|| with its own rounding covered (a relative 2^-10 is far above it)
     const float xn = sxn * (1.0f + 0x1p-10f);
-    // a_v of this wavefront's rows, lane q + 4 c taking row q of chunk c
+    // a_v of this wavefront's rows: the bf16 copy sums each row over the
+    // wavefront in turn; the int8 copy, with twice the rows a chunk, sums the
+    // chunk's 8 rows at once (halving the rows a lane carries at each of the
+    // first three exchanges, then three on one value), after which lane 8 q + c
+    // holds row q of chunk c
     float a_l = 0.f;
 #pragma unroll
     for (int c = 0; c < kHsMaxChunks; ++c) {
         if (c < nch) {  // uniform across the wavefront
-            const uint4 (&r)[kHsChunk][2] = buf[c & 1];
+            const uint4 (&r)[CH][RU] = buf[c & 1];
+            float sv[CH];
 #pragma unroll
-            for (int q = 0; q < kHsChunk; ++q) {
-                const uint32_t w32[8] = {r[q][0].x, r[q][0].y, r[q][0].z, r[q][0].w,
-                                         r[q][1].x, r[q][1].y, r[q][1].z, r[q][1].w};
+            for (int q = 0; q < CH; ++q) {
                 float s = 0.f;
+                if constexpr (I8) {
+                    const uint32_t w32[4] = {r[q][0].x, r[q][0].y, r[q][0].z, r[q][0].w};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    s = fmaf(bf_lo(w32[j]), xl[2 * j], s);
-                    s = fmaf(bf_hi(w32[j]), xl[2 * j + 1], s);
+                    for (int j = 0; j < 4; ++j) {
+                        s = fmaf(sbyte_f32<0>(w32[j]), xl[4 * j], s);
+                        s = fmaf(sbyte_f32<1>(w32[j]), xl[4 * j + 1], s);
+                        s = fmaf(sbyte_f32<2>(w32[j]), xl[4 * j + 2], s);
+                        s = fmaf(sbyte_f32<3>(w32[j]), xl[4 * j + 3], s);
+                    }
+                } else {
+                    const uint32_t w32[8] = {r[q][0].x, r[q][0].y, r[q][0].z, r[q][0].w,
+                                             r[q][RU - 1].x, r[q][RU - 1].y, r[q][RU - 1].z, r[q][RU - 1].w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        s = fmaf(bf_lo(w32[j]), xl[2 * j], s);
+                        s = fmaf(bf_hi(w32[j]), xl[2 * j + 1], s);
+                    }
                 }
-                const float a = wave_sum_dpp(act ? s : 0.f);
-                a_l = lane == q + kHsChunk * c ? a : a_l;
+                if constexpr (I8) {
+                    sv[q] = act ? s : 0.f;
+                } else {
+                    const float a = wave_sum_dpp(act ? s : 0.f);
+                    a_l = lane == q + CH * c ? a : a_l;
+                }
+            }
+            if constexpr (I8) {
+                float t4[4], t2[2];
+                const bool u5 = lane & 32, u4 = lane & 16, u3 = lane & 8;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) t4[j] = (u5 ? sv[4 + j] : sv[j]) + __shfl_xor(u5 ? sv[j] : sv[4 + j], 32, 64);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) t2[j] = (u4 ? t4[2 + j] : t4[j]) + __shfl_xor(u4 ? t4[j] : t4[2 + j], 16, 64);
+                float t1 = (u3 ? t2[1] : t2[0]) + __shfl_xor(u3 ? t2[0] : t2[1], 8, 64);
+                t1 += __shfl_xor(t1, 4, 64);
+                t1 += __shfl_xor(t1, 2, 64);
+                t1 += __shfl_xor(t1, 1, 64);
+                a_l = (lane & 7) == c ? t1 : a_l;
             }
             if (c + 2 < nch) load(c + 2, buf[c & 1]);  // its registers are free now
         }
     }
+    if constexpr (I8) a_l *= s_l;  // x . q_v scaled: one rounding, inside gamma_(C + 1)
     const float b_l = xn * k_l * (1.0f + 0x1p-10f);
     const float hi_l = a_l + b_l;
     if (mine) logits[my_row] = a_l;
@@ -636,11 +689,11 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
     // the candidates of this wavefront, recomputed from the fp32 rows
     float best = -INFINITY;
     int bidx = INT32_MAX;
-    uint64_t cand = __ballot(mine && hi_l >= L);  // lane q + 4 c: row q of chunk c
+    uint64_t cand = __ballot(mine && hi_l >= L);
     while (cand) {
         const int l = __builtin_ctzll(cand);
         cand &= cand - 1;
-        const int n = (gw + (l / kHsChunk) * W) * kHsChunk + l % kHsChunk;
+        const int n = I8 ? (gw + (l & 7) * W) * CH + (l >> 3) : (gw + (l / CH) * W) * CH + l % CH;
         const float* p = wf + (int64_t)n * ldw + cl;
         float s = 0.f;
 #pragma unroll
@@ -663,7 +716,7 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
     if (tid == 0) {
         // no row above -inf: the group's first row, as argmax_partial_kernel
         float v = -INFINITY;
-        int i = gw < NC ? gw * kHsChunk : INT32_MAX;
+        int i = gw < NC ? gw * CH : INT32_MAX;
 #pragma unroll
         for (int w = 0; w < kHsWaves; ++w) better_i32(v, i, bv[w], bi[w]);
         pv[blockIdx.x] = v;
@@ -740,6 +793,56 @@ __global__ __launch_bounds__(256) void head_screen_prepare_kernel(const float* _
         const double sn = (red[1][0] + red[1][1] + red[1][2] + red[1][3]) * (1.0 + (C + 4) * 0x1p-52);
         const double err = sqrt(se) * (1.0 + 0x1p-50), nrm = sqrt(sn) * (1.0 + 0x1p-50);
         const double cu = (double)C * 0x1p-24, gamma = cu / (1.0 - cu);
+        row_coef[n] = f32_round_up((err + gamma * (2.0 * nrm + err)) * (1.0 + 0x1p-50));
+    }
+}
+
+// int8 copy of the head for the screen: per row s = max|w| / 127 (0 for a zero
+// row), q = rint(w / s) clamped to +-127 (any codes serve: the bound uses their
+// actual error), and the coefficient err + gamma_(C + 1) (2 norm + err) from
+// the fp64 2-norms of w - s q and of w, rounded up to fp32. A row holding NaN
+// gets a NaN coefficient, so it is never a candidate (as in the bf16 copy).
+__global__ __launch_bounds__(256) void head_screen_prepare_i8_kernel(const float* __restrict__ w, int C, int64_t ldw,
+                                                                     int8_t* __restrict__ wq,
+                                                                     float* __restrict__ row_scale,
+                                                                     float* __restrict__ row_coef) {
+    __shared__ double red[2][4];
+    __shared__ float mx[4];
+    const int64_t n = blockIdx.x;
+    const int tid = threadIdx.x;
+    float m = 0.f;
+    for (int c = tid; c < C; c += 256) m = fmaxf(m, fabsf(w[n * ldw + c]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) mx[tid >> 6] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    const float sc = amax / 127.f;
+    double e2 = 0.0, n2 = 0.0;
+    for (int c = tid; c < C; c += 256) {
+        const float v = w[n * ldw + c];
+        const float qf = sc > 0.f ? fminf(fmaxf(rintf(v / sc), -127.f), 127.f) : 0.f;
+        wq[n * C + c] = (int8_t)(int)qf;
+        const double d = (double)v - (double)qf * (double)sc;
+        e2 += d * d;
+        n2 += (double)v * (double)v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        e2 += __shfl_xor(e2, off, 64);
+        n2 += __shfl_xor(n2, off, 64);
+    }
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = e2;
+        red[1][tid >> 6] = n2;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const double se = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) * (1.0 + (C + 4) * 0x1p-52);
+        const double sn = (red[1][0] + red[1][1] + red[1][2] + red[1][3]) * (1.0 + (C + 4) * 0x1p-52);
+        const double err = sqrt(se) * (1.0 + 0x1p-50), nrm = sqrt(sn) * (1.0 + 0x1p-50);
+        const double cu = (double)(C + 1) * 0x1p-24, gamma = cu / (1.0 - cu);
+        row_scale[n] = sc;
         row_coef[n] = f32_round_up((err + gamma * (2.0 * nrm + err)) * (1.0 + 0x1p-50));
     }
 }
@@ -917,19 +1020,30 @@ extern "C" int tiq_head_screen_prepare(const float* w, int64_t vocab, int64_t n_
     return launch_status();
 }
 
-extern "C" int tiq_head_argmax_screened(const float* x, int64_t n_embd, const float* ln_w, const float* ln_b,
-                                        float ln_eps, const uint16_t* w_bf16, const float* w, int64_t ldw,
-                                        const float* row_coef, int64_t vocab, float* logits, int64_t* out,
-                                        int64_t* ids, int64_t ld_ids, int64_t* pos, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+extern "C" int tiq_head_screen_prepare_i8(const float* w, int64_t vocab, int64_t n_embd, int64_t ldw, int8_t* w_i8,
+                                          float* row_scale, float* row_coef, void* stream) {
     if (vocab <= 0 || n_embd <= 0 || ldw < n_embd) return TIQ_EINVAL;
-    if (!x || !ln_w || !ln_b || !w_bf16 || !w || !row_coef || !logits || !out || (ids && !pos))
+    if (!w || !w_i8 || !row_scale || !row_coef) return TIQ_EINVAL;
+    if (vocab > INT32_MAX || n_embd > INT32_MAX) return TIQ_EUNSUPPORTED;
+    hipLaunchKernelGGL(head_screen_prepare_i8_kernel, dim3((unsigned)vocab), dim3(256), 0, as_stream(stream), w,
+                       (int)n_embd, ldw, w_i8, row_scale, row_coef);
+    return launch_status();
+}
+
+static int head_argmax_screened(bool i8, const float* x, int64_t n_embd, const float* ln_w, const float* ln_b,
+                                float ln_eps, const void* wq, const float* row_scale, const float* w, int64_t ldw,
+                                const float* row_coef, int64_t vocab, float* logits, int64_t* out, int64_t* ids,
+                                int64_t ld_ids, int64_t* pos, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+    if (vocab <= 0 || n_embd <= 0 || ldw < n_embd) return TIQ_EINVAL;
+    if (!x || !ln_w || !ln_b || !wq || (i8 && !row_scale) || !w || !row_coef || !logits || !out || (ids && !pos))
         return TIQ_EINVAL;
     if (!workspace) return TIQ_EINVAL;
-    // every wavefront's chunks in its registers' reach (GPT-2's 50257 rows: 4 chunks a wavefront)
-    if (n_embd % 16 != 0 || n_embd > kHsMaxCols || vocab > (int64_t)kHsMaxChunks * kHsChunk * kHsGroups * kHsWaves)
-        return TIQ_EUNSUPPORTED;
-    if (!aligned(x, 16) || !aligned(ln_w, 16) || !aligned(ln_b, 16) || !aligned(w_bf16, 16) || !aligned(w, 16) ||
+    // every wavefront's chunks in its registers' reach (GPT-2's 50257 rows: 4 chunks of 4 bf16 rows or 2 of 8
+    // int8 rows a wavefront)
+    const int64_t rows_max = (int64_t)kHsMaxChunks * (i8 ? 2 * kHsChunk : kHsChunk) * kHsGroups * kHsWaves;
+    if (n_embd % 16 != 0 || n_embd > kHsMaxCols || vocab > rows_max) return TIQ_EUNSUPPORTED;
+    if (!aligned(x, 16) || !aligned(ln_w, 16) || !aligned(ln_b, 16) || !aligned(wq, 16) || !aligned(w, 16) ||
         ldw % 4 != 0)
         return TIQ_EALIGN;
     if (workspace_bytes < tiq_head_screen_workspace(vocab)) return TIQ_EWORKSPACE;
@@ -938,12 +1052,34 @@ extern "C" int tiq_head_argmax_screened(const float* x, int64_t n_embd, const fl
     float* pv = static_cast<float*>(workspace);
     int* pi = reinterpret_cast<int*>(pv + P);
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(head_screen_kernel, dim3((unsigned)P), dim3(64 * kHsWaves), 0, st, x, (int)n_embd, ln_w, ln_b,
-                       ln_eps, w_bf16, w, ldw, row_coef, (int)vocab, logits, pv, pi);
+    if (i8)
+        hipLaunchKernelGGL(head_screen_kernel<true>, dim3((unsigned)P), dim3(64 * kHsWaves), 0, st, x, (int)n_embd,
+                           ln_w, ln_b, ln_eps, wq, row_scale, w, ldw, row_coef, (int)vocab, logits, pv, pi);
+    else
+        hipLaunchKernelGGL(head_screen_kernel<false>, dim3((unsigned)P), dim3(64 * kHsWaves), 0, st, x, (int)n_embd,
+                           ln_w, ln_b, ln_eps, wq, nullptr, w, ldw, row_coef, (int)vocab, logits, pv, pi);
     int rc = launch_status();
     if (rc) return rc;
     hipLaunchKernelGGL(argmax_parts_kernel, dim3(1), dim3(1024), 0, st, pv, pi, (int)P, out, ids, ld_ids, pos);
     return launch_status();
+}
+
+extern "C" int tiq_head_argmax_screened(const float* x, int64_t n_embd, const float* ln_w, const float* ln_b,
+                                        float ln_eps, const uint16_t* w_bf16, const float* w, int64_t ldw,
+                                        const float* row_coef, int64_t vocab, float* logits, int64_t* out,
+                                        int64_t* ids, int64_t ld_ids, int64_t* pos, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    return head_argmax_screened(false, x, n_embd, ln_w, ln_b, ln_eps, w_bf16, nullptr, w, ldw, row_coef, vocab,
+                                logits, out, ids, ld_ids, pos, workspace, workspace_bytes, stream);
+}
+
+extern "C" int tiq_head_argmax_screened_i8(const float* x, int64_t n_embd, const float* ln_w, const float* ln_b,
+                                           float ln_eps, const int8_t* w_i8, const float* row_scale, const float* w,
+                                           int64_t ldw, const float* row_coef, int64_t vocab, float* logits,
+                                           int64_t* out, int64_t* ids, int64_t ld_ids, int64_t* pos,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+    return head_argmax_screened(true, x, n_embd, ln_w, ln_b, ln_eps, w_i8, row_scale, w, ldw, row_coef, vocab,
+                                logits, out, ids, ld_ids, pos, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t tiq_argmax_rows_workspace(int64_t rows) {

@@ -81,6 +81,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tiq_head_screen_prepare": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp], _i32),
     "tiq_head_argmax_screened": ([_vp, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
                                   _vp, _sz, _vp], _i32),
+    "tiq_head_screen_prepare_i8": ([_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp], _i32),
+    "tiq_head_argmax_screened_i8": ([_vp, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
+                                     _vp, _vp, _sz, _vp], _i32),
 }
 
 WF_INT8, WF_INT4, WF_INT4G, WF_F32, WF_INT8_TILED, WF_F32_TILED = 0, 1, 2, 3, 4, 5

@@ -202,9 +202,16 @@ def _layer_norm(ln, x: torch.Tensor) -> torch.Tensor:
 
 
 class FusedDecoder(_DecoderBase):
-    """Decode step built from the library's fused decode kernels."""
+    """Decode step built from the library's fused decode kernels.
 
-    def __init__(self, model, batch: int, max_len: int) -> None:
+    ``head_screen`` (one sequence with the tied fp32 head): the copy of the head
+    its screened argmax reads, ``"int8"`` (per-row int8 codes and scales, 1 byte
+    a weight) or ``"bf16"`` (2 bytes a weight); either gives the argmax of the
+    fp32 logits."""
+
+    def __init__(self, model, batch: int, max_len: int, head_screen: str = "int8") -> None:
+        if head_screen not in ("int8", "bf16"):
+            raise ValueError(f"head_screen must be 'int8' or 'bf16', got {head_screen!r}")
         why = fused_supported(model)
         if why is not None:
             raise ValueError(f"fused decode unavailable: {why}")
@@ -241,20 +248,30 @@ class FusedDecoder(_DecoderBase):
         self.chain = 5 <= B <= 64 and head_ok and all(l.fmt == FMT_W8 for l in lins)
         self.rows_prefill = all(l.fmt == FMT_W8 for l in lins)
         # One sequence with the tied fp32 head: the decode step's head and
-        # argmax read a bf16 copy of the head and recompute from the fp32
-        # rows only those whose certified bound reaches the best of their
-        # group (tiq_head_argmax_screened): the argmax of the fp32 logits
+        # argmax read an int8 (or bf16) copy of the head and recompute from
+        # the fp32 rows only those whose certified bound reaches the best of
+        # their group (tiq_head_argmax_screened_i8 / tiq_head_argmax_screened):
+        # the argmax of the fp32 logits
         self.screen = (B == 1 and self.head_q is None and C % 16 == 0 and C <= 1024)
+        self.screen_i8 = head_screen == "int8"
         if self.screen:
             V, L = cfg.vocab_size, self.L
             st = torch.cuda.current_stream(dev).cuda_stream
-            self.head_bf16 = torch.empty(V, C, dtype=torch.int16, device=dev)  # bf16 bits
-            self.head_coef = torch.empty(V, device=dev)                          # bound coefficient a row
+            self.head_coef = torch.empty(V, device=dev)  # bound coefficient a row
             n = int(L.tiq_head_screen_workspace(V))
             self.screen_ws = torch.empty(n, dtype=torch.uint8, device=dev)
-            _lib.check(L.tiq_head_screen_prepare(self.head_w.data_ptr(), V, C, self.head_w.stride(0),
-                                                 self.head_bf16.data_ptr(), self.head_coef.data_ptr(), st),
-                       "head screen prepare")
+            if self.screen_i8:
+                self.head_copy = torch.empty(V, C, dtype=torch.int8, device=dev)
+                self.head_scale = torch.empty(V, device=dev)
+                _lib.check(L.tiq_head_screen_prepare_i8(self.head_w.data_ptr(), V, C, self.head_w.stride(0),
+                                                        self.head_copy.data_ptr(), self.head_scale.data_ptr(),
+                                                        self.head_coef.data_ptr(), st), "head screen prepare")
+            else:
+                self.head_copy = torch.empty(V, C, dtype=torch.int16, device=dev)  # bf16 bits
+                self.head_scale = None
+                _lib.check(L.tiq_head_screen_prepare(self.head_w.data_ptr(), V, C, self.head_w.stride(0),
+                                                     self.head_copy.data_ptr(), self.head_coef.data_ptr(), st),
+                           "head screen prepare")
         if self.chain:
             L = self.L
             head_wf = _lib.WF_F32 if self.head_q is None else _lib.WF_INT8
@@ -301,9 +318,12 @@ class FusedDecoder(_DecoderBase):
         """Device bytes of the weight copies this decoder holds beyond the
         model's own (the batched step's operand tiles of the int8 block codes
         and of the fp32 tied head; for one sequence with the fp32 tied head
-        its bf16 copy and one float a row for the screened argmax; 0 for two
-        to four sequences, which read the model's row-major codes)."""
-        extra = [self.head_bf16, self.head_coef] if getattr(self, "screen", False) else []
+        its int8 copy and two floats a row, or its bf16 copy and one float a
+        row, for the screened argmax; 0 for two to four sequences, which read
+        the model's row-major codes)."""
+        extra = []
+        if getattr(self, "screen", False):
+            extra = [t for t in (self.head_copy, self.head_scale, self.head_coef) if t is not None]
         return sum(t.numel() * t.element_size() for t in [*getattr(self, "tiles", {}).values(), *extra])
 
     def _linear(self, lin: QuantLinear, x: torch.Tensor, y: torch.Tensor, ln=None, act: int = 0, res=None) -> None:
@@ -497,10 +517,18 @@ class FusedDecoder(_DecoderBase):
             self._linear(mlp.c_fc, self.x, self.hid, ln=block.ln_2, act=_lib.ACT_GELU_TANH)
             self._linear(mlp.c_proj, self.hid, self.x, res=self.x)
         ln = m.ln_f
-        if self.screen:  # head + argmax, which also records the token and advances pos
+        if self.screen and self.screen_i8:  # head + argmax, which also records the token and advances pos
+            _lib.check(L.tiq_head_argmax_screened_i8(
+                self.x.data_ptr(), C, ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps),
+                self.head_copy.data_ptr(), self.head_scale.data_ptr(), self.head_w.data_ptr(), self.head_w.stride(0),
+                self.head_coef.data_ptr(), cfg.vocab_size, self.logits.data_ptr(), self.tok_flat.data_ptr(),
+                self.out.data_ptr(), self.T, self.pos.data_ptr(), self.screen_ws.data_ptr(), self.screen_ws.numel(),
+                st), "screened head")
+            return
+        if self.screen:
             _lib.check(L.tiq_head_argmax_screened(
                 self.x.data_ptr(), C, ln.weight.data_ptr(), ln.bias.data_ptr(), float(ln.eps),
-                self.head_bf16.data_ptr(), self.head_w.data_ptr(), self.head_w.stride(0), self.head_coef.data_ptr(),
+                self.head_copy.data_ptr(), self.head_w.data_ptr(), self.head_w.stride(0), self.head_coef.data_ptr(),
                 cfg.vocab_size, self.logits.data_ptr(), self.tok_flat.data_ptr(),
                 self.out.data_ptr(), self.T, self.pos.data_ptr(), self.screen_ws.data_ptr(), self.screen_ws.numel(),
                 st), "screened head")

@@ -513,6 +513,21 @@ int tiq_head_argmax_screened(const float* x, int64_t n_embd, const float* ln_w, 
                              const uint16_t* w_bf16, const float* w, int64_t ldw, const float* row_coef,
                              int64_t vocab, float* logits, int64_t* out, int64_t* ids, int64_t ld_ids, int64_t* pos,
                              void* workspace, size_t workspace_bytes, void* stream);
+/* The same screen from an int8 copy of the head (half the bytes of the bf16
+ * copy): w_i8 = rint(w / s) clamped to +-127 with s = row_scale[v] = max|w_v| /
+ * 127, each row's estimate s (x . q_v) in fp32, err = ||w_v - s q_v||_2 and
+ * gamma = (C + 1) 2^-24 / (1 - (C + 1) 2^-24) (the product by s is one more
+ * rounding); vocab <= 262144, the rest as tiq_head_argmax_screened, and the
+ * token the argmax of the fp32 logits all the same. The extra device bytes are
+ * the int8 copy (1 byte a weight) and two floats a row, from
+ * tiq_head_screen_prepare_i8. No counterpart in the reference beyond the head
+ * and argmax it replaces. */
+int tiq_head_screen_prepare_i8(const float* w, int64_t vocab, int64_t n_embd, int64_t ldw, int8_t* w_i8,
+                               float* row_scale, float* row_coef, void* stream);
+int tiq_head_argmax_screened_i8(const float* x, int64_t n_embd, const float* ln_w, const float* ln_b, float ln_eps,
+                                const int8_t* w_i8, const float* row_scale, const float* w, int64_t ldw,
+                                const float* row_coef, int64_t vocab, float* logits, int64_t* out, int64_t* ids,
+                                int64_t ld_ids, int64_t* pos, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

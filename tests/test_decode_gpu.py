@@ -156,12 +156,17 @@ def test_graph_decode_matches_reference_tiny(reference_decode, dev, bits):
     assert eager.cpu().tolist() == [r[: prompt.size(1) + 5] for r in gr["ids"]]
 
 
-def test_graph_decode_matches_reference_gpt2_small(reference_decode, dev):
+@pytest.mark.parametrize("head_screen", ["int8", "bf16"])
+def test_graph_decode_matches_reference_gpt2_small(reference_decode, dev, head_screen):
+    """The captured fused decode (one sequence: the screened tied head from
+    its int8 or its bf16 copy) gives the reference's 64 + 64 tokens."""
     e = reference_decode["gpt2_small"]
     qm, _ = g.quantize_model(_model(e["config"], dev), 8)
     gr = e["greedy_int8"]
     prompt = OM.benchmark_prompt(e["config"]["vocab_size"], *gr["prompt_shape"]).to(dev)
-    out = g.generate_graph(qm, prompt, gr["new_tokens"])
+    dec = g.FusedDecoder(qm, prompt.size(0), prompt.size(1) + gr["new_tokens"], head_screen=head_screen)
+    assert dec.screen and dec.screen_i8 == (head_screen == "int8")
+    out = g.generate_graph(qm, prompt, gr["new_tokens"], decoder=dec)
     assert out.cpu().tolist() == gr["ids"]
 
 
