@@ -381,7 +381,7 @@ bool gemm_supported(const LinearArgs& a) {
 
 int launch_gemm_tile(const LinearArgs& a, int tile) {
     if (!gemm_supported(a)) return TIQ_EUNSUPPORTED;
-    if (tile < 0 || (tile > 4 && (tile < 10 || tile > 16))) return TIQ_EINVAL;
+    if (tile < 0 || (tile > 4 && (tile < 10 || tile > 17))) return TIQ_EINVAL;
     if (a.fmt == kW8) return dispatch_gemm<kW8>(a, tile);
     if (a.fmt == kW4G) return dispatch_gemm<kW4G>(a, tile);
     return dispatch_gemm<kW4>(a, tile);

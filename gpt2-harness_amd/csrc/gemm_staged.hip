@@ -158,6 +158,7 @@ int dispatch_staged_bf16(const LinearArgs& a, int choice) {
         case 4: return run_staged<160, 256, 1, FMT, uint16_t>(a);
         case 5: return run_staged<224, 128, 1, FMT, uint16_t>(a);
         case 6: return run_staged<128, 128, 2, FMT, uint16_t, 4>(a);
+        case 7: return run_staged<128, 128, 1, FMT, uint16_t>(a);
         default: return run_staged<128, 128, 2, FMT, uint16_t>(a);
     }
 }
@@ -165,14 +166,20 @@ int dispatch_staged_bf16(const LinearArgs& a, int choice) {
 
 bool staged_gemm_supported(const LinearArgs& a) { return staged_supported_impl(a); }
 
-// 128 x 128 tiles that all fit on the CUs at once (one a CU) take the copy with
-// four staging sets: the loads of a stage go out three k64 steps before they
-// are needed (GPT-2-XL shapes at M = 256 / 1024: 7-9% faster, bit-identical);
-// with more tiles two workgroups share a CU, which the deeper copy's registers
-// do not allow.
+// 128 x 128 tiles that all fit on the CUs at once (one a CU): with bf16
+// output and at most 32 k64 steps, the wavefronts side by side along N (each
+// loads its own weight rows into registers, only activations pass through
+// LDS): GPT-2-XL shapes with K = 1600, M = 256 .. 2048, 7-22% faster than the
+// 2 x 2 and 224-row tiles, bit-identical; else the 2 x 2 copy with four
+// staging sets, whose loads go out three k64 steps before they are needed
+// (7-9% faster than two sets; at K = 6400 also ahead of the side-by-side
+// tile, 53 against 59 us). With more tiles the cost model's choice stands
+// (e.g. M = 1024, N = 4800: 224 x 128 tiles, 24.0 against 24.7 us).
 int staged_gemm_choice(const LinearArgs& a) {
+    const bool one_round = ((a.M + 127) / 128) * ((a.N + 127) / 128) <= 256;
+    if (one_round && a.y_dtype == TIQ_BF16 && a.K / BK <= 32) return 7;
     const int c = staged_choice(a.M, a.N, a.K, a.y_dtype == TIQ_BF16);
-    return c == 2 && ((a.M + 127) / 128) * ((a.N + 127) / 128) <= 256 ? 6 : c;
+    return c == 2 && one_round ? 6 : c;
 }
 
 int launch_staged_gemm(const LinearArgs& a, int choice) {

@@ -72,7 +72,7 @@ int launch_gemm(const LinearArgs& a);
 // The GEMM with a given tile configuration: 0 automatic, 1-4 the LDS-dequant
 // kernel's tiles (gemm.hip), 10-16 the staged int8 kernel's (256x256, 256x128,
 // 128x128; with bf16 output 224x256, 160x256, 224x128; 128x128 with four
-// staging sets).
+// staging sets; with bf16 output 128x128 with the wavefronts along N).
 int launch_gemm_tile(const LinearArgs& a, int tile);
 // True when the MFMA GEMM has a kernel for these arguments.
 bool gemm_supported(const LinearArgs& a);

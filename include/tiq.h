@@ -204,7 +204,8 @@ int tiq_gemm_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
  * register-staged kernel at 256x256 / 256x128 / 128x128 tiles and, with bf16
  * output, 224x256 / 160x256 / 224x128 (128x128 with fp32 output; falls back
  * to the automatic tile when that kernel does not take the shape), 16 = its
- * 128x128 tile with four register staging sets. No
+ * 128x128 tile with four register staging sets, 17 = 128x128 with the
+ * wavefronts side by side along N (bf16 output; else as 12). No
  * counterpart in the reference (same interface as tiq_gemm_w8); the product
  * path never calls it. */
 int tiq_gemm_w8_tile(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,

@@ -98,9 +98,10 @@ def test_gemm_w8_small_shapes(dev, c_oracle, KN, M):
 # register-staged int8 kernel at 256x256 / 256x128 / 128x128 tiles, 13/14/15
 # the same kernel with its wavefronts side by side along N at 224x256 /
 # 160x256 / 224x128 (bf16 output; 128x128 for fp32 output), 16 its 128x128
-# tile with four register staging sets, 1-4 the LDS-dequant kernel that also
-# serves int4), on full, partial-row and partial-column tiles.
-@pytest.mark.parametrize("tile", [10, 11, 12, 13, 14, 15, 16, 1, 2, 3, 4])
+# tile with four register staging sets, 17 128x128 side by side along N (bf16
+# output), 1-4 the LDS-dequant kernel that also serves int4), on full,
+# partial-row and partial-column tiles.
+@pytest.mark.parametrize("tile", [10, 11, 12, 13, 14, 15, 16, 17, 1, 2, 3, 4])
 @pytest.mark.parametrize("K,N,M", [(1600, 1600, 512), (1600, 4800, 300), (6400, 1600, 257), (768, 2304, 1024),
                                    (1600, 6400, 4096)])
 def test_gemm_w8_tiles(dev, c_oracle, tile, K, N, M):
@@ -114,13 +115,14 @@ def test_gemm_w8_tile_rejects_unknown_configuration(dev):
     s = torch.ones(64, device=dev)
     y = torch.empty(256, 64, device=dev)
     st = torch.cuda.current_stream().cuda_stream
-    for bad in (-1, 5, 9, 17):
+    for bad in (-1, 5, 9, 18):
         assert L.tiq_gemm_w8_tile(x.data_ptr(), 1, 256, 64, 64, q.data_ptr(), s.data_ptr(), None, 64, y.data_ptr(),
                                   0, 64, bad, st) == -1
 
 
-# The 128x128 tile with four staging sets sums the same products in the same
-# order as the two-set one: bit-identical outputs, fp32 and bf16, with a bias,
+# The 128x128 tile with four staging sets, and the one with its wavefronts
+# side by side along N (bf16 output), sum the same products in the same order
+# as the two-set 2 x 2 one: bit-identical outputs, fp32 and bf16, with a bias,
 # for k-step counts that leave every remainder of the four-step loop (25, 12,
 # 3, 1, 5 steps), partial tiles, and both fp32-output and bf16-output copies.
 @pytest.mark.parametrize("K,N,M", [(1600, 1600, 256), (768, 2304, 1024), (192, 640, 200), (64, 256, 130),
@@ -135,7 +137,7 @@ def test_gemm_w8_deep_staging_bit_identical(dev, K, N, M):
     st = torch.cuda.current_stream().cuda_stream
     for ydt in (torch.float32, torch.bfloat16):
         ys = []
-        for tile in (12, 16):
+        for tile in (12, 16, 17):
             y = torch.full((M, N), float("nan"), device=dev).to(ydt)
             rc = L.tiq_gemm_w8_tile(x.data_ptr(), 1, M, K, K, q.data_ptr(), s.data_ptr(), b.data_ptr(), N,
                                     y.data_ptr(), _lib.dtype_code(ydt), N, tile, st)
@@ -143,8 +145,9 @@ def test_gemm_w8_deep_staging_bit_identical(dev, K, N, M):
             ys.append(y)
         torch.cuda.synchronize()
         assert not torch.isnan(ys[0].float()).any()
-        assert torch.equal(ys[0].cpu().view(torch.int16 if ydt == torch.bfloat16 else torch.int32),
-                           ys[1].cpu().view(torch.int16 if ydt == torch.bfloat16 else torch.int32))
+        iv = torch.int16 if ydt == torch.bfloat16 else torch.int32
+        assert torch.equal(ys[0].cpu().view(iv), ys[1].cpu().view(iv))
+        assert torch.equal(ys[0].cpu().view(iv), ys[2].cpu().view(iv))
 
 
 # fp32 activations through the matrix cores (three exact bf16 planes): the
