@@ -190,10 +190,11 @@ int launch_staged_gemm(const LinearArgs& a, int choice) {
 
 int launch_staged_gemm_split(const LinearArgs& a, void* ws, size_t ws_bytes) {
     if ((a.fmt != kW8 && a.fmt != kW4) || !staged_supported_impl(a)) return TIQ_EUNSUPPORTED;
-    // a quarter of the CUs or more with tiles and a short K: the slices' trip
-    // through memory costs more than the idle CUs (GPT-2-XL at M = 256 with
-    // N >= 4800 and at M = 1024 with N = K = 1600: 7-11% slower split)
-    if (((a.M + 127) / 128) * ((a.N + 127) / 128) >= 64 && a.K / BK <= 32) return TIQ_EUNSUPPORTED;
+    // 48 tiles or more and a short K: the slices' trip through memory costs
+    // more than the idle CUs (GPT-2-XL at M = 256 with N >= 4800 and at
+    // M = 1024 with N = K = 1600: 7-11% slower split; M = 512, N = K = 1600,
+    // 52 tiles: 18.7 split against 16.9 us on the side-by-side 128 x 128 tile)
+    if (((a.M + 127) / 128) * ((a.N + 127) / 128) >= 48 && a.K / BK <= 32) return TIQ_EUNSUPPORTED;
     const int64_t S = staged_splits(a.M, a.N, a.K);
     const size_t need = staged_split_workspace(a.M, a.N, a.K);
     if (S <= 1 || !ws || ws_bytes < need || !aligned(ws, 16)) return TIQ_EUNSUPPORTED;
