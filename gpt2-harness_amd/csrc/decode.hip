@@ -539,7 +539,9 @@ __device__ __forceinline__ void better_i32(float& v, int& i, float ov, int oi) {
     }
 }
 
-template <bool I8>
+// P: columns a lane (16; 12 for the int8 copy at 768 columns, so that all 64
+// lanes work instead of 48).
+template <bool I8, int P = 16>
 __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4))) void head_screen_kernel(
     const float* __restrict__ x, int C, const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
     const void* __restrict__ wq, const float* __restrict__ row_scale, const float* __restrict__ wf, int64_t ldw,
@@ -547,7 +549,8 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
     int* __restrict__ pi) {
     constexpr int CH = I8 ? 2 * kHsChunk : kHsChunk;  // rows a chunk
     constexpr int RU = I8 ? 1 : 2;                    // 16-byte loads of a row a lane
-    __shared__ float4 xs[64][4];  // the LayerNorm'd row, lane l's 16 columns at xs[l]
+    static_assert(P == 16 || (P == 12 && I8), "16 columns a lane, or 12 from the int8 copy");
+    __shared__ float4 xs[64][P / 4];  // the LayerNorm'd row, lane l's P columns at xs[l]
     __shared__ float sxn;         // its 2-norm
     __shared__ float lo[kHsWaves];
     __shared__ float bv[kHsWaves];
@@ -555,9 +558,9 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
     __shared__ int nc[kHsWaves];             // candidates of each wavefront
     __shared__ int crow[kHsWaves * 64];      // the workgroup's candidate rows, wavefront by wavefront
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int CK = C / 16;
+    const int CK = C / P;
     const bool act = lane < CK;
-    const int cl = 16 * min(lane, CK - 1);  // a lane past the row repeats the last chunk, unused
+    const int cl = P * min(lane, CK - 1);  // a lane past the row repeats the last chunk, unused
     const int W = gridDim.x * kHsWaves, gw = blockIdx.x * kHsWaves + wave;
     const int NC = (V + CH - 1) / CH;
     const int nch = gw < NC ? (NC - 1 - gw) / W + 1 : 0;  // this wavefront's chunks (<= kHsMaxChunks)
@@ -567,7 +570,12 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
         for (int q = 0; q < CH; ++q) {
             if constexpr (I8) {
                 const int8_t* p = static_cast<const int8_t*>(wq) + (int64_t)min(row0 + q, V - 1) * C + cl;
-                r[q][0] = *reinterpret_cast<const uint4*>(p);
+                if constexpr (P == 12) {
+                    const uint3 t = *reinterpret_cast<const uint3*>(p);
+                    r[q][0] = uint4{t.x, t.y, t.z, 0u};
+                } else {
+                    r[q][0] = *reinterpret_cast<const uint4*>(p);
+                }
             } else {
                 const uint16_t* p = static_cast<const uint16_t*>(wq) + (int64_t)min(row0 + q, V - 1) * C + cl;
                 r[q][0] = *reinterpret_cast<const uint4*>(p);
@@ -587,38 +595,38 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
     const float k_l = row_coef[nl];
     const float s_l = I8 ? row_scale[nl] : 1.f;
     if (wave == 0) {  // LayerNorm (two-pass mean and biased variance, as torch) into LDS
-        float v[16], g[16], bb[16];
+        float v[P], g[P], bb[P];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < P / 4; ++q) {
             *reinterpret_cast<float4*>(v + 4 * q) = reinterpret_cast<const float4*>(x + cl)[q];
             *reinterpret_cast<float4*>(g + 4 * q) = reinterpret_cast<const float4*>(ln_w + cl)[q];
             *reinterpret_cast<float4*>(bb + 4 * q) = reinterpret_cast<const float4*>(ln_b + cl)[q];
         }
         float sum = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) sum += v[j];
+        for (int j = 0; j < P; ++j) sum += v[j];
         const float mean = wave_sum_dpp(act ? sum : 0.f) / (float)C;
         float d = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) d += (v[j] - mean) * (v[j] - mean);
+        for (int j = 0; j < P; ++j) d += (v[j] - mean) * (v[j] - mean);
         const float rstd = 1.0f / sqrtf(wave_sum_dpp(act ? d : 0.f) / (float)C + eps);
         float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < P; ++j) {
             v[j] = (v[j] - mean) * rstd * g[j] + bb[j];
             ss = fmaf(v[j], v[j], ss);
         }
         ss = wave_sum_dpp(act ? ss : 0.f);
         if (act) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) xs[lane][q] = *reinterpret_cast<const float4*>(v + 4 * q);
+            for (int q = 0; q < P / 4; ++q) xs[lane][q] = *reinterpret_cast<const float4*>(v + 4 * q);
         }
         if (lane == 0) sxn = sqrtf(ss);
     }
     __syncthreads();
-    float xl[16];
+    float xl[P];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(xl + 4 * q) = xs[act ? lane : 0][q];
+    for (int q = 0; q < P / 4; ++q) *reinterpret_cast<float4*>(xl + 4 * q) = xs[act ? lane : 0][q];
     // ||x|| with its own rounding covered (a relative 2^-10 is far above it)
     const float xn = sxn * (1.0f + 0x1p-10f);
     // a_v of this wavefront's rows: the bf16 copy sums each row over the
@@ -638,7 +646,7 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
                 if constexpr (I8) {
                     const uint32_t w32[4] = {r[q][0].x, r[q][0].y, r[q][0].z, r[q][0].w};
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < P / 4; ++j) {
                         s = fmaf(sbyte_f32<0>(w32[j]), xl[4 * j], s);
                         s = fmaf(sbyte_f32<1>(w32[j]), xl[4 * j + 1], s);
                         s = fmaf(sbyte_f32<2>(w32[j]), xl[4 * j + 2], s);
@@ -697,7 +705,7 @@ __global__ __launch_bounds__(64 * kHsWaves) __attribute__((amdgpu_waves_per_eu(4
         const float* p = wf + (int64_t)n * ldw + cl;
         float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < P / 4; ++q) {
             const float4 f = reinterpret_cast<const float4*>(p)[q];
             s = fmaf(f.x, xl[4 * q], s);
             s = fmaf(f.y, xl[4 * q + 1], s);
@@ -1052,7 +1060,10 @@ static int head_argmax_screened(bool i8, const float* x, int64_t n_embd, const f
     float* pv = static_cast<float*>(workspace);
     int* pi = reinterpret_cast<int*>(pv + P);
     hipStream_t st = as_stream(stream);
-    if (i8)
+    if (i8 && n_embd == 768)  // 12 columns a lane: all 64 lanes busy
+        hipLaunchKernelGGL((head_screen_kernel<true, 12>), dim3((unsigned)P), dim3(64 * kHsWaves), 0, st, x,
+                           (int)n_embd, ln_w, ln_b, ln_eps, wq, row_scale, w, ldw, row_coef, (int)vocab, logits, pv, pi);
+    else if (i8)
         hipLaunchKernelGGL(head_screen_kernel<true>, dim3((unsigned)P), dim3(64 * kHsWaves), 0, st, x, (int)n_embd,
                            ln_w, ln_b, ln_eps, wq, row_scale, w, ldw, row_coef, (int)vocab, logits, pv, pi);
     else

@@ -140,7 +140,7 @@ def test_prepare_bounds_hold(dev, fmt):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("V,C", [(50257, 768), (50257, 1024), (5003, 64), (33, 128), (1, 16)])
+@pytest.mark.parametrize("V,C", [(50257, 768), (50257, 1024), (5003, 768), (5003, 64), (33, 128), (1, 16)])
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_screened_argmax_matches_fp32(dev, fmt, V, C, seed):
     x, lw, lb, w = _inputs(V, C, seed, dev)
