@@ -172,7 +172,7 @@ int run_linear(const LinearArgs& a) {
 
 using namespace tiq;
 
-extern "C" int tiq_version(void) { return 125; }
+extern "C" int tiq_version(void) { return 126; }
 
 extern "C" const char* tiq_status_string(int status) {
     switch (status) {
