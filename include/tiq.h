@@ -180,7 +180,10 @@ int tiq_linear_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
 size_t tiq_gemm_w8_workspace(int x_dtype, int64_t M, int64_t K, int64_t N);
 /* tiq_gemm_w8 with a caller workspace (see tiq_gemm_w8_workspace): the
  * prefill product of the reference's Linears (model.py:254,319,352,355 at
- * M = B * T) on the matrix cores; without enough workspace it runs unsplit. */
+ * M = B * T) on the matrix cores; without enough workspace it runs unsplit,
+ * and also with it when the product has 48 or more 128 x 128 tiles and at
+ * most 32 k64 steps (the split would be slower; the workspace is then not
+ * touched). */
 int tiq_gemm_w8_ws(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* q, const float* scale,
                    const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy, void* workspace,
                    size_t workspace_bytes, void* stream);
