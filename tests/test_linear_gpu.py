@@ -120,6 +120,48 @@ def test_gemm_w8_tile_rejects_unknown_configuration(dev):
                                   0, 64, bad, st) == -1
 
 
+# The prefill dispatch at its thresholds, through tiq_gemm_w8_ws with a
+# workspace and tiq_gemm_w8 without: 47 / 48 tiles of 128 x 128 with a short
+# K (split / unsplit on the side-by-side tile), 256 / 272 tiles (one round on
+# the side-by-side tile / the cost model), 32 / 33 k64 steps (side-by-side /
+# four staging sets), and 26 tiles at K = 6400 (split over 8). Every result
+# within the oracle's bound, the bf16 output the rounding of the fp32 one, and
+# the unsplit products of both entry points bit-identical.
+@pytest.mark.parametrize("K,N,M", [(1600, 47 * 128, 128), (1600, 2048, 384), (1600, 2048, 2048), (1600, 2048, 2049),
+                                   (2048, 1024, 256), (2112, 1024, 256), (6400, 1600, 256)])
+def test_gemm_dispatch_thresholds(dev, c_oracle, K, N, M):
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, M + N + K, torch.bfloat16)
+    q, s = c_oracle.quantize_per_channel(w.numpy(), 8)
+    qd, sd, bd, xd = torch.from_numpy(q).to(dev), torch.from_numpy(s.reshape(-1)).to(dev), b.to(dev), x.to(dev)
+    n_ws = int(L.tiq_gemm_w8_workspace(_lib.BF16, M, K, N))
+    ws = torch.empty(max(n_ws, 16), dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for with_ws in (True, False):
+        for dt in (torch.float32, torch.bfloat16):
+            y = torch.full((M, N), float("nan"), device=dev).to(dt)
+            if with_ws:
+                rc = L.tiq_gemm_w8_ws(xd.data_ptr(), _lib.BF16, M, K, K, qd.data_ptr(), sd.data_ptr(), bd.data_ptr(),
+                                      N, y.data_ptr(), _lib.dtype_code(dt), N, ws.data_ptr(), n_ws, st)
+            else:
+                rc = L.tiq_gemm_w8(xd.data_ptr(), _lib.BF16, M, K, K, qd.data_ptr(), sd.data_ptr(), bd.data_ptr(), N,
+                                   y.data_ptr(), _lib.dtype_code(dt), N, st)
+            _lib.check(rc, "gemm")
+            outs[(with_ws, dt)] = y
+    torch.cuda.synchronize()
+    y_ref = OL.linear_ref(x, OL.dequantize(q, s), b)
+    for with_ws in (True, False):
+        y32 = outs[(with_ws, torch.float32)].cpu()
+        ok, err, bound = OL.within_tolerance(y32, y_ref, TOL)
+        assert ok, (with_ws, err, bound)
+        assert torch.equal(outs[(with_ws, torch.bfloat16)].cpu(), y32.to(torch.bfloat16))
+    tiles = ((M + 127) // 128) * ((N + 127) // 128)
+    split = tiles * 2 < 512 and not (tiles >= 48 and K // 64 <= 32)
+    if not split:  # the same unsplit kernel both ways
+        assert torch.equal(outs[(True, torch.float32)].cpu(), outs[(False, torch.float32)].cpu())
+
+
 # The 128x128 tile with four staging sets, and the one with its wavefronts
 # side by side along N (bf16 output), sum the same products in the same order
 # as the two-set 2 x 2 one: bit-identical outputs, fp32 and bf16, with a bias,
