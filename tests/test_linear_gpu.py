@@ -538,6 +538,33 @@ def test_gemm_w4_groupwise_prefill(dev, c_oracle, KN, M):
     _run_w4g(dev, c_oracle, *KN, M, 128, seed=M + KN[0], bias=M != 1024)
 
 
+# Group-wise int4 at the dispatch thresholds (groups of 128, K = 1600): 128-row
+# tiles while 128 x 128 tiles fit one round (M = 1024: 256 tiles at N = 4096,
+# 264 at N = 4224 take 224-row tiles), without the workspace and with it,
+# where 96 tiles or more run unsplit (M = 384: 96 at N = 4096) and 93 split
+# (N = 3968). Within the oracle's bound, the bf16 output the rounding of the
+# fp32 one.
+@pytest.mark.parametrize("N,M", [(4096, 1024), (4224, 1024), (4096, 384), (3968, 384)])
+def test_gemm_w4_groupwise_dispatch_thresholds(dev, c_oracle, N, M):
+    K = 1600
+    _run_w4g(dev, c_oracle, K, N, M, 128, seed=N + M)
+    L = _lib.lib()
+    w, x, b = _inputs(K, N, M, N + M + 1, torch.bfloat16)
+    packed, s16 = c_oracle.quantize_groupwise_int4(w.numpy(), 128)
+    pd, sd = torch.from_numpy(packed).to(dev), torch.from_numpy(s16.view(np.uint16).copy()).to(dev)
+    n_ws = int(L.tiq_gemm_w8_workspace(_lib.BF16, M, K, N))
+    ws = torch.empty(max(n_ws, 16), dtype=torch.uint8, device=dev)
+    y = torch.empty(M, N, device=dev)
+    rc = L.tiq_linear_w4g_ws(x.to(dev).data_ptr(), _lib.BF16, M, K, K, pd.data_ptr(), sd.data_ptr(), 128,
+                             b.to(dev).data_ptr(), N, y.data_ptr(), _lib.F32, N, ws.data_ptr(), n_ws,
+                             torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "tiq_linear_w4g_ws")
+    torch.cuda.synchronize()
+    w_hat = torch.from_numpy(OQ.dequantize_groupwise_int4(packed, s16, K, 128))
+    ok, err, bound = OL.within_tolerance(y.cpu(), OL.linear_ref(x, w_hat, b))
+    assert ok, (err, bound)
+
+
 # Group-wise int4 with bf16 rows and the GEMM workspace: products with few
 # 128 x 128 tiles split over K, whole groups a split, the fp32 slices summed in
 # order (6400x1600 at M = 256: 26 tiles, eight splits of 6-7 groups; group
